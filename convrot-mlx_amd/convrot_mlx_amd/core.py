@@ -1,0 +1,548 @@
+"""ConvRot W4A4 / W4A16 primitives on MI355X (gfx950), PyTorch-ROCm host side.
+
+Mirrors the public API of the reference package `convrot_mlx`
+(/root/reference/src/convrot_mlx/core.py, re-exported by its __init__.py).
+Every compute function runs one of the hand-written HIP kernels behind the C
+ABI in include/convrot_amd.h; argument validation happens here first, with
+the reference's messages, so a bad call raises ValueError before any launch.
+
+Quantization contract (the reference's, core.py:4-21): each group of 64 or
+256 features is rotated by a normalized regular Hadamard matrix, each row is
+quantized symmetrically as absmax/7 into signed [-7, 7], two's-complement
+nibbles are packed low nibble first, the integer GEMM is exact and the
+epilogue is ((dot * xscale) * wscale) + bias in float32.
+
+Weight layouts
+  NK    uint8 [N, K/2], low nibble = even input feature   (core.py:1252-1253)
+  KN    uint8 [K, N/2], low nibble = even output feature  (core.py:1249-1250)
+  CDNA4 uint8 [ceil(K/128), ceil(N/16), 1024] tile blocks read directly by
+        the gfx950 GEMMs (16 output rows x 128 features per 1 KB block).
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+from torch import nn
+
+from . import _native as nat
+
+CONVROT_GROUP_SIZE = 256  # core.py:32
+INT4_MAX = 7  # core.py:34
+# The reference fuses groups 64 and 256 (core.py:33); the gfx950 kernel also
+# covers the other powers of four its eager path accepts, up to 1024.
+SUPPORTED_FUSED_GROUP_SIZES = frozenset({4, 16, 64, 256, 1024})
+# "hip-*" store the CDNA4 tile layout; "mpp-*" keep the reference's KN layout
+# contract for qweight (core.py:1244-1250) and repack it once on device.
+SUPPORTED_BACKENDS = frozenset({"hip-w4a4", "hip-w4a16", "mpp-w4a4", "mpp-w4a16"})
+# One fused HIP preprocessor; the reference's names are accepted as aliases.
+SUPPORTED_PREPROCESSORS = frozenset({"hip-fused", "metal-fused", "mlx-compiled"})
+
+WEIGHT_LAYOUT_NK = "packed-nk-low-nibble-even-feature"
+WEIGHT_LAYOUT_KN = "packed-kn-low-nibble-even-output"
+WEIGHT_LAYOUT_CDNA4 = "packed-cdna4-n16-k128-split-nibble"
+
+
+# ------------------------------------------------------------------ validation
+
+
+def _validate_group_size(group_size: int) -> None:
+    """core.py:50-61."""
+    if group_size < 4:
+        raise ValueError(f"Regular Hadamard size must be a power of 4, got {group_size}")
+    value = group_size
+    while value > 1 and value % 4 == 0:
+        value //= 4
+    if value != 1:
+        raise ValueError(f"Regular Hadamard size must be a power of 4, got {group_size}")
+
+
+def _validate_fused(x: torch.Tensor, group_size: int, what: str) -> None:
+    """core.py:431-442 (and :462-473, :493-502)."""
+    if x.ndim != 2:
+        raise ValueError(f"fused ConvRot {what} expects 2D input, got {tuple(x.shape)}")
+    _validate_group_size(group_size)
+    if group_size not in SUPPORTED_FUSED_GROUP_SIZES:
+        raise ValueError(
+            f"fused ConvRot {what} supports groups {sorted(SUPPORTED_FUSED_GROUP_SIZES)}, got {group_size}"
+        )
+    if x.shape[1] % group_size:
+        raise ValueError(f"features {x.shape[1]} not divisible by ConvRot group size {group_size}")
+
+
+def _log4(group_size: int) -> int:
+    s = 0
+    while group_size > 1:
+        group_size //= 4
+        s += 1
+    return s
+
+
+def cdna4_shape(out_features: int, in_features: int) -> tuple[int, int, int]:
+    """Shape of a CDNA4-layout weight for an (out_features, in_features) linear."""
+    return (-(-in_features // 128), -(-out_features // 16), 1024)
+
+
+# ------------------------------------------------------------------ preparation
+
+
+def _prepare(x: torch.Tensor, group_size: int, mode: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+    nat.require_device(x)
+    x = x.contiguous()
+    rows, features = x.shape
+    kind = mode & ~nat.PREP_NO_ROTATE
+    if kind == nat.PREP_PACKED:
+        out = torch.empty((rows, features // 2), dtype=torch.uint8, device=x.device)
+    elif kind == nat.PREP_INT8:
+        out = torch.empty((rows, features), dtype=torch.int8, device=x.device)
+    else:
+        out = torch.empty_like(x)
+    scales = None if kind == nat.PREP_ROTATE else torch.empty((rows,), dtype=torch.float32, device=x.device)
+    lib = nat.load()
+    nat.check(
+        lib.convrot_prepare(
+            nat.ptr(x), nat.dtype_code(x.dtype), rows, features, group_size, mode,
+            nat.ptr(out), nat.ptr(scales), nat.stream_of(x.device),
+        )
+    )
+    return out, scales
+
+
+def hip_fused_prepare_convrot_activation(x: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE):
+    """Rotation + absmax + A4 quantize + pack in one pass.
+
+    Returns (uint8 [M, K/2] packed codes, float32 [M] scales); bit-identical
+    to prepare_convrot_activation (core.py:161-167) and to the reference's
+    fused kernel metal_fused_prepare_convrot_activation (core.py:425-453).
+    """
+    _validate_fused(x, group_size, "activation preparation")
+    return _prepare(x, group_size, nat.PREP_PACKED)
+
+
+def hip_fused_prepare_convrot_activation_i8(x: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE):
+    """As above, writing each signed A4 code as one int8 (core.py:456-484)."""
+    _validate_fused(x, group_size, "activation preparation")
+    return _prepare(x, group_size, nat.PREP_INT8)
+
+
+def hip_fused_rotate_convrot_activation(x: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE) -> torch.Tensor:
+    """Rotation only, in the input dtype (core.py:487-511)."""
+    _validate_fused(x, group_size, "rotation")
+    return _prepare(x, group_size, nat.PREP_ROTATE)[0]
+
+
+def regular_hadamard(x: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE) -> torch.Tensor:
+    """Right-multiply each feature group by the normalized regular Hadamard (core.py:64-94).
+
+    Any leading shape; per-op rounding in the input dtype, exactly as the
+    reference's eager radix-4 butterfly.
+    """
+    _validate_group_size(group_size)
+    features = x.shape[-1]
+    if features % group_size:
+        raise ValueError(f"features {features} not divisible by ConvRot group size {group_size}")
+    if group_size not in SUPPORTED_FUSED_GROUP_SIZES:
+        raise ValueError(
+            f"fused ConvRot rotation supports groups {sorted(SUPPORTED_FUSED_GROUP_SIZES)}, got {group_size}"
+        )
+    x2d = x.reshape(-1, features)
+    return _prepare(x2d, group_size, nat.PREP_ROTATE)[0].reshape(x.shape)
+
+
+def quantize_signed_int4_rowwise(x: torch.Tensor):
+    """Symmetric absmax/7 row quantization without rotation (core.py:149-158)."""
+    if x.ndim != 2:
+        raise ValueError(f"rowwise int4 quantization expects 2D input, got {tuple(x.shape)}")
+    if x.shape[-1] % 2:
+        raise ValueError(f"last dimension must be even, got {x.shape[-1]}")
+    return _prepare(x, 1, nat.PREP_PACKED | nat.PREP_NO_ROTATE)
+
+
+def prepare_convrot_activation(x: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE):
+    """Rotate and row-quantize an activation (core.py:161-167)."""
+    _validate_group_size(group_size)
+    if x.ndim != 2:
+        raise ValueError(f"rowwise int4 quantization expects 2D input, got {tuple(x.shape)}")
+    if x.shape[-1] % group_size:
+        raise ValueError(f"features {x.shape[-1]} not divisible by ConvRot group size {group_size}")
+    return _prepare(x, group_size, nat.PREP_PACKED)
+
+
+def quantize_convrot_weight(weight: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE):
+    """Rotate a dense (out, in) weight and store it as packed signed W4, NK layout (core.py:514-527)."""
+    if weight.ndim != 2:
+        raise ValueError(f"ConvRot weight must be 2D, got {tuple(weight.shape)}")
+    if weight.shape[-1] % group_size:
+        raise ValueError(f"in_features {weight.shape[-1]} not divisible by ConvRot group size {group_size}")
+    _validate_group_size(group_size)
+    return _prepare(weight, group_size, nat.PREP_PACKED)
+
+
+# ------------------------------------------------------------------ layouts
+
+
+def pack_signed_int4(values: torch.Tensor) -> torch.Tensor:
+    """Pack signed nibbles low-column first (core.py:97-105)."""
+    if values.shape[-1] % 2:
+        raise ValueError(f"last dimension must be even, got {values.shape[-1]}")
+    nat.require_device(values)
+    v = values.to(torch.int8).contiguous()
+    cols = v.shape[-1] // 2
+    rows = v.numel() // max(v.shape[-1], 1)
+    out = torch.empty((*v.shape[:-1], cols), dtype=torch.uint8, device=v.device)
+    nat.check(nat.load().convrot_pack_int4(nat.ptr(v), rows, cols, nat.ptr(out), nat.stream_of(v.device)))
+    return out
+
+
+def unpack_signed_int4(packed: torch.Tensor) -> torch.Tensor:
+    """Unpack two's-complement nibbles to int8 in [-8, 7] (core.py:108-120, kernel :915-922)."""
+    nat.require_device(packed)
+    p = packed.contiguous()
+    if p.dtype != torch.uint8:
+        p = p.to(torch.uint8)
+    cols = p.shape[-1]
+    rows = p.numel() // max(cols, 1)
+    out = torch.empty((*p.shape[:-1], cols * 2), dtype=torch.int8, device=p.device)
+    nat.check(nat.load().convrot_unpack_int4(nat.ptr(p), rows, cols, nat.ptr(out), nat.stream_of(p.device)))
+    return out
+
+
+def _repack(q: torch.Tensor, in_layout: int, out_layout: int, n: int, k: int, out_shape) -> torch.Tensor:
+    nat.require_device(q)
+    q = q.contiguous()
+    out = torch.empty(out_shape, dtype=torch.uint8, device=q.device)
+    nat.check(
+        nat.load().convrot_repack_weight(
+            nat.ptr(q), in_layout, nat.ptr(out), out_layout, n, k, nat.stream_of(q.device)
+        )
+    )
+    return out
+
+
+def repack_nk_weight_for_mpp(qweight: torch.Tensor) -> torch.Tensor:
+    """Bit-exact N x packed-K to K x packed-N conversion (core.py:123-133)."""
+    if qweight.ndim != 2:
+        raise ValueError(f"MPP weight repack expects a 2D tensor, got {tuple(qweight.shape)}")
+    n, k = qweight.shape[0], qweight.shape[1] * 2
+    if n % 2:
+        raise ValueError(f"MPP int4 packing requires even out_features, got {n}")
+    return _repack(qweight, nat.LAYOUT_NK, nat.LAYOUT_KN, n, k, (k, n // 2))
+
+
+def repack_mpp_weight_to_nk(qweight: torch.Tensor) -> torch.Tensor:
+    """Reverse the K x packed-N layout back to N x packed-K (core.py:136-146)."""
+    if qweight.ndim != 2:
+        raise ValueError(f"MPP weight repack expects a 2D tensor, got {tuple(qweight.shape)}")
+    k, n = qweight.shape[0], qweight.shape[1] * 2
+    if k % 2:
+        raise ValueError(f"row-major int4 packing requires even in_features, got {k}")
+    return _repack(qweight, nat.LAYOUT_KN, nat.LAYOUT_NK, n, k, (n, k // 2))
+
+
+def repack_nk_weight_for_cdna4(qweight: torch.Tensor) -> torch.Tensor:
+    """N x packed-K -> CDNA4 tile blocks (lossless; zero padding to 16 x 128)."""
+    if qweight.ndim != 2:
+        raise ValueError(f"CDNA4 weight repack expects a 2D tensor, got {tuple(qweight.shape)}")
+    n, k = qweight.shape[0], qweight.shape[1] * 2
+    return _repack(qweight, nat.LAYOUT_NK, nat.LAYOUT_CDNA4, n, k, cdna4_shape(n, k))
+
+
+def repack_cdna4_weight_to_nk(qweight: torch.Tensor, out_features: int, in_features: int) -> torch.Tensor:
+    """Exact inverse of repack_nk_weight_for_cdna4 (drops the padding)."""
+    _check_cdna4(qweight, out_features, in_features)
+    if in_features % 2:
+        raise ValueError(f"row-major int4 packing requires even in_features, got {in_features}")
+    return _repack(qweight, nat.LAYOUT_CDNA4, nat.LAYOUT_NK, out_features, in_features,
+                   (out_features, in_features // 2))
+
+
+def repack_mpp_weight_for_cdna4(qweight: torch.Tensor) -> torch.Tensor:
+    """K x packed-N (the reference's MPP layout) -> CDNA4 tile blocks."""
+    if qweight.ndim != 2:
+        raise ValueError(f"MPP W4 weight must be 2D, got {tuple(qweight.shape)}")
+    k, n = qweight.shape[0], qweight.shape[1] * 2
+    return _repack(qweight, nat.LAYOUT_KN, nat.LAYOUT_CDNA4, n, k, cdna4_shape(n, k))
+
+
+def repack_cdna4_weight_to_mpp(qweight: torch.Tensor, out_features: int, in_features: int) -> torch.Tensor:
+    """CDNA4 tile blocks -> K x packed-N."""
+    _check_cdna4(qweight, out_features, in_features)
+    if out_features % 2:
+        raise ValueError(f"MPP int4 packing requires even out_features, got {out_features}")
+    return _repack(qweight, nat.LAYOUT_CDNA4, nat.LAYOUT_KN, out_features, in_features,
+                   (in_features, out_features // 2))
+
+
+def _check_cdna4(qweight: torch.Tensor, n: int, k: int) -> None:
+    want = cdna4_shape(n, k)
+    if tuple(qweight.shape) != want or qweight.dtype != torch.uint8:
+        raise ValueError(f"CDNA4 weight for ({n}, {k}) must be uint8 {want}, got {qweight.dtype} {tuple(qweight.shape)}")
+
+
+# ------------------------------------------------------------------ GEMMs
+
+
+def _weight_cdna4(qweight: torch.Tensor, k: int) -> tuple[torch.Tensor, int]:
+    """Accept the reference's K x packed-N layout (2-D) or CDNA4 blocks (3-D).
+
+    Returns (CDNA4 tensor, N).  A KN weight is repacked on device per call;
+    ConvRotLinear caches the repacked tensor instead.
+    """
+    if qweight.ndim == 3:
+        kb, nb, blk = qweight.shape
+        if blk != 1024 or kb != -(-k // 128):
+            raise ValueError(f"CDNA4 W4 weight {tuple(qweight.shape)} does not match activation K={k}")
+        return qweight.contiguous(), nb * 16
+    n = _validate_mpp_weight_layout(qweight, k)
+    return repack_mpp_weight_for_cdna4(qweight), n
+
+
+def _validate_mpp_weight_layout(qweight: torch.Tensor, k: int) -> int:
+    """core.py:1030-1039."""
+    if qweight.ndim != 2:
+        raise ValueError(f"MPP W4 weight must be 2D, got {tuple(qweight.shape)}")
+    if qweight.shape[0] != k:
+        raise ValueError(
+            f"MPP W4 weight must use K x packed-N layout; activation K={k}, weight={tuple(qweight.shape)}"
+        )
+    if k % 32:
+        raise ValueError(f"MPP W4 TensorOp requires K divisible by 32, got {k}")
+    return qweight.shape[1] * 2
+
+
+def _validate_mpp_epilogue(m: int, n: int, xscales, wscales, bias) -> None:
+    """core.py:1042-1058."""
+    if xscales is not None and tuple(xscales.shape) != (m,):
+        raise ValueError(f"MPP activation scales must have shape {(m,)}, got {tuple(xscales.shape)}")
+    if tuple(wscales.shape) != (n,):
+        raise ValueError(f"MPP weight scales must have shape {(n,)}, got {tuple(wscales.shape)}")
+    if bias is not None and tuple(bias.shape) != (n,):
+        raise ValueError(f"MPP bias must have shape {(n,)}, got {tuple(bias.shape)}")
+
+
+def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
+    return None if t is None else t.to(torch.float32).contiguous()
+
+
+def _w4a4(act: torch.Tensor, act_format: int, k: int, qweight, xscales, wscales, bias, output_dtype, n=None):
+    m = act.shape[0]
+    if qweight.ndim == 3 and n is not None:
+        _check_cdna4(qweight, n, k)
+        w = qweight.contiguous()
+    else:
+        w, n_pad = _weight_cdna4(qweight, k)
+        n = n if n is not None else n_pad
+    if k % 32:
+        raise ValueError(f"MPP W4 TensorOp requires K divisible by 32, got {k}")
+    _validate_mpp_epilogue(m, n, xscales, wscales, bias)
+    nat.require_device(act, w, xscales, wscales, bias)
+    out = torch.empty((m, n), dtype=output_dtype, device=act.device)
+    xs, ws, b = _f32(xscales), _f32(wscales), _f32(bias)
+    nat.check(
+        nat.load().convrot_w4a4_gemm(
+            nat.ptr(act), act_format, nat.ptr(xs), nat.ptr(w), nat.ptr(ws), nat.ptr(b), m, n, k,
+            nat.ptr(out), nat.dtype_code(output_dtype), nat.stream_of(act.device),
+        )
+    )
+    return out
+
+
+def hip_w4a4_matmul(qact, qweight, xscales, wscales, bias, *, output_dtype, out_features=None):
+    """Packed-A4 activations [M, K/2] x W4 weight -> output_dtype [M, N] (core.py:1061-1085).
+
+    qweight: CDNA4 blocks (3-D; pass out_features when N is not a multiple of
+    16) or the reference's K x packed-N layout (2-D).
+    """
+    if qact.ndim != 2:
+        raise ValueError(f"MPP W4A4 activation must be 2D, got {tuple(qact.shape)}")
+    k = qact.shape[1] * 2
+    return _w4a4(qact.contiguous(), nat.ACT_PACKED, k, qweight, xscales, wscales, bias, output_dtype, out_features)
+
+
+def hip_w4a4_int8_matmul(activations, qweight, xscales, wscales, bias, *, output_dtype, out_features=None):
+    """int8 A4 activations [M, K] x W4 weight -> output_dtype [M, N] (core.py:1088-1120)."""
+    if activations.ndim != 2 or activations.dtype != torch.int8:
+        raise ValueError(
+            f"MPP W4A4 requires a 2D int8 activation, got {tuple(activations.shape)} {activations.dtype}"
+        )
+    k = activations.shape[1]
+    return _w4a4(activations.contiguous(), nat.ACT_INT8, k, qweight, xscales, wscales, bias, output_dtype,
+                 out_features)
+
+
+def hip_w4a16_matmul(activations, qweight, wscales, bias, *, output_dtype, out_features=None):
+    """Rotated bf16/f16 activations x W4 weight -> output_dtype (core.py:1123-1152)."""
+    if activations.ndim != 2:
+        raise ValueError(f"MPP W4A16 activation must be 2D, got {tuple(activations.shape)}")
+    if activations.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"MPP W4A16 requires float16 or bfloat16 activation, got {activations.dtype}")
+    m, k = activations.shape
+    if qweight.ndim == 3 and out_features is not None:
+        _check_cdna4(qweight, out_features, k)
+        w, n = qweight.contiguous(), out_features
+    else:
+        w, n_pad = _weight_cdna4(qweight, k)
+        n = out_features if out_features is not None else n_pad
+    if k % 32:
+        raise ValueError(f"MPP W4 TensorOp requires K divisible by 32, got {k}")
+    _validate_mpp_epilogue(m, n, None, wscales, bias)
+    act = activations.contiguous()
+    nat.require_device(act, w, wscales, bias)
+    out = torch.empty((m, n), dtype=output_dtype, device=act.device)
+    ws, b = _f32(wscales), _f32(bias)
+    nat.check(
+        nat.load().convrot_w4a16_gemm(
+            nat.ptr(act), nat.dtype_code(act.dtype), nat.ptr(w), nat.ptr(ws), nat.ptr(b), m, n, k,
+            nat.ptr(out), nat.dtype_code(output_dtype), nat.stream_of(act.device),
+        )
+    )
+    return out
+
+
+# Reference names (the reference's Metal/MPP entry points) -> the gfx950 kernels.
+metal_fused_prepare_convrot_activation = hip_fused_prepare_convrot_activation
+metal_fused_prepare_convrot_activation_i8 = hip_fused_prepare_convrot_activation_i8
+metal_fused_rotate_convrot_activation = hip_fused_rotate_convrot_activation
+metal_unpack_signed_int4 = unpack_signed_int4
+mpp_w4a4_matmul = hip_w4a4_matmul
+mpp_w4a4_int8_matmul = hip_w4a4_int8_matmul
+mpp_w4a16_matmul = hip_w4a16_matmul
+# core.py:174-175 are MLX-compiled graphs of the same contract; the fused
+# kernel is this build's compiled form.
+compiled_prepare_convrot_activation = prepare_convrot_activation
+compiled_regular_hadamard = regular_hadamard
+
+
+# ------------------------------------------------------------------ module
+
+
+class ConvRotLinear(nn.Module):
+    """A linear layer stored and executed under the ConvRot W4A4 contract (core.py:1210-1313).
+
+    Same constructor, attributes and defaults as the reference: `qweight`
+    (uint8), `scales` (float32 [N], ones), `bias` (float32 [N], zeros -- one
+    fixed signature for biased and biasless layers, core.py:1255-1258),
+    `group_size`, `backend`, `preprocessor`, `weight_layout`,
+    `source_has_bias`; the output dtype is the input dtype.
+
+    Backends: "hip-w4a4" (default) / "hip-w4a16" hold qweight in the CDNA4
+    tile layout; "mpp-w4a4" / "mpp-w4a16" keep the reference's K x packed-N
+    contract for qweight (so reference checkpoints and repacks load
+    unchanged) and run the same kernels on a cached CDNA4 repack.
+    The default comes from $CONVROT_BACKEND, then $CONVROT_MLX_BACKEND.
+    """
+
+    def __init__(
+        self,
+        in_features: int,
+        out_features: int,
+        *,
+        bias: bool = True,
+        group_size: int = CONVROT_GROUP_SIZE,
+        backend: str | None = None,
+        preprocessor: str | None = None,
+        device=None,
+    ):
+        super().__init__()
+        if in_features % group_size:
+            raise ValueError(f"in_features {in_features} not divisible by ConvRot group size {group_size}")
+        _validate_group_size(group_size)
+        if group_size not in SUPPORTED_FUSED_GROUP_SIZES:
+            raise ValueError(
+                f"fused ConvRot activation preparation supports groups {sorted(SUPPORTED_FUSED_GROUP_SIZES)}, "
+                f"got {group_size}"
+            )
+        self.in_features = in_features
+        self.out_features = out_features
+        self.group_size = group_size
+        self.backend = backend or os.getenv("CONVROT_BACKEND") or os.getenv("CONVROT_MLX_BACKEND") or "hip-w4a4"
+        if self.backend not in SUPPORTED_BACKENDS:
+            raise ValueError(
+                f"Unknown ConvRot backend {self.backend!r}; expected one of {sorted(SUPPORTED_BACKENDS)}"
+            )
+        self.preprocessor = preprocessor or os.getenv("CONVROT_PREPROCESSOR") or os.getenv(
+            "CONVROT_MLX_PREPROCESSOR", "hip-fused"
+        )
+        if self.preprocessor not in SUPPORTED_PREPROCESSORS:
+            raise ValueError(
+                f"Unknown ConvRot preprocessor {self.preprocessor!r}; "
+                f"expected one of {sorted(SUPPORTED_PREPROCESSORS)}"
+            )
+        if self.backend.startswith("mpp-"):
+            if out_features % 2:
+                raise ValueError(f"MPP packed weights require even out_features, got {out_features}")
+            qweight = torch.zeros((in_features, out_features // 2), dtype=torch.uint8, device=device)
+            self.weight_layout = WEIGHT_LAYOUT_KN
+        else:
+            qweight = torch.zeros(cdna4_shape(out_features, in_features), dtype=torch.uint8, device=device)
+            self.weight_layout = WEIGHT_LAYOUT_CDNA4
+        self.register_buffer("qweight", qweight)
+        self.register_buffer("scales", torch.ones((out_features,), dtype=torch.float32, device=device))
+        self.register_buffer("bias", torch.zeros((out_features,), dtype=torch.float32, device=device))
+        self.source_has_bias = bias
+        self._cdna4_cache: tuple | None = None
+
+    @property
+    def a4(self) -> bool:
+        return self.backend.endswith("w4a4")
+
+    def load_nk_weight(self, qweight_nk: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None = None):
+        """Install an NK-packed weight (as quantize_convrot_weight returns) in this layer's layout."""
+        if tuple(qweight_nk.shape) != (self.out_features, self.in_features // 2):
+            raise ValueError(
+                f"NK weight must have shape {(self.out_features, self.in_features // 2)}, got {tuple(qweight_nk.shape)}"
+            )
+        if self.weight_layout == WEIGHT_LAYOUT_KN:
+            self.qweight = repack_nk_weight_for_mpp(qweight_nk)
+        else:
+            self.qweight = repack_nk_weight_for_cdna4(qweight_nk)
+        self.scales = scales.to(torch.float32)
+        if bias is not None:
+            self.bias = bias.to(torch.float32)
+        return self
+
+    def _device_weight(self) -> torch.Tensor:
+        q = self.qweight
+        if self.weight_layout == WEIGHT_LAYOUT_CDNA4:
+            _check_cdna4(q, self.out_features, self.in_features)
+            return q
+        key = (q.data_ptr(), q._version, tuple(q.shape), q.device)
+        if self._cdna4_cache is None or self._cdna4_cache[0] != key:
+            _validate_mpp_weight_layout(q, self.in_features)
+            if q.shape[1] * 2 != self.out_features:
+                raise ValueError(
+                    f"MPP W4 weight must use K x packed-N layout; activation K={self.in_features}, "
+                    f"weight={tuple(q.shape)}"
+                )
+            self._cdna4_cache = (key, repack_mpp_weight_for_cdna4(q))
+        return self._cdna4_cache[1]
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"ConvRotLinear expected K={self.in_features}, got {x.shape[-1]}")
+        lead = x.shape[:-1]
+        x2d = x.reshape(-1, self.in_features)
+        w = self._device_weight()
+        if self.a4:
+            qact, xscales = _prepare(x2d, self.group_size, nat.PREP_INT8)
+            out = _w4a4(qact, nat.ACT_INT8, self.in_features, w, xscales, self.scales, self.bias, x.dtype,
+                        self.out_features)
+        else:
+            rotated = _prepare(x2d, self.group_size, nat.PREP_ROTATE)[0]
+            out = hip_w4a16_matmul(rotated, w, self.scales, self.bias, output_dtype=x.dtype,
+                                   out_features=self.out_features)
+        return out.reshape(*lead, self.out_features)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, group_size={self.group_size}, "
+                f"backend={self.backend!r}, weight_layout={self.weight_layout!r}")
+
+
+def eligible_linear(module: object, group_size: int = CONVROT_GROUP_SIZE) -> bool:
+    """core.py:1316-1321: a Linear with a 2-D weight whose in_features divide into groups."""
+    return (
+        isinstance(module, nn.Linear)
+        and module.weight.ndim == 2
+        and module.weight.shape[1] % group_size == 0
+    )

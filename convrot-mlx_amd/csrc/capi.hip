@@ -1,0 +1,183 @@
+// C ABI of the gfx950 ConvRot library (declared in include/convrot_amd.h).
+//
+// Every entry point validates its arguments before any launch and reports
+// failures as a status code plus a thread-local message; messages for the
+// conditions the reference checks reuse the reference's wording
+// (/root/reference/src/convrot_mlx/core.py:50-61,75-77,431-442,1030-1058).
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "convrot_launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return CONVROT_OK;
+}
+
+int launch_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(CONVROT_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+bool valid_dtype(int dt) { return dt == CONVROT_DTYPE_F32 || dt == CONVROT_DTYPE_F16 || dt == CONVROT_DTYPE_BF16; }
+
+const char* dtype_name(int dt) {
+  switch (dt) {
+    case CONVROT_DTYPE_F32: return "float32";
+    case CONVROT_DTYPE_F16: return "float16";
+    case CONVROT_DTYPE_BF16: return "bfloat16";
+    default: return "unknown";
+  }
+}
+
+// core.py:50-61; returns log4(G) or -1
+int log4_group(int g) {
+  if (g < 4) return -1;
+  int s = 0;
+  while (g > 1 && g % 4 == 0) {
+    g /= 4;
+    ++s;
+  }
+  return g == 1 ? s : -1;
+}
+
+constexpr int64_t kMaxFeatures = 65536;
+
+}  // namespace
+
+extern "C" {
+
+const char* convrot_last_error(void) { return g_err; }
+
+const char* convrot_version(void) { return "convrot-mi355x 0.1.0 (gfx950)"; }
+
+int64_t convrot_cdna4_bytes(int64_t N, int64_t K) {
+  if (N < 0 || K < 0) return -1;
+  return ((K + 127) / 128) * ((N + 15) / 16) * 1024;
+}
+
+int convrot_prepare(const void* x, int dtype, int64_t rows, int64_t features, int group_size, int mode,
+                    void* out, float* scales, void* stream) {
+  const bool no_rotate = (mode & CONVROT_PREP_NO_ROTATE) != 0;
+  const int kind = mode & ~CONVROT_PREP_NO_ROTATE;
+  if (kind != CONVROT_PREP_PACKED && kind != CONVROT_PREP_INT8 && kind != CONVROT_PREP_ROTATE)
+    return fail(CONVROT_ERR_INVALID, "unknown ConvRot preparation mode %d", mode);
+  if (no_rotate && kind == CONVROT_PREP_ROTATE)
+    return fail(CONVROT_ERR_INVALID, "rotate mode cannot skip the rotation");
+  if (!valid_dtype(dtype)) return fail(CONVROT_ERR_INVALID, "unsupported activation dtype code %d", dtype);
+  if (rows < 0 || features <= 0) return fail(CONVROT_ERR_INVALID, "invalid shape (%lld, %lld)", (long long)rows, (long long)features);
+  int s = 0;
+  if (!no_rotate) {
+    s = log4_group(group_size);
+    if (s < 0) return fail(CONVROT_ERR_INVALID, "Regular Hadamard size must be a power of 4, got %d", group_size);
+    if (s > 5)
+      return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot supports groups [4, 16, 64, 256, 1024], got %d", group_size);
+    if (features % group_size)
+      return fail(CONVROT_ERR_INVALID, "features %lld not divisible by ConvRot group size %d", (long long)features,
+                  group_size);
+  }
+  if (features % 16)
+    return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot preparation requires features divisible by 16, got %lld",
+                (long long)features);
+  if (features > kMaxFeatures)
+    return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot preparation supports at most %lld features, got %lld",
+                (long long)kMaxFeatures, (long long)features);
+  if (rows == 0) return ok();
+  if (!x || !out || (kind != CONVROT_PREP_ROTATE && !scales))
+    return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (!aligned(x, 16) || !aligned(out, 16)) return fail(CONVROT_ERR_INVALID, "x and out must be 16-byte aligned");
+  return launch_status(convrot::launch_prep(x, dtype, rows, features, s, kind, out, scales, (hipStream_t)stream),
+                       "convrot_prepare");
+}
+
+int convrot_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
+                      const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K, void* out,
+                      int out_dtype, void* stream) {
+  if (act_format != CONVROT_ACT_PACKED && act_format != CONVROT_ACT_INT8)
+    return fail(CONVROT_ERR_INVALID, "unknown activation format %d", act_format);
+  if (!valid_dtype(out_dtype)) return fail(CONVROT_ERR_INVALID, "unsupported output dtype code %d", out_dtype);
+  if (M < 0 || N < 0 || K <= 0) return fail(CONVROT_ERR_INVALID, "invalid GEMM shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  if (K % 32) return fail(CONVROT_ERR_INVALID, "W4A4 GEMM requires K divisible by 32, got %lld", (long long)K);
+  if (K > kMaxFeatures)
+    return fail(CONVROT_ERR_UNSUPPORTED, "W4A4 GEMM supports K up to %lld, got %lld", (long long)kMaxFeatures, (long long)K);
+  if (M > 0x7fffffff || N > 0x7fffffff) return fail(CONVROT_ERR_UNSUPPORTED, "GEMM dimension too large");
+  if (M == 0 || N == 0) return ok();
+  if (!act || !xscales || !qweight || !wscales || !out) return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (!aligned(act, 16) || !aligned(qweight, 16) || !aligned(out, 16))
+    return fail(CONVROT_ERR_INVALID, "act, qweight and out must be 16-byte aligned");
+  return launch_status(convrot::launch_w4a4_gemm(act, act_format, xscales, qweight, wscales, bias, M, N, K, out,
+                                                 out_dtype, (hipStream_t)stream),
+                       "convrot_w4a4_gemm");
+}
+
+int convrot_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales,
+                       const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype, void* stream) {
+  if (act_dtype != CONVROT_DTYPE_F16 && act_dtype != CONVROT_DTYPE_BF16)
+    return fail(CONVROT_ERR_INVALID, "MPP W4A16 requires float16 or bfloat16 activation, got %s", dtype_name(act_dtype));
+  if (!valid_dtype(out_dtype)) return fail(CONVROT_ERR_INVALID, "unsupported output dtype code %d", out_dtype);
+  if (M < 0 || N < 0 || K <= 0) return fail(CONVROT_ERR_INVALID, "invalid GEMM shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  if (K % 32) return fail(CONVROT_ERR_INVALID, "W4A16 GEMM requires K divisible by 32, got %lld", (long long)K);
+  if (K > kMaxFeatures)
+    return fail(CONVROT_ERR_UNSUPPORTED, "W4A16 GEMM supports K up to %lld, got %lld", (long long)kMaxFeatures, (long long)K);
+  if (M > 0x7fffffff || N > 0x7fffffff) return fail(CONVROT_ERR_UNSUPPORTED, "GEMM dimension too large");
+  if (M == 0 || N == 0) return ok();
+  if (!act || !qweight || !wscales || !out) return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (!aligned(act, 16) || !aligned(qweight, 16) || !aligned(out, 16))
+    return fail(CONVROT_ERR_INVALID, "act, qweight and out must be 16-byte aligned");
+  return launch_status(convrot::launch_w4a16_gemm(act, act_dtype, qweight, wscales, bias, M, N, K, out, out_dtype,
+                                                  (hipStream_t)stream),
+                       "convrot_w4a16_gemm");
+}
+
+int convrot_pack_int4(const int8_t* values, int64_t rows, int64_t packed_cols, uint8_t* out, void* stream) {
+  if (rows < 0 || packed_cols < 0) return fail(CONVROT_ERR_INVALID, "invalid pack shape");
+  if (rows * packed_cols == 0) return ok();
+  if (!values || !out) return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (!aligned(values, 2)) return fail(CONVROT_ERR_INVALID, "values must be 2-byte aligned");
+  return launch_status(convrot::launch_pack_int4(values, rows, packed_cols, out, (hipStream_t)stream),
+                       "convrot_pack_int4");
+}
+
+int convrot_unpack_int4(const uint8_t* packed, int64_t rows, int64_t packed_cols, int8_t* out, void* stream) {
+  if (rows < 0 || packed_cols < 0) return fail(CONVROT_ERR_INVALID, "invalid unpack shape");
+  if (rows * packed_cols == 0) return ok();
+  if (!packed || !out) return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (!aligned(out, 2)) return fail(CONVROT_ERR_INVALID, "out must be 2-byte aligned");
+  return launch_status(convrot::launch_unpack_int4(packed, rows, packed_cols, out, (hipStream_t)stream),
+                       "convrot_unpack_int4");
+}
+
+int convrot_repack_weight(const uint8_t* in, int in_layout, uint8_t* out, int out_layout, int64_t N, int64_t K,
+                          void* stream) {
+  auto valid_layout = [](int l) {
+    return l == CONVROT_LAYOUT_NK || l == CONVROT_LAYOUT_KN || l == CONVROT_LAYOUT_CDNA4;
+  };
+  if (!valid_layout(in_layout) || !valid_layout(out_layout))
+    return fail(CONVROT_ERR_INVALID, "unknown weight layout %d -> %d", in_layout, out_layout);
+  if (N < 0 || K < 0) return fail(CONVROT_ERR_INVALID, "invalid weight shape (%lld, %lld)", (long long)N, (long long)K);
+  if ((in_layout == CONVROT_LAYOUT_KN || out_layout == CONVROT_LAYOUT_KN) && (N % 2))
+    return fail(CONVROT_ERR_INVALID, "MPP int4 packing requires even out_features, got %lld", (long long)N);
+  if ((in_layout == CONVROT_LAYOUT_NK || out_layout == CONVROT_LAYOUT_NK) && (K % 2))
+    return fail(CONVROT_ERR_INVALID, "row-major int4 packing requires even in_features, got %lld", (long long)K);
+  if (N == 0 || K == 0) return ok();
+  if (!in || !out) return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (in == out) return fail(CONVROT_ERR_INVALID, "repack cannot run in place");
+  return launch_status(convrot::launch_repack(in, in_layout, out, out_layout, N, K, (hipStream_t)stream),
+                       "convrot_repack_weight");
+}
+
+}  // extern "C"

@@ -1,0 +1,196 @@
+// W4A4 GEMM for gfx950 on INT8 MFMA with the scale/bias epilogue fused.
+//
+// Replaces the reference's MPP int8 x int4 TensorOp kernel plus its separate
+// int32 -> output epilogue kernel (/root/reference/src/convrot_mlx/core.py:
+// 839-874 and 925-937, launched by mpp_w4a4_int8_matmul :1088-1120 and
+// mpp_w4a4_matmul :1061-1085) with the numerics of the eager oracle
+// reference_w4a4_matmul (core.py:1155-1171): an exact integer dot, then
+// ((float(dot) * xscale[m]) * wscale[n]) + bias[n] in float32, left to right,
+// rounded once to the output dtype.  No int32 M x N intermediate touches HBM.
+//
+// Operands
+//  * activations: int8 codes [M, K] row-major (the INT8 prep output), or
+//    packed A4 [M, K/2] (low nibble = even feature);
+//  * weights: CDNA4 tile layout -- 1 KB blocks of 16 output rows x 128
+//    features, block order [K/128][N/16]; lane L = 16q + r of a wave reads
+//    the 16 bytes at L*16, i.e. row r, features 32q .. 32q+31, laid out so
+//    that (w << 4) & 0xf0f0f0f0 and w & 0xf0f0f0f0 yield the int8 codes x16
+//    of features 8c+0..3 and 8c+4..7 of dword c, in natural order.
+//
+// MFMA mapping: v_mfma_i32_16x16x64_i8 with the weights as the first operand
+// (rows = output features n) and the activations as the second (columns =
+// tokens m), so each lane's accumulator holds 4 consecutive n of one m and
+// the epilogue stores 4 contiguous outputs per lane.  The x16 nibble scaling
+// makes every accumulator an exact multiple of 16 (x256 with packed
+// activations); |acc| <= 256 * 64 * K < 2^31 for K <= 65536 / 2.
+#include "convrot_device.h"
+#include "convrot_launch.h"
+
+namespace convrot {
+namespace {
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool APACK, int ODT>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void w4a4_gemm_kernel(
+    const uint8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
+    const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
+    int K, int nblocks, int kblocks) {
+  constexpr int NT = WAVES_M * WAVES_N * 64;
+  constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  constexpr int AROW = APACK ? 64 : 128;  // activation bytes per row per 128-feature block
+  constexpr int ASTR = AROW + 16;         // padded LDS row stride (conflict-free 16-byte reads)
+  constexpr int ACH = BM * AROW / 16;     // 16-byte chunks per block
+  constexpr int BCH = BN * 4;             // (BN/16 tiles) x 64 chunks
+  constexpr int APT = ACH / NT, BPT = BCH / NT;
+  constexpr int SHIFT = APACK ? 8 : 4;    // acc = 2^SHIFT * dot
+  static_assert(ACH % NT == 0 && BCH % NT == 0, "tile / thread mismatch");
+
+  __shared__ __attribute__((aligned(16))) uint8_t sA[BM * ASTR];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[BN * 64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int64_t arow_bytes = APACK ? (K >> 1) : K;
+
+  uint4 ra[APT], rb[BPT];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+      const int c = tid + i * NT;
+      const int row = c / (AROW / 16), col = c % (AROW / 16);
+      const int gm = m0 + row;
+      const int64_t gk = (int64_t)kb * AROW + col * 16;
+      ra[i] = (gm < M && gk < arow_bytes) ? *(const uint4*)(act + gm * arow_bytes + gk) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      const int c = tid + i * NT;
+      const int nb = n0 / 16 + c / 64;
+      rb[i] = nb < nblocks ? *(const uint4*)(wq + ((int64_t)kb * nblocks + nb) * 1024 + (c % 64) * 16)
+                           : make_uint4(0, 0, 0, 0);
+    }
+  };
+
+  i32x4 acc[FN][FM];
+#pragma unroll
+  for (int a = 0; a < FN; ++a)
+#pragma unroll
+    for (int b = 0; b < FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
+
+  gload(0);
+  for (int kb = 0; kb < kblocks; ++kb) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+      const int c = tid + i * NT;
+      *(uint4*)(sA + (c / (AROW / 16)) * ASTR + (c % (AROW / 16)) * 16) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) *(uint4*)(sB + (tid + i * NT) * 16) = rb[i];
+    __syncthreads();
+    if (kb + 1 < kblocks) gload(kb + 1);
+
+    uint4 bw[FN];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) bw[fn] = *(const uint4*)(sB + (wn * FN + fn) * 1024 + lane * 16);
+
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      i32x4 bop[FN];
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const uint32_t w0 = ks ? bw[fn].z : bw[fn].x;
+        const uint32_t w1 = ks ? bw[fn].w : bw[fn].y;
+        uint32_t l0, h0, l1, h1;
+        nibbles_x16(w0, l0, h0);
+        nibbles_x16(w1, l1, h1);
+        bop[fn] = (i32x4){(int)l0, (int)h0, (int)l1, (int)h1};
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int row = wm * TM + fm * 16 + (lane & 15);
+        i32x4 aop;
+        if constexpr (!APACK) {
+          aop = *(const i32x4*)(sA + row * ASTR + (lane >> 4) * 32 + ks * 16);
+        } else {
+          // standard packing: byte j = k[2j] | k[2j+1] << 4 -> natural-order int8 x16
+          const uint2 p = *(const uint2*)(sA + row * ASTR + (lane >> 4) * 16 + ks * 8);
+          const uint32_t e0 = (p.x << 4) & 0xf0f0f0f0u, o0 = p.x & 0xf0f0f0f0u;
+          const uint32_t e1 = (p.y << 4) & 0xf0f0f0f0u, o1 = p.y & 0xf0f0f0f0u;
+          aop = (i32x4){(int)__builtin_amdgcn_perm(o0, e0, 0x05010400u), (int)__builtin_amdgcn_perm(o0, e0, 0x07030602u),
+                        (int)__builtin_amdgcn_perm(o1, e1, 0x05010400u), (int)__builtin_amdgcn_perm(o1, e1, 0x07030602u)};
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+          acc[fn][fm] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bop[fn], aop, acc[fn][fm], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- fused epilogue (core.py:1168-1171): ((dot * xs) * ws) + bias, then round once
+  const bool vec_ok = (N & 3) == 0;
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+    const int m = m0 + wm * TM + fm * 16 + (lane & 15);
+    if (m >= M) continue;
+    const float xs = xscales[m];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int n = n0 + wn * TN + fn * 16 + 4 * (lane >> 4);
+      if (n >= N) continue;
+      float o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int nn = n + r < N ? n + r : N - 1;
+        float v = (float)(acc[fn][fm][r] >> SHIFT);
+        v = v * xs;
+        v = v * wscales[nn];
+        v = v + (bias ? bias[nn] : 0.0f);
+        o[r] = v;
+      }
+      const int64_t idx = (int64_t)m * N + n;
+      if (vec_ok) {
+        store_out4<ODT>(out, idx, o[0], o[1], o[2], o[3]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) store_out<ODT>(out, idx + r, o[r]);
+      }
+    }
+  }
+}
+
+template <bool APACK, int ODT>
+hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
+                    int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+  constexpr int BM = 128, BN = 128;
+  const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
+  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+  hipLaunchKernelGGL((w4a4_gemm_kernel<BM, BN, 2, 2, APACK, ODT>), grid, dim3(256), 0, stream,
+                     (const uint8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks);
+  return hipGetLastError();
+}
+
+template <bool APACK>
+hipError_t launch_odt(int odt, const void* act, const float* xs, const uint8_t* wq, const float* ws,
+                      const float* bias, int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+  switch (odt) {
+    case kF32: return launch_t<APACK, kF32>(act, xs, wq, ws, bias, M, N, K, out, stream);
+    case kF16: return launch_t<APACK, kF16>(act, xs, wq, ws, bias, M, N, K, out, stream);
+    default: return launch_t<APACK, kBF16>(act, xs, wq, ws, bias, M, N, K, out, stream);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
+                            const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
+                            void* out, int out_dtype, hipStream_t stream) {
+  if (M == 0 || N == 0) return hipSuccess;
+  if (act_format == CONVROT_ACT_PACKED)
+    return launch_odt<true>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, stream);
+  return launch_odt<false>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, stream);
+}
+
+}  // namespace convrot

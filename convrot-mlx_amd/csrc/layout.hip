@@ -1,0 +1,121 @@
+// Packed-int4 layout kernels for gfx950: pack, unpack and lossless weight
+// re-layout between the reference's NK / KN layouts and the CDNA4 tile layout.
+//
+// These are HBM-bound byte permutations: one thread per output byte (or per
+// four output bytes where rows allow), each gathering its two source nibbles.
+// Reference counterparts: pack_signed_int4 / unpack_signed_int4
+// (/root/reference/src/convrot_mlx/core.py:97-120), the Metal unpack kernel
+// (:915-922), repack_nk_weight_for_mpp / repack_mpp_weight_to_nk (:123-146).
+#include "convrot_device.h"
+#include "convrot_launch.h"
+
+namespace convrot {
+namespace {
+
+// pack: out[r, c] = (v[r, 2c] & 0xf) | ((v[r, 2c+1] & 0xf) << 4)   (core.py:101-105)
+__global__ void pack_kernel(const int8_t* __restrict__ v, uint8_t* __restrict__ out, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const uint16_t pair = *(const uint16_t*)(v + 2 * i);
+  out[i] = (uint8_t)((pair & 0x0fu) | ((pair >> 4) & 0xf0u));
+}
+
+// unpack: two's-complement nibbles -> int8 in [-8, 7], low nibble first (core.py:108-120, :919-921)
+__global__ void unpack_kernel(const uint8_t* __restrict__ packed, int8_t* __restrict__ out, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const uint32_t b = packed[i];
+  const int lo = (int)((b & 0x0fu) ^ 0x08u) - 8;
+  const int hi = (int)((b >> 4) ^ 0x08u) - 8;
+  *(uint16_t*)(out + 2 * i) = (uint16_t)((uint8_t)lo | ((uint32_t)(uint8_t)hi << 8));
+}
+
+// Nibble (two's complement, 4 bits) of weight element (n, k) in a layout;
+// zero outside the N x K weight (CDNA4 padding).
+__device__ __forceinline__ uint32_t nibble_at(const uint8_t* __restrict__ in, int layout, int64_t n, int64_t k,
+                                              int64_t N, int64_t K, int64_t nblocks) {
+  if (n >= N || k >= K) return 0u;
+  uint32_t byte;
+  int shift;
+  if (layout == CONVROT_LAYOUT_NK) {
+    byte = in[n * (K >> 1) + (k >> 1)];
+    shift = (int)(k & 1) * 4;
+  } else if (layout == CONVROT_LAYOUT_KN) {
+    byte = in[k * (N >> 1) + (n >> 1)];
+    shift = (int)(n & 1) * 4;
+  } else {
+    const int64_t kb = k >> 7, nb = n >> 4;
+    const int kk = (int)(k & 127), r = (int)(n & 15);
+    const int q = kk >> 5, c = (kk >> 3) & 3, j = kk & 3, h = (kk >> 2) & 1;
+    byte = in[(kb * nblocks + nb) * 1024 + (16 * q + r) * 16 + 4 * c + j];
+    shift = h * 4;
+  }
+  return (byte >> shift) & 0x0fu;
+}
+
+// One output byte per thread: decode which two (n, k) elements it holds in the
+// output layout, gather both nibbles from the input layout.
+__global__ void repack_kernel(const uint8_t* __restrict__ in, int in_layout, uint8_t* __restrict__ out,
+                              int out_layout, int64_t N, int64_t K, int64_t total, int64_t nblocks) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  int64_t n0, k0, n1, k1;
+  if (out_layout == CONVROT_LAYOUT_NK) {
+    const int64_t pk = K >> 1;
+    n0 = n1 = i / pk;
+    k0 = 2 * (i % pk);
+    k1 = k0 + 1;
+  } else if (out_layout == CONVROT_LAYOUT_KN) {
+    const int64_t pn = N >> 1;
+    k0 = k1 = i / pn;
+    n0 = 2 * (i % pn);
+    n1 = n0 + 1;
+  } else {
+    const int64_t blk = i >> 10;
+    const int off = (int)(i & 1023);
+    const int64_t kb = blk / nblocks, nb = blk % nblocks;
+    const int L = off >> 4, c = (off >> 2) & 3, j = off & 3;
+    const int q = L >> 4, r = L & 15;
+    n0 = n1 = nb * 16 + r;
+    k0 = kb * 128 + 32 * q + 8 * c + j;
+    k1 = k0 + 4;
+  }
+  const uint32_t lo = nibble_at(in, in_layout, n0, k0, N, K, nblocks);
+  const uint32_t hi = nibble_at(in, in_layout, n1, k1, N, K, nblocks);
+  out[i] = (uint8_t)(lo | (hi << 4));
+}
+
+inline unsigned grid_for(int64_t total, int block) { return (unsigned)((total + block - 1) / block); }
+
+}  // namespace
+
+hipError_t launch_pack_int4(const int8_t* values, int64_t rows, int64_t packed_cols, uint8_t* out,
+                            hipStream_t stream) {
+  const int64_t total = rows * packed_cols;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(pack_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream, values, out, total);
+  return hipGetLastError();
+}
+
+hipError_t launch_unpack_int4(const uint8_t* packed, int64_t rows, int64_t packed_cols, int8_t* out,
+                              hipStream_t stream) {
+  const int64_t total = rows * packed_cols;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(unpack_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream, packed, out, total);
+  return hipGetLastError();
+}
+
+hipError_t launch_repack(const uint8_t* in, int in_layout, uint8_t* out, int out_layout, int64_t N, int64_t K,
+                         hipStream_t stream) {
+  const int64_t nblocks = (N + 15) / 16, kblocks = (K + 127) / 128;
+  int64_t total;
+  if (out_layout == CONVROT_LAYOUT_NK) total = N * (K / 2);
+  else if (out_layout == CONVROT_LAYOUT_KN) total = K * (N / 2);
+  else total = kblocks * nblocks * 1024;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(repack_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream, in, in_layout, out,
+                     out_layout, N, K, total, nblocks);
+  return hipGetLastError();
+}
+
+}  // namespace convrot

@@ -1,0 +1,372 @@
+// Fused ConvRot activation preparation for gfx950: normalized regular-Hadamard
+// rotation + rowwise absmax + symmetric A4 quantization + packing, one pass.
+//
+// Replaces the reference's two-pass Metal kernels (one threadgroup per row,
+// a barrier per butterfly stage, the row read and rotated twice:
+// /root/reference/src/convrot_mlx/core.py:205-304 packed, :307-327 int8,
+// :330-370 rotate-only) and reproduces the eager contract bit for bit
+// (regular_hadamard core.py:64-94, quantize_signed_int4_rowwise :149-158).
+//
+// Data layout and work split
+//  * One workgroup per row, W waves per row, NI iterations per wave.  In one
+//    iteration a wave owns 1024 consecutive features: lane l holds the 16
+//    consecutive features [16l, 16l+16) in registers (two 16-byte loads).
+//  * A feature index inside a group of G = 4^S is written in base 4 as
+//    (d_{S-1} ... d1 d0).  Stage s of the butterfly runs along digit d_s
+//    (stride 4^s).  Phase 1 keeps (d1, d0) in registers and runs stages 0
+//    and 1 without any data movement; every later stage s keeps (d_s, d0) in
+//    registers and is reached through one LDS exchange (four 16-byte writes,
+//    four 16-byte reads per lane, wave-private region, no workgroup barrier).
+//  * The rotated row stays in registers (NI*16 floats per lane) until the
+//    row absmax is known -- one HBM read of x instead of the reference's two.
+//  * bf16 rounding after every add costs one v_cvt_pk_bf16_f32 (see
+//    round_bf16); the division by scale is a multiply by a correctly rounded
+//    reciprocal, which is exact for bf16 operands (r/scale can never lie
+//    within 2^-16.8 of a bf16 rounding midpoint, so an error below 2^-23
+//    cannot change the rounded ratio).  f16/f32 inputs use a true division.
+#include "convrot_device.h"
+#include "convrot_launch.h"
+
+namespace convrot {
+namespace {
+
+constexpr int kMaxWaves = 16;
+constexpr int kRegionFloats = 1280;  // per wave: 1024 features + 1/4 padding
+
+// One radix-4 butterfly with a dtype rounding after every add (core.py:89-91):
+//   a+b+c-d, a+b-c+d, a-b+c+d, -a+b+c+d, each evaluated left to right.
+// rnd(-a+b) == -rnd(a-b) exactly, so the fourth output reuses a-b.
+template <int DT>
+__device__ __forceinline__ void radix4(float& a, float& b, float& c, float& d) {
+  const float t1 = rnd<DT>(a + b);
+  const float t2 = rnd<DT>(a - b);
+  const float u0 = rnd<DT>(t1 + c);
+  const float u1 = rnd<DT>(t1 - c);
+  const float u2 = rnd<DT>(t2 + c);
+  const float u3 = rnd<DT>(c - t2);
+  a = rnd<DT>(u0 - d);
+  b = rnd<DT>(u1 + d);
+  c = rnd<DT>(u2 + d);
+  d = rnd<DT>(u3 + d);
+}
+
+// Stage along d0 (register slots 4r .. 4r+3).
+template <int DT>
+__device__ __forceinline__ void stage_lo(float (&v)[16]) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) radix4<DT>(v[4 * r], v[4 * r + 1], v[4 * r + 2], v[4 * r + 3]);
+}
+
+// Stage along the digit held in register-slot bits 2-3.
+template <int DT>
+__device__ __forceinline__ void stage_hi(float (&v)[16]) {
+#pragma unroll
+  for (int d0 = 0; d0 < 4; ++d0) radix4<DT>(v[d0], v[4 + d0], v[8 + d0], v[12 + d0]);
+}
+
+// Index inside the group of register run `run` (slots 4*run .. 4*run+3,
+// digit d0 = 0..3) for a lane at position p of its group during phase PH.
+// Phase 1: (d1, d0) in registers, the lane owns features 16p .. 16p+15.
+// Phase PH >= 2: (d_PH, d0) in registers, the remaining digits
+// d1..d_{S-1} (skipping d_PH) come from p, lowest first.
+template <int S, int PH>
+__device__ __forceinline__ int run_index(int p, int run) {
+  if constexpr (PH == 1) {
+    return 16 * p + 4 * run;
+  } else {
+    int i = 0, pp = p, w = 4;
+#pragma unroll
+    for (int t = 1; t < S; ++t, w *= 4) {
+      int digit;
+      if (t == PH) {
+        digit = run;
+      } else {
+        digit = pp & 3;
+        pp >>= 2;
+      }
+      i += digit * w;
+    }
+    return i;
+  }
+}
+
+// Padded LDS offset (floats): 4 floats of padding after every 16 features,
+// which keeps the phase-1 writes and the phase-2 reads bank-conflict free.
+__device__ __forceinline__ int lds_off(int i) { return i + 4 * (i >> 4); }
+
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Move the lane's 16 values from the phase PH-1 layout to the phase PH layout
+// through the wave's LDS region and run stage PH.
+template <int DT, int S, int PH>
+__device__ __forceinline__ void exchange_and_stage(float (&v)[16], float* region, int p) {
+#pragma unroll
+  for (int run = 0; run < 4; ++run) {
+    const int i = run_index<S, PH - 1>(p, run);
+    *(float4*)(region + lds_off(i)) = make_float4(v[4 * run], v[4 * run + 1], v[4 * run + 2], v[4 * run + 3]);
+  }
+  wave_lds_fence();
+#pragma unroll
+  for (int run = 0; run < 4; ++run) {
+    const int i = run_index<S, PH>(p, run);
+    const float4 t = *(const float4*)(region + lds_off(i));
+    v[4 * run] = t.x;
+    v[4 * run + 1] = t.y;
+    v[4 * run + 2] = t.z;
+    v[4 * run + 3] = t.w;
+  }
+  wave_lds_fence();
+  stage_hi<DT>(v);
+}
+
+template <int DT, int S>
+__device__ __forceinline__ void rotate16(float (&v)[16], float* region, int p) {
+  if constexpr (S >= 1) stage_lo<DT>(v);
+  if constexpr (S >= 2) stage_hi<DT>(v);
+  if constexpr (S >= 3) exchange_and_stage<DT, S, 2>(v, region, p);
+  if constexpr (S >= 4) exchange_and_stage<DT, S, 3>(v, region, p);
+  if constexpr (S >= 5) exchange_and_stage<DT, S, 4>(v, region, p);
+}
+
+template <int DT>
+__device__ __forceinline__ void load16(const void* x, int64_t idx, float (&v)[16]) {
+  if constexpr (DT == kF32) {
+    const float4* p = (const float4*)((const float*)x + idx);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 t = p[q];
+      v[4 * q] = t.x;
+      v[4 * q + 1] = t.y;
+      v[4 * q + 2] = t.z;
+      v[4 * q + 3] = t.w;
+    }
+  } else {
+    const uint4* p = (const uint4*)((const uint16_t*)x + idx);
+    const uint4 a = p[0], b = p[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      if constexpr (DT == kBF16) {
+        v[2 * q] = bf16_lo(w[q]);
+        v[2 * q + 1] = bf16_hi(w[q]);
+      } else {
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        const f16x2 h = __builtin_bit_cast(f16x2, w[q]);
+        v[2 * q] = (float)h[0];
+        v[2 * q + 1] = (float)h[1];
+      }
+    }
+  }
+}
+
+// Signed code in [-7, 7] of a ratio: clamp, then round half to even by adding
+// 1.5 * 2^23 (the float add rounds to the nearest integer, ties to even, and
+// leaves the integer in the low mantissa bits in two's complement).
+__device__ __forceinline__ uint32_t code_bits(float ratio) {
+  const float c = __builtin_amdgcn_fmed3f(ratio, -7.0f, 7.0f);
+  return __builtin_bit_cast(uint32_t, c + 12582912.0f);
+}
+
+// Four codes (low bytes of code_bits) gathered into one int8x4 word.
+__device__ __forceinline__ uint32_t gather_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+  const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x04000c0cu);
+  return lo | hi;
+}
+
+// Four codes packed as four nibbles, low nibble = lowest feature (core.py:101-105).
+__device__ __forceinline__ uint32_t gather_nibbles(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+  const uint32_t bytes = gather_bytes(b0, b1, b2, b3) & 0x0f0f0f0fu;
+  const uint32_t pairs = bytes | (bytes >> 4);  // byte0 = n0|n1<<4, byte2 = n2|n3<<4
+  return __builtin_amdgcn_perm(0u, pairs, 0x0c0c0200u);
+}
+
+template <int DT, int S, int NI, int MODE>
+__global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, void* __restrict__ out,
+                                                     float* __restrict__ scales, int K) {
+  extern __shared__ float lds[];
+  __shared__ float wave_max[kMaxWaves];
+
+  constexpr int G = (S == 0) ? 1 : (1 << (2 * S));
+  constexpr int LG = (S >= 3) ? (G / 16) : 1;        // lanes per group
+  constexpr int GS = (S >= 3) ? G : 16;               // features per lane group
+  constexpr bool kImplicitNorm = (DT == kBF16);      // x/sqrt(G) is exact in bf16
+  constexpr float kNorm = (S == 0) ? 1.0f : 1.0f / (float)(1 << S);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int64_t row = blockIdx.x;
+  const int chunks = K >> 4;
+  float* region = lds + wave * kRegionFloats + (lane / LG) * (G + G / 4);
+  const int p = lane % LG;
+
+  float keep[NI][16];
+  float amax = 0.0f;
+
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int block = wave * NI + it;
+    const int chunk = block * 64 + lane;
+    const bool active = chunk < chunks;
+    float (&v)[16] = keep[it];
+    if (active) {
+      load16<DT>(x, row * K + (int64_t)chunk * 16, v);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = 0.0f;
+    }
+    rotate16<DT, S>(v, region, p);
+    if constexpr (!kImplicitNorm && S > 0 && MODE != CONVROT_PREP_ROTATE) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = rnd<DT>(v[j] * kNorm);
+    }
+    if constexpr (MODE != CONVROT_PREP_ROTATE) {
+#pragma unroll
+      for (int j = 0; j < 16; j += 2) amax = fmaxf(amax, fmaxf(fabsf(v[j]), fabsf(v[j + 1])));
+    }
+  }
+
+  // ---- row scale (core.py:154-156)
+  float inv = 0.0f, scale = 0.0f;
+  if constexpr (MODE != CONVROT_PREP_ROTATE) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if (nwaves > 1) {
+      if (lane == 0) wave_max[wave] = amax;
+      __syncthreads();
+      amax = wave_max[0];
+      for (int w = 1; w < nwaves; ++w) amax = fmaxf(amax, wave_max[w]);
+    }
+    if constexpr (kImplicitNorm) amax *= kNorm;
+    float floor_v;
+    if constexpr (DT == kBF16) floor_v = __builtin_bit_cast(float, 0x2edc0000u);  // bf16(1e-10)
+    else if constexpr (DT == kF16) floor_v = 0.0f;                                // f16(1e-10) underflows
+    else floor_v = 1e-10f;
+    scale = rnd<DT>(fmaxf(amax, floor_v) / 7.0f);
+    if constexpr (kImplicitNorm) inv = (1.0f / scale) * kNorm;
+    if (wave == 0 && lane == 0) scales[row] = scale;
+  }
+
+  // ---- quantize + store, phase-final layout
+  constexpr int PHF = (S >= 3) ? (S - 1) : 1;
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int block = wave * NI + it;
+    const int chunk = block * 64 + lane;
+    if (chunk >= chunks) continue;
+    const int64_t gbase = row * K + (int64_t)block * 1024 + (lane / LG) * GS;
+    const float (&v)[16] = keep[it];
+    uint32_t q[16];
+    if constexpr (MODE != CONVROT_PREP_ROTATE) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float ratio;
+        if constexpr (DT == kBF16) ratio = round_bf16(v[j] * inv);
+        else ratio = scale > 0.0f ? rnd<DT>(v[j] / scale) : 0.0f;  // 0/0 on an all-zero f16 row
+        q[j] = code_bits(ratio);
+      }
+    }
+#pragma unroll
+    for (int run = 0; run < 4; ++run) {
+      const int64_t f = gbase + run_index<(S >= 3 ? S : 3), PHF>(p, run);
+      const float* vr = &v[4 * run];
+      if constexpr (MODE == CONVROT_PREP_INT8) {
+        ((uint32_t*)out)[f >> 2] = gather_bytes(q[4 * run], q[4 * run + 1], q[4 * run + 2], q[4 * run + 3]);
+      } else if constexpr (MODE == CONVROT_PREP_PACKED) {
+        ((uint16_t*)out)[f >> 2] =
+            (uint16_t)gather_nibbles(q[4 * run], q[4 * run + 1], q[4 * run + 2], q[4 * run + 3]);
+      } else {
+        // core.py:94 -- y / sqrt(G), rounded to the dtype
+        store_out4<DT>(out, f, rnd<DT>(vr[0] * kNorm), rnd<DT>(vr[1] * kNorm), rnd<DT>(vr[2] * kNorm),
+                       rnd<DT>(vr[3] * kNorm));
+      }
+    }
+  }
+}
+
+template <int DT, int S, int NI, int MODE>
+hipError_t launch_prep_t(const void* x, void* out, float* scales, int64_t rows, int K, int waves,
+                         hipStream_t stream) {
+  const size_t lds_bytes = (S >= 3) ? (size_t)waves * kRegionFloats * sizeof(float) : 0;
+  hipLaunchKernelGGL((prep_kernel<DT, S, NI, MODE>), dim3((unsigned)rows), dim3(64 * waves), lds_bytes,
+                     stream, x, out, scales, K);
+  return hipGetLastError();
+}
+
+template <int DT, int S, int NI>
+hipError_t launch_prep_mode(int mode, const void* x, void* out, float* scales, int64_t rows, int K,
+                            int waves, hipStream_t stream) {
+  switch (mode) {
+    case CONVROT_PREP_PACKED: return launch_prep_t<DT, S, NI, CONVROT_PREP_PACKED>(x, out, scales, rows, K, waves, stream);
+    case CONVROT_PREP_INT8: return launch_prep_t<DT, S, NI, CONVROT_PREP_INT8>(x, out, scales, rows, K, waves, stream);
+    default: return launch_prep_t<DT, S, NI, CONVROT_PREP_ROTATE>(x, out, scales, rows, K, waves, stream);
+  }
+}
+
+template <int DT, int S>
+hipError_t launch_prep_ni(int ni, int mode, const void* x, void* out, float* scales, int64_t rows, int K,
+                          int waves, hipStream_t stream) {
+  switch (ni) {
+    case 1: return launch_prep_mode<DT, S, 1>(mode, x, out, scales, rows, K, waves, stream);
+    case 3: return launch_prep_mode<DT, S, 3>(mode, x, out, scales, rows, K, waves, stream);
+    default: return launch_prep_mode<DT, S, 4>(mode, x, out, scales, rows, K, waves, stream);
+  }
+}
+
+template <int DT>
+hipError_t launch_prep_s(int s, int ni, int mode, const void* x, void* out, float* scales, int64_t rows,
+                         int K, int waves, hipStream_t stream) {
+  switch (s) {
+    case 0: return launch_prep_ni<DT, 0>(ni, mode, x, out, scales, rows, K, waves, stream);
+    case 1: return launch_prep_ni<DT, 1>(ni, mode, x, out, scales, rows, K, waves, stream);
+    case 2: return launch_prep_ni<DT, 2>(ni, mode, x, out, scales, rows, K, waves, stream);
+    case 3: return launch_prep_ni<DT, 3>(ni, mode, x, out, scales, rows, K, waves, stream);
+    case 4: return launch_prep_ni<DT, 4>(ni, mode, x, out, scales, rows, K, waves, stream);
+    default: return launch_prep_ni<DT, 5>(ni, mode, x, out, scales, rows, K, waves, stream);
+  }
+}
+
+}  // namespace
+
+// Pick (iterations per wave, waves per row) so that 1024*NI*W covers K with
+// the fewest idle 1024-feature blocks; NI in {3, 4, 1}, W <= 16.
+bool prep_plan(int64_t K, int* ni_out, int* waves_out) {
+  const int64_t blocks = (K + 1023) / 1024;
+  int best_ni = 0, best_w = 0;
+  int64_t best_idle = -1;
+  const int cand[3] = {3, 4, 1};
+  for (int c = 0; c < 3; ++c) {
+    const int ni = cand[c];
+    const int64_t w = (blocks + ni - 1) / ni;
+    if (w > kMaxWaves) continue;
+    const int64_t idle = w * ni - blocks;
+    if (best_idle < 0 || idle < best_idle) {
+      best_idle = idle;
+      best_ni = ni;
+      best_w = (int)w;
+    }
+  }
+  if (best_idle < 0) return false;
+  *ni_out = best_ni;
+  *waves_out = best_w;
+  return true;
+}
+
+hipError_t launch_prep(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode, void* out,
+                       float* scales, hipStream_t stream) {
+  int ni = 0, waves = 0;
+  if (!prep_plan(K, &ni, &waves)) return hipErrorInvalidValue;
+  if (rows == 0) return hipSuccess;
+  switch (dtype) {
+    case kF32: return launch_prep_s<kF32>(log4g, ni, mode, x, out, scales, rows, (int)K, waves, stream);
+    case kF16: return launch_prep_s<kF16>(log4g, ni, mode, x, out, scales, rows, (int)K, waves, stream);
+    default: return launch_prep_s<kBF16>(log4g, ni, mode, x, out, scales, rows, (int)K, waves, stream);
+  }
+}
+
+}  // namespace convrot

@@ -1,0 +1,134 @@
+/*
+ * convrot_amd.h -- C ABI of the MI355X (gfx950) ConvRot W4A4 / W4A16 library.
+ *
+ * The reference (Lumenbeing/convrot-mlx) has no C FFI: its kernels are Metal
+ * source strings dispatched through `mx.fast.metal_kernel` from Python.  Each
+ * entry point below replaces one of those kernel launch sites; the citation
+ * names the reference function (src/convrot_mlx/core.py:line) whose kernel
+ * and argument meaning it takes over.
+ *
+ * Conventions
+ *  - Every pointer is a device pointer the caller allocated (the library never
+ *    allocates or frees); tensors are dense row-major unless stated.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *    Work is enqueued asynchronously; nothing synchronizes the host.
+ *  - Return value: CONVROT_OK or a nonzero status.  convrot_last_error()
+ *    returns a thread-local message for the last failure on the calling
+ *    thread (the same text the Python layer raises as ValueError).
+ *  - Calls are stateless and reentrant; concurrent calls on different streams
+ *    are safe.
+ */
+#ifndef CONVROT_AMD_H
+#define CONVROT_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+#define CONVROT_DTYPE_F32 0
+#define CONVROT_DTYPE_F16 1
+#define CONVROT_DTYPE_BF16 2
+
+/* status codes */
+#define CONVROT_OK 0
+#define CONVROT_ERR_INVALID 1     /* bad shape / dtype / group size / layout */
+#define CONVROT_ERR_UNSUPPORTED 2 /* valid request outside this build's kernels */
+#define CONVROT_ERR_LAUNCH 3      /* HIP launch or device error */
+
+/* convrot_prepare output modes */
+#define CONVROT_PREP_PACKED 0 /* out: uint8 [rows, features/2] packed A4, + scales */
+#define CONVROT_PREP_INT8 1   /* out: int8  [rows, features] A4 codes,   + scales */
+#define CONVROT_PREP_ROTATE 2 /* out: dtype [rows, features] rotated values (scales unused) */
+/* OR-able flag: skip the rotation (quantize_signed_int4_rowwise semantics) */
+#define CONVROT_PREP_NO_ROTATE 0x10
+
+/* weight layouts accepted by convrot_repack_weight */
+#define CONVROT_LAYOUT_NK 0    /* uint8 [N, K/2], low nibble = even feature   (core.py:1252-1253) */
+#define CONVROT_LAYOUT_KN 1    /* uint8 [K, N/2], low nibble = even output    (core.py:1249-1250) */
+#define CONVROT_LAYOUT_CDNA4 2 /* uint8 [ceil(K/128)][ceil(N/16)][1024] MFMA tile blocks */
+
+/* activation operand formats for convrot_w4a4_gemm */
+#define CONVROT_ACT_PACKED 0 /* uint8 [M, K/2] packed A4 (core.py:1061 mpp_w4a4_matmul) */
+#define CONVROT_ACT_INT8 1   /* int8  [M, K]              (core.py:1088 mpp_w4a4_int8_matmul) */
+
+/*
+ * Fused activation preparation: normalized regular-Hadamard rotation of each
+ * group of `group_size` features, rowwise absmax, symmetric A4 quantization
+ * into [-7, 7] and packing, in one pass over x.
+ * Replaces the kernels of
+ *   metal_fused_prepare_convrot_activation      core.py:425  (mode PACKED)
+ *   metal_fused_prepare_convrot_activation_i8   core.py:456  (mode INT8)
+ *   metal_fused_rotate_convrot_activation       core.py:487  (mode ROTATE)
+ * and, bit-exactly, the eager graphs regular_hadamard (core.py:64),
+ * prepare_convrot_activation (core.py:161), quantize_convrot_weight
+ * (core.py:514) and, with CONVROT_PREP_NO_ROTATE, quantize_signed_int4_rowwise
+ * (core.py:149).
+ * x: dtype [rows, features]; group_size in {4, 16, 64, 256, 1024};
+ * features % group_size == 0, features % 16 == 0, features <= 65536.
+ * scales: float32 [rows] (ignored for ROTATE).
+ */
+int convrot_prepare(const void* x, int dtype, int64_t rows, int64_t features,
+                    int group_size, int mode, void* out, float* scales, void* stream);
+
+/*
+ * W4A4 GEMM with fused epilogue:
+ *   out[m, n] = out_dtype(((float(sum_k a[m,k] * w[n,k]) * xscales[m]) * wscales[n]) + bias[n])
+ * (left to right, no contraction; integer dot exact in int32).
+ * Replaces mpp_w4a4_matmul (core.py:1061, act_format PACKED) and
+ * mpp_w4a4_int8_matmul (core.py:1088, act_format INT8) -- the MPP TensorOp
+ * (core.py:839-874) plus the separate epilogue kernel (core.py:925-937) --
+ * with the numerics of reference_w4a4_matmul (core.py:1155-1171).
+ * qweight: CONVROT_LAYOUT_CDNA4 bytes for an (N, K) weight.  bias may be NULL
+ * (treated as zeros, like the reference's zero bias vector, core.py:1258).
+ * K % 32 == 0, K <= 65536.
+ */
+int convrot_w4a4_gemm(const void* act, int act_format, const float* xscales,
+                      const uint8_t* qweight, const float* wscales, const float* bias,
+                      int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
+                      void* stream);
+
+/*
+ * W4A16 GEMM: out[m, n] = out_dtype((dot_f32(act[m, :], w[n, :]) * wscales[n]) + bias[n]).
+ * Replaces mpp_w4a16_matmul (core.py:1123-1152): the MPP float x int4 TensorOp
+ * (core.py:877-912) plus the elementwise epilogue (core.py:1151-1152).
+ * act: act_dtype in {F16, BF16}, [M, K], already rotated.  qweight: CDNA4 layout.
+ */
+int convrot_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight,
+                       const float* wscales, const float* bias, int64_t M, int64_t N,
+                       int64_t K, void* out, int out_dtype, void* stream);
+
+/* pack_signed_int4 (core.py:97-105): int8 [rows, 2*packed_cols] -> uint8 [rows, packed_cols]. */
+int convrot_pack_int4(const int8_t* values, int64_t rows, int64_t packed_cols, uint8_t* out,
+                      void* stream);
+
+/* metal_unpack_signed_int4 (core.py:1014-1027, kernel :915-922):
+ * uint8 [rows, packed_cols] -> int8 [rows, 2*packed_cols] in [-8, 7]. */
+int convrot_unpack_int4(const uint8_t* packed, int64_t rows, int64_t packed_cols, int8_t* out,
+                        void* stream);
+
+/*
+ * Lossless weight re-layout between CONVROT_LAYOUT_* for an (N, K) weight.
+ * NK -> KN is repack_nk_weight_for_mpp (core.py:123-133, needs even N);
+ * KN -> NK is repack_mpp_weight_to_nk (core.py:136-146, needs even K);
+ * NK/KN <-> CDNA4 is this build's tile layout (zero padding; exact inverse).
+ */
+int convrot_repack_weight(const uint8_t* in, int in_layout, uint8_t* out, int out_layout,
+                          int64_t N, int64_t K, void* stream);
+
+/* Size in bytes of a CDNA4-layout weight for an (N, K) weight. */
+int64_t convrot_cdna4_bytes(int64_t N, int64_t K);
+
+/* Thread-local message of the last failed call on this thread ("" if none). */
+const char* convrot_last_error(void);
+
+/* Library version string. */
+const char* convrot_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CONVROT_AMD_H */

@@ -1,0 +1,325 @@
+"""CPU oracle for the ConvRot W4A4 / W4A16 path -- TEST INFRASTRUCTURE ONLY.
+
+This module is the checker the HIP kernels are compared against.  It is never
+imported by the product package (`convrot_mlx_amd`); only `tests/`,
+`__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` use it.
+
+Two halves:
+
+* arithmetic (rotation, quantization, both matmul epilogues) is the C
+  restatement in `convrot_oracle.c`, loaded here through ctypes;
+* the integer/byte layout functions are restated in numpy below.
+
+Every function cites the reference function it restates
+(`/root/reference/src/convrot_mlx/core.py`).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+DTYPE_CODES = {"float32": DTYPE_F32, "float16": DTYPE_F16, "bfloat16": DTYPE_BF16}
+
+INT4_MAX = 7  # core.py:34
+
+
+def build(force: bool = False) -> Path:
+    """Compile the C restatement with the committed Makefile."""
+    src = HERE / "convrot_oracle.c"
+    if force or not LIB_PATH.exists() or LIB_PATH.stat().st_mtime < src.stat().st_mtime:
+        subprocess.run(["make", "-s", "-B", "-C", str(HERE), "liboracle.so"], check=True)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.cr_oracle_regular_hadamard.argtypes = [vp, i32, i64, i64, i32, vp, vp]
+        L.cr_oracle_quantize_rowwise.argtypes = [vp, i32, i64, i64, vp, vp, vp]
+        L.cr_oracle_prepare.argtypes = [vp, i32, i64, i64, i32, vp, vp, vp]
+        L.cr_oracle_w4a4_matmul.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, vp, vp]
+        L.cr_oracle_w4a16_matmul.argtypes = [vp, i32, vp, vp, vp, i64, i64, i64, i32, vp, vp, vp]
+        L.cr_oracle_f32_to_dtype.argtypes = [vp, i64, i32, vp]
+        L.cr_oracle_dtype_to_f32.argtypes = [vp, i64, i32, vp]
+        L.cr_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.cr_f32_to_bf16.restype = ctypes.c_uint16
+        L.cr_f32_to_f16.argtypes = [ctypes.c_float]
+        L.cr_f32_to_f16.restype = ctypes.c_uint16
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags.c_contiguous
+    return a.ctypes.data
+
+
+# ----------------------------------------------------------------- dtypes
+# Activations travel as uint16 bit patterns (bf16 / f16) or float32.
+
+
+def from_f32(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Round float32 values to `dtype` (RNE).  Returns uint16 bits or float32.
+
+    Mirrors `mx.array(float32).astype(mx.bfloat16)` used to build every test
+    input in /root/reference/tests/test_core.py (e.g. :56-58).
+    """
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if dtype == "float32":
+        return x.copy()
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().cr_oracle_f32_to_dtype(_ptr(x), x.size, DTYPE_CODES[dtype], _ptr(out))
+    return out
+
+
+def to_f32(x: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "float32":
+        return np.ascontiguousarray(x, dtype=np.float32).copy()
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    out = np.empty(x.shape, dtype=np.float32)
+    lib().cr_oracle_dtype_to_f32(_ptr(x), x.size, DTYPE_CODES[dtype], _ptr(out))
+    return out
+
+
+# ----------------------------------------------------------------- arithmetic
+
+
+def _validate_group_size(group_size: int) -> None:
+    """core.py:50-61."""
+    if group_size < 4:
+        raise ValueError(f"Regular Hadamard size must be a power of 4, got {group_size}")
+    value = group_size
+    while value > 1 and value % 4 == 0:
+        value //= 4
+    if value != 1:
+        raise ValueError(f"Regular Hadamard size must be a power of 4, got {group_size}")
+
+
+def regular_hadamard(x: np.ndarray, dtype: str, group_size: int = 256) -> np.ndarray:
+    """core.py:64-94 with per-op dtype rounding (C restatement)."""
+    _validate_group_size(group_size)
+    x = np.ascontiguousarray(x)
+    rows = int(np.prod(x.shape[:-1])) if x.ndim > 1 else 1
+    K = x.shape[-1]
+    if K % group_size:
+        raise ValueError(f"features {K} not divisible by ConvRot group size {group_size}")
+    out = np.empty_like(x)
+    work = np.empty(K, dtype=np.float32)
+    rc = lib().cr_oracle_regular_hadamard(_ptr(x), DTYPE_CODES[dtype], rows, K, group_size, _ptr(out), _ptr(work))
+    assert rc == 0
+    return out
+
+
+def quantize_rowwise_codes(x: np.ndarray, dtype: str) -> tuple[np.ndarray, np.ndarray]:
+    """quantize_signed_int4_rowwise (core.py:149-158) before packing: int8 codes, f32 scales."""
+    x = np.ascontiguousarray(x)
+    if x.ndim != 2:
+        raise ValueError(f"rowwise int4 quantization expects 2D input, got {x.shape}")
+    rows, K = x.shape
+    codes = np.empty((rows, K), dtype=np.int8)
+    scales = np.empty(rows, dtype=np.float32)
+    work = np.empty(K, dtype=np.float32)
+    lib().cr_oracle_quantize_rowwise(_ptr(x), DTYPE_CODES[dtype], rows, K, _ptr(codes), _ptr(scales), _ptr(work))
+    return codes, scales
+
+
+def quantize_signed_int4_rowwise(x: np.ndarray, dtype: str) -> tuple[np.ndarray, np.ndarray]:
+    """core.py:149-158: packed codes and float32 scales."""
+    codes, scales = quantize_rowwise_codes(x, dtype)
+    return pack_signed_int4(codes), scales
+
+
+def prepare_codes(x: np.ndarray, dtype: str, group_size: int = 256) -> tuple[np.ndarray, np.ndarray]:
+    """prepare_convrot_activation (core.py:161-167) before packing."""
+    _validate_group_size(group_size)
+    x = np.ascontiguousarray(x)
+    rows, K = x.shape
+    if K % group_size:
+        raise ValueError(f"features {K} not divisible by ConvRot group size {group_size}")
+    codes = np.empty((rows, K), dtype=np.int8)
+    scales = np.empty(rows, dtype=np.float32)
+    work = np.empty(K, dtype=np.float32)
+    rc = lib().cr_oracle_prepare(_ptr(x), DTYPE_CODES[dtype], rows, K, group_size, _ptr(codes), _ptr(scales), _ptr(work))
+    assert rc == 0
+    return codes, scales
+
+
+def prepare_convrot_activation(x: np.ndarray, dtype: str, group_size: int = 256) -> tuple[np.ndarray, np.ndarray]:
+    """core.py:161-167: packed A4 codes and float32 row scales."""
+    codes, scales = prepare_codes(x, dtype, group_size)
+    return pack_signed_int4(codes), scales
+
+
+def quantize_convrot_weight(weight: np.ndarray, dtype: str, group_size: int = 256) -> tuple[np.ndarray, np.ndarray]:
+    """core.py:514-527: identical math to the activation path, NK packed output."""
+    if weight.ndim != 2:
+        raise ValueError(f"ConvRot weight must be 2D, got {weight.shape}")
+    if weight.shape[-1] % group_size:
+        raise ValueError(
+            f"in_features {weight.shape[-1]} not divisible by ConvRot group size {group_size}"
+        )
+    return prepare_convrot_activation(weight, dtype, group_size)
+
+
+def w4a4_matmul_codes(a_codes, w_codes, xscales, wscales, bias, out_dtype: str, want_dots: bool = False):
+    """reference_w4a4_matmul (core.py:1155-1171) on unpacked codes (w in NK orientation)."""
+    a_codes = np.ascontiguousarray(a_codes, dtype=np.int8)
+    w_codes = np.ascontiguousarray(w_codes, dtype=np.int8)
+    M, K = a_codes.shape
+    N = w_codes.shape[0]
+    assert w_codes.shape[1] == K
+    xs = np.ascontiguousarray(xscales, dtype=np.float32)
+    ws = np.ascontiguousarray(wscales, dtype=np.float32)
+    b = np.ascontiguousarray(bias, dtype=np.float32)
+    out = np.empty((M, N), dtype=np.float32 if out_dtype == "float32" else np.uint16)
+    dots = np.empty((M, N), dtype=np.int32) if want_dots else None
+    lib().cr_oracle_w4a4_matmul(
+        _ptr(a_codes), _ptr(w_codes), _ptr(xs), _ptr(ws), _ptr(b), M, N, K,
+        DTYPE_CODES[out_dtype], _ptr(out), _ptr(dots) if want_dots else None,
+    )
+    return (out, dots) if want_dots else out
+
+
+def reference_w4a4_matmul(qact, qweight_nk, xscales, wscales, bias, out_dtype: str):
+    """core.py:1155-1171 on packed operands."""
+    return w4a4_matmul_codes(unpack_signed_int4(qact), unpack_signed_int4(qweight_nk), xscales, wscales, bias, out_dtype)
+
+
+def w4a16_matmul_codes(act, act_dtype: str, w_codes, wscales, bias, out_dtype: str):
+    """mpp_w4a16_matmul (core.py:1123-1152) numerics on NK codes.
+
+    Returns (out, dots_f32, abs_sum_f32) -- the last is sum_k |a_k * w_k| per
+    output, which sizes the summation-order tolerance of the comparison.
+    """
+    act = np.ascontiguousarray(act)
+    w_codes = np.ascontiguousarray(w_codes, dtype=np.int8)
+    M, K = act.shape
+    N = w_codes.shape[0]
+    ws = np.ascontiguousarray(wscales, dtype=np.float32)
+    b = np.ascontiguousarray(bias, dtype=np.float32)
+    out = np.empty((M, N), dtype=np.float32 if out_dtype == "float32" else np.uint16)
+    dots = np.empty((M, N), dtype=np.float32)
+    mag = np.empty((M, N), dtype=np.float32)
+    lib().cr_oracle_w4a16_matmul(
+        _ptr(act), DTYPE_CODES[act_dtype], _ptr(w_codes), _ptr(ws), _ptr(b), M, N, K,
+        DTYPE_CODES[out_dtype], _ptr(out), _ptr(dots), _ptr(mag),
+    )
+    return out, dots, mag
+
+
+# ----------------------------------------------------------------- layouts
+
+
+def pack_signed_int4(values: np.ndarray) -> np.ndarray:
+    """core.py:97-105: two's-complement nibbles, even column in the low nibble."""
+    values = np.asarray(values)
+    if values.shape[-1] % 2:
+        raise ValueError(f"last dimension must be even, got {values.shape[-1]}")
+    v = values.astype(np.int32)
+    lo = v[..., 0::2] & 0x0F
+    hi = v[..., 1::2] & 0x0F
+    return (lo | (hi << 4)).astype(np.uint8)
+
+
+def unpack_signed_int4(packed: np.ndarray) -> np.ndarray:
+    """core.py:108-120: nibbles to int8 in [-8, 7], low nibble first."""
+    d = np.asarray(packed).astype(np.int32)
+    lo = d & 0x0F
+    hi = (d >> 4) & 0x0F
+    lo = np.where(lo >= 8, lo - 16, lo)
+    hi = np.where(hi >= 8, hi - 16, hi)
+    out = np.stack([lo, hi], axis=-1).reshape(*d.shape[:-1], d.shape[-1] * 2)
+    return out.astype(np.int8)
+
+
+def repack_nk_weight_for_mpp(qweight: np.ndarray) -> np.ndarray:
+    """core.py:123-133: N x packed-K -> K x packed-N (requires even N)."""
+    if qweight.ndim != 2:
+        raise ValueError(f"MPP weight repack expects a 2D tensor, got {qweight.shape}")
+    unpacked = unpack_signed_int4(qweight)
+    if unpacked.shape[0] % 2:
+        raise ValueError(f"MPP int4 packing requires even out_features, got {unpacked.shape[0]}")
+    return pack_signed_int4(unpacked.T)
+
+
+def repack_mpp_weight_to_nk(qweight: np.ndarray) -> np.ndarray:
+    """core.py:136-146: K x packed-N -> N x packed-K (requires even K)."""
+    if qweight.ndim != 2:
+        raise ValueError(f"MPP weight repack expects a 2D tensor, got {qweight.shape}")
+    unpacked = unpack_signed_int4(qweight)
+    if unpacked.shape[0] % 2:
+        raise ValueError(f"row-major int4 packing requires even in_features, got {unpacked.shape[0]}")
+    return pack_signed_int4(unpacked.T)
+
+
+# CDNA4 tile layout (no reference counterpart; defined by this build).
+# Blocks of 16 output rows x 128 features, 1024 bytes each, ordered
+# [K_pad/128][N_pad/16].  Inside a block, byte  16*L + 4*c + j  (lane
+# L = 16*q + r, dword c, byte j) holds row r's codes for features
+#   k = 32*q + 8*c + j      (low nibble)
+#   k = 32*q + 8*c + j + 4  (high nibble)
+# N is zero-padded to a multiple of 16 and K to a multiple of 128.
+CDNA4_BLOCK_N, CDNA4_BLOCK_K = 16, 128
+
+
+def cdna4_shape(n: int, k: int) -> tuple[int, int, int]:
+    npad = -(-n // CDNA4_BLOCK_N) * CDNA4_BLOCK_N
+    kpad = -(-k // CDNA4_BLOCK_K) * CDNA4_BLOCK_K
+    return kpad // CDNA4_BLOCK_K, npad // CDNA4_BLOCK_N, 1024
+
+
+def codes_to_cdna4(w_codes: np.ndarray) -> np.ndarray:
+    """NK int8 codes [N, K] -> CDNA4 packed blocks (see the layout comment)."""
+    N, K = w_codes.shape
+    kb, nb, _ = cdna4_shape(N, K)
+    full = np.zeros((nb * 16, kb * 128), dtype=np.int32)
+    full[:N, :K] = w_codes
+    # full[n, k] with n = 16*nblk + r, k = 128*kblk + 32*q + 8*c + j + 4*h
+    t = full.reshape(nb, 16, kb, 4, 4, 2, 4)  # nblk, r, kblk, q, c, h, j
+    lo = t[..., 0, :] & 0xF
+    hi = t[..., 1, :] & 0xF
+    byte = (lo | (hi << 4)).astype(np.uint8)  # nblk, r, kblk, q, c, j
+    # -> kblk, nblk, q, r, c, j
+    return np.ascontiguousarray(byte.transpose(2, 0, 3, 1, 4, 5)).reshape(kb, nb, 1024)
+
+
+def cdna4_to_codes(blocks: np.ndarray, n: int, k: int) -> np.ndarray:
+    """Exact inverse of codes_to_cdna4, dropping the padding."""
+    kb, nb, _ = blocks.shape
+    b = blocks.reshape(kb, nb, 4, 16, 4, 4).astype(np.int32)  # kblk, nblk, q, r, c, j
+    lo = b & 0xF
+    hi = (b >> 4) & 0xF
+    lo = np.where(lo >= 8, lo - 16, lo)
+    hi = np.where(hi >= 8, hi - 16, hi)
+    t = np.stack([lo, hi], axis=-2)  # kblk, nblk, q, r, c, h, j
+    full = t.transpose(1, 3, 0, 2, 4, 5, 6).reshape(nb * 16, kb * 128)
+    return full[:n, :k].astype(np.int8)
+
+
+def nk_to_cdna4(qweight_nk: np.ndarray) -> np.ndarray:
+    n = qweight_nk.shape[0]
+    return codes_to_cdna4(unpack_signed_int4(qweight_nk)) if n else np.zeros((0, 0, 1024), np.uint8)
+
+
+def cdna4_to_nk(blocks: np.ndarray, n: int, k: int) -> np.ndarray:
+    return pack_signed_int4(cdna4_to_codes(blocks, n, k))
+
+
+def cpu_threads() -> int:
+    return len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)

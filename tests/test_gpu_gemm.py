@@ -1,0 +1,145 @@
+"""GPU parity: INT8-MFMA W4A4 GEMM + fused epilogue vs the CPU oracle.
+
+Integer accumulators must be exact (unit scales, zero bias, float32 output),
+and every output must equal the oracle's bit for bit (the epilogue is the
+same sequence of float32 roundings).  Seeds and shapes follow
+/root/reference/tests/test_core.py:139-175,213-283,329-373.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _util import from_dev, normal_input, outlier_input, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _api():
+    import convrot_mlx_amd as api
+
+    return api
+
+
+def _dev_u8(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _run_both(orc, dev, a_codes, w_codes, xs, ws, bias, out_dtype):
+    """Run the packed-A and int8-A entry points with a CDNA4 weight; return both outputs."""
+    api = _api()
+    N, K = w_codes.shape
+    wq = _dev_u8(orc.codes_to_cdna4(w_codes), dev)
+    qact = _dev_u8(orc.pack_signed_int4(a_codes), dev)
+    a8 = torch.from_numpy(np.ascontiguousarray(a_codes)).to(dev)
+    xs_d, ws_d = torch.from_numpy(xs).to(dev), torch.from_numpy(ws).to(dev)
+    b_d = torch.from_numpy(bias).to(dev)
+    dt = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}[out_dtype]
+    out_p = api.hip_w4a4_matmul(qact, wq, xs_d, ws_d, b_d, output_dtype=dt, out_features=N)
+    out_8 = api.hip_w4a4_int8_matmul(a8, wq, xs_d, ws_d, b_d, output_dtype=dt, out_features=N)
+    torch.cuda.synchronize()
+    return from_dev(out_p), from_dev(out_8)
+
+
+def _assert_exact(got, expected, label):
+    if got.dtype == np.float32:
+        bad = int((got.view(np.uint32) != expected.view(np.uint32)).sum())
+    else:
+        bad = int((got != expected).sum())
+    assert bad == 0, f"{label}: {bad} of {expected.size} outputs differ"
+
+
+@pytest.mark.parametrize("out_dtype", ["float32", "bfloat16", "float16"])
+def test_edges_37x64x46(orc, dev, out_dtype):
+    """test_core.py:213-283: seed 2026082302, M=37, K=64, N=46, codes in [-7, 7]."""
+    rng = np.random.default_rng(2026082302)
+    a = rng.integers(-7, 8, size=(37, 64), dtype=np.int8)
+    w = rng.integers(-7, 8, size=(46, 64), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(37,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(46,)).astype(np.float32)
+    b = rng.normal(size=(46,)).astype(np.float32)
+    expected = orc.w4a4_matmul_codes(a, w, xs, ws, b, out_dtype)
+    for got, name in zip(_run_both(orc, dev, a, w, xs, ws, b, out_dtype), ("packed", "int8")):
+        _assert_exact(got, expected, f"{name} {out_dtype}")
+
+
+def test_exact_integer_dots(orc, dev):
+    """Unit scales and zero bias: the float32 output is the exact integer dot (test_core.py:244-264)."""
+    rng = np.random.default_rng(2026082302)
+    a = rng.integers(-8, 8, size=(37, 320), dtype=np.int8)  # -8 included: unpack covers [-8, 7]
+    w = rng.integers(-8, 8, size=(46, 320), dtype=np.int8)
+    ones_m, ones_n, zeros_n = np.ones(37, np.float32), np.ones(46, np.float32), np.zeros(46, np.float32)
+    dots = a.astype(np.int64) @ w.astype(np.int64).T
+    for got, name in zip(_run_both(orc, dev, a, w, ones_m, ones_n, zeros_n, "float32"), ("packed", "int8")):
+        assert np.array_equal(got, dots.astype(np.float32)), name
+
+
+def test_max_magnitude_accumulators(orc, dev):
+    """|acc| at its largest: every code -8/7 at K=15360 stays exact."""
+    K = 15360
+    a = np.full((16, K), -8, np.int8)
+    a[1::2] = 7
+    w = np.full((32, K), -8, np.int8)
+    w[::3] = 7
+    ones_m, ones_n, zeros_n = np.ones(16, np.float32), np.ones(32, np.float32), np.zeros(32, np.float32)
+    dots = a.astype(np.int64) @ w.astype(np.int64).T
+    for got, name in zip(_run_both(orc, dev, a, w, ones_m, ones_n, zeros_n, "float32"), ("packed", "int8")):
+        assert np.array_equal(got, dots.astype(np.float32)), name
+
+
+@pytest.mark.parametrize(
+    "seed,M,K,N", [(29, 17, 512, 39), (27, 31, 1024, 61), (2026082300, 14, 256, 33), (5, 1, 3072, 64),
+                   (6, 130, 2688, 272), (8, 257, 128, 129)]
+)
+def test_odd_shapes_bf16(orc, dev, seed, M, K, N):
+    """test_core.py:139-175,329-355 shapes and ragged tails on every tile edge, bf16 output."""
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    b = rng.normal(size=(N,)).astype(np.float32)
+    expected = orc.w4a4_matmul_codes(a, w, xs, ws, b, "bfloat16")
+    for got, name in zip(_run_both(orc, dev, a, w, xs, ws, b, "bfloat16"), ("packed", "int8")):
+        _assert_exact(got, expected, f"{name} seed {seed}")
+
+
+def test_kn_layout_entry_matches(orc, dev):
+    """mpp_w4a4_matmul with the reference's K x packed-N weight (repacked on device)."""
+    api = _api()
+    rng = np.random.default_rng(2026082302)
+    a = rng.integers(-7, 8, size=(37, 64), dtype=np.int8)
+    w = rng.integers(-7, 8, size=(46, 64), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(37,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(46,)).astype(np.float32)
+    b = rng.normal(size=(46,)).astype(np.float32)
+    kn = orc.repack_nk_weight_for_mpp(orc.pack_signed_int4(w))
+    out = api.mpp_w4a4_matmul(
+        _dev_u8(orc.pack_signed_int4(a), dev), _dev_u8(kn, dev), torch.from_numpy(xs).to(dev),
+        torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev), output_dtype=torch.float32,
+    )
+    _assert_exact(from_dev(out), orc.w4a4_matmul_codes(a, w, xs, ws, b, "float32"), "kn entry")
+
+
+@pytest.mark.parametrize("K,N", [(3072, 9216), (3072, 3072), (3072, 12288), (12288, 3072), (3072, 21504), (15360, 3072)])
+def test_flux_shapes_complete_path(orc, dev, K, N):
+    """BASELINE configs 2/3 at full size: prep (HIP) -> GEMM (HIP).  Codes and scales must equal
+    the oracle's everywhere; outputs are compared exactly on a seeded sample of 48 rows x all columns."""
+    api = _api()
+    M, G = 1536, 64
+    x = outlier_input(K + N, (M, K), "bfloat16", orc)
+    w = outlier_input(K * 3 + N, (N, K), "bfloat16", orc, std=0.02, frac=0.01, factor=10.0)
+    bias = np.random.default_rng(N).normal(0.0, 0.02, size=N).astype(np.float32)
+    xd, wd = to_dev(x, "bfloat16", dev), to_dev(w, "bfloat16", dev)
+    qw, ws = api.quantize_convrot_weight(wd, G)
+    layer = api.ConvRotLinear(K, N, group_size=G, backend="hip-w4a4", device=dev)
+    layer.load_nk_weight(qw, ws, torch.from_numpy(bias).to(dev))
+    y = from_dev(layer(xd))
+    rows = np.sort(np.random.default_rng(K).choice(M, size=48, replace=False))
+    a_codes, xs = orc.prepare_codes(x[rows], "bfloat16", G)
+    w_codes, wscales = orc.prepare_codes(w, "bfloat16", G)
+    assert np.array_equal(from_dev(ws), wscales)
+    expected = orc.w4a4_matmul_codes(a_codes, w_codes, xs, wscales, bias, "bfloat16")
+    _assert_exact(y[rows], expected, f"{M}x{K}->{N}")
