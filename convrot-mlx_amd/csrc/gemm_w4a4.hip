@@ -23,34 +23,59 @@
 // the epilogue stores 4 contiguous outputs per lane.  The x16 nibble scaling
 // makes every accumulator an exact multiple of 16 (x256 with packed
 // activations); |acc| <= 256 * 64 * K < 2^31 for K <= 65536 / 2.
+//
+// Pipeline: a workgroup of WM x WN waves owns a BM x BN output tile and walks
+// K in 128-feature blocks.  Block kb+1 is fetched from HBM/L2 into registers
+// while block kb is multiplied out of LDS; the registers are then written to
+// the other LDS stage -- two LDS stages, one workgroup barrier per block.
+// Workgroups are renumbered so that the tiles one XCD (one L2) runs are
+// adjacent in groups of GM tile rows.
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "convrot_device.h"
 #include "convrot_launch.h"
 
 namespace convrot {
 namespace {
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool APACK, int ODT>
-__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void w4a4_gemm_kernel(
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin
+constexpr int kGroupM = 4;
+
+template <int BM, int BN, int WM, int WN, bool APACK, int ODT>
+__global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_kernel(
     const uint8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
-    int K, int nblocks, int kblocks) {
-  constexpr int NT = WAVES_M * WAVES_N * 64;
-  constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;
+    int K, int nblocks, int kblocks, int tiles_m, int tiles_n) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 16, FN = TN / 16;
   constexpr int AROW = APACK ? 64 : 128;  // activation bytes per row per 128-feature block
   constexpr int ASTR = AROW + 16;         // padded LDS row stride (conflict-free 16-byte reads)
+  constexpr int A_BYTES = BM * ASTR, B_BYTES = BN * 64, STAGE = A_BYTES + B_BYTES;
   constexpr int ACH = BM * AROW / 16;     // 16-byte chunks per block
   constexpr int BCH = BN * 4;             // (BN/16 tiles) x 64 chunks
   constexpr int APT = ACH / NT, BPT = BCH / NT;
   constexpr int SHIFT = APACK ? 8 : 4;    // acc = 2^SHIFT * dot
   static_assert(ACH % NT == 0 && BCH % NT == 0, "tile / thread mismatch");
 
-  __shared__ __attribute__((aligned(16))) uint8_t sA[BM * ASTR];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[BN * 64];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // ---- XCD-aware tile order
+  const int tiles = tiles_m * tiles_n;
+  int logical = blockIdx.x;
+  const int per_xcd = tiles / kXcds;
+  if (logical < per_xcd * kXcds) logical = (logical % kXcds) * per_xcd + logical / kXcds;
+  const int group = logical / (kGroupM * tiles_n);
+  const int first_m = group * kGroupM;
+  const int group_rows = min(kGroupM, tiles_m - first_m);
+  const int in_group = logical - group * kGroupM * tiles_n;
+  const int m0 = (first_m + in_group % group_rows) * BM;
+  const int n0 = (in_group / group_rows) * BN;
+
   const int64_t arow_bytes = APACK ? (K >> 1) : K;
 
   uint4 ra[APT], rb[BPT];
@@ -71,6 +96,17 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void w4a4_gemm_kernel(
                            : make_uint4(0, 0, 0, 0);
     }
   };
+  auto sstore = [&](int stage) {
+    uint8_t* sA = smem + stage * STAGE;
+    uint8_t* sB = sA + A_BYTES;
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+      const int c = tid + i * NT;
+      *(uint4*)(sA + (c / (AROW / 16)) * ASTR + (c % (AROW / 16)) * 16) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) *(uint4*)(sB + (tid + i * NT) * 16) = rb[i];
+  };
 
   i32x4 acc[FN][FM];
 #pragma unroll
@@ -79,17 +115,14 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void w4a4_gemm_kernel(
     for (int b = 0; b < FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
 
   gload(0);
+  sstore(0);
+  __syncthreads();
+
   for (int kb = 0; kb < kblocks; ++kb) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < APT; ++i) {
-      const int c = tid + i * NT;
-      *(uint4*)(sA + (c / (AROW / 16)) * ASTR + (c % (AROW / 16)) * 16) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < BPT; ++i) *(uint4*)(sB + (tid + i * NT) * 16) = rb[i];
-    __syncthreads();
-    if (kb + 1 < kblocks) gload(kb + 1);
+    const bool more = kb + 1 < kblocks;
+    if (more) gload(kb + 1);
+    const uint8_t* sA = smem + (kb & 1) * STAGE;
+    const uint8_t* sB = sA + A_BYTES;
 
     uint4 bw[FN];
 #pragma unroll
@@ -126,27 +159,35 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void w4a4_gemm_kernel(
           acc[fn][fm] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bop[fn], aop, acc[fn][fm], 0, 0, 0);
       }
     }
+    if (more) sstore((kb + 1) & 1);
+    __syncthreads();
   }
 
   // ---- fused epilogue (core.py:1168-1171): ((dot * xs) * ws) + bias, then round once
   const bool vec_ok = (N & 3) == 0;
 #pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-    const int m = m0 + wm * TM + fm * 16 + (lane & 15);
-    if (m >= M) continue;
-    const float xs = xscales[m];
+  for (int fn = 0; fn < FN; ++fn) {
+    const int n = n0 + wn * TN + fn * 16 + 4 * (lane >> 4);
+    if (n >= N) continue;
+    float wsv[4], bv[4];
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) {
-      const int n = n0 + wn * TN + fn * 16 + 4 * (lane >> 4);
-      if (n >= N) continue;
+    for (int r = 0; r < 4; ++r) {
+      const int nn = n + r < N ? n + r : N - 1;
+      wsv[r] = wscales[nn];
+      bv[r] = bias ? bias[nn] : 0.0f;
+    }
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int m = m0 + wm * TM + fm * 16 + (lane & 15);
+      if (m >= M) continue;
+      const float xs = xscales[m];
       float o[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int nn = n + r < N ? n + r : N - 1;
         float v = (float)(acc[fn][fm][r] >> SHIFT);
         v = v * xs;
-        v = v * wscales[nn];
-        v = v + (bias ? bias[nn] : 0.0f);
+        v = v * wsv[r];
+        v = v + bv[r];
         o[r] = v;
       }
       const int64_t idx = (int64_t)m * N + n;
@@ -161,15 +202,62 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void w4a4_gemm_kernel(
   }
 }
 
+struct Tile {
+  int bm, bn, wm, wn;
+};
+
+template <int BM, int BN, int WM, int WN, bool APACK, int ODT>
+hipError_t launch_tile(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
+                       int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+  const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
+  const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
+  hipLaunchKernelGGL((w4a4_gemm_kernel<BM, BN, WM, WN, APACK, ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
+                     0, stream, (const uint8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks,
+                     tm, tn);
+  return hipGetLastError();
+}
+
+// Tile choice: the largest tile whose grid still fills the 256 CUs about
+// evenly; CONVROT_GEMM_TILE=BMxBN overrides (tuning sweeps).
+Tile choose_tile(int64_t M, int64_t N) {
+  if (const char* env = getenv("CONVROT_GEMM_TILE")) {
+    int bm = 0, bn = 0, wm = 2, wn = 2;
+    if (sscanf(env, "%dx%dw%dx%d", &bm, &bn, &wm, &wn) >= 2) return {bm, bn, wm, wn};
+  }
+  const Tile cands[4] = {{256, 256, 2, 4}, {256, 128, 2, 2}, {128, 256, 2, 2}, {128, 128, 2, 2}};
+  Tile best = {128, 128, 2, 2};
+  double best_score = -1.0;
+  for (const Tile& t : cands) {
+    const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+    const double waves = (double)tiles / 256.0;
+    const double fill = waves / (double)((tiles + 255) / 256);  // fraction of the last round that is busy
+    // larger tiles move fewer bytes per MFMA; require a reasonably full machine
+    const double size_gain = (t.bm * t.bn) / (128.0 * 128.0);
+    const double score = fill * (1.0 + 0.15 * size_gain) * (waves >= 0.75 ? 1.0 : waves);
+    if (score > best_score) {
+      best_score = score;
+      best = t;
+    }
+  }
+  return best;
+}
+
 template <bool APACK, int ODT>
 hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
                     int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
-  constexpr int BM = 128, BN = 128;
-  const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
-  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-  hipLaunchKernelGGL((w4a4_gemm_kernel<BM, BN, 2, 2, APACK, ODT>), grid, dim3(256), 0, stream,
-                     (const uint8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks);
-  return hipGetLastError();
+  const Tile t = choose_tile(M, N);
+#define CONVROT_TILE(BM_, BN_, WM_, WN_)                    \
+  if (t.bm == BM_ && t.bn == BN_ && t.wm == WM_ && t.wn == WN_) \
+    return launch_tile<BM_, BN_, WM_, WN_, APACK, ODT>(act, xs, wq, ws, bias, M, N, K, out, stream);
+  CONVROT_TILE(256, 256, 2, 4)
+  CONVROT_TILE(256, 256, 4, 2)
+  CONVROT_TILE(256, 256, 2, 2)
+  CONVROT_TILE(256, 128, 2, 2)
+  CONVROT_TILE(256, 128, 4, 2)
+  CONVROT_TILE(128, 256, 2, 2)
+  CONVROT_TILE(128, 256, 2, 4)
+#undef CONVROT_TILE
+  return launch_tile<128, 128, 2, 2, APACK, ODT>(act, xs, wq, ws, bias, M, N, K, out, stream);
 }
 
 template <bool APACK>

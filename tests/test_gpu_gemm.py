@@ -106,6 +106,22 @@ def test_odd_shapes_bf16(orc, dev, seed, M, K, N):
         _assert_exact(got, expected, f"{name} seed {seed}")
 
 
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128"])
+@pytest.mark.parametrize("seed,M,K,N", [(41, 300, 384, 530), (42, 17, 2688, 46), (43, 520, 256, 264)])
+def test_every_tile_config(orc, dev, monkeypatch, tile, seed, M, K, N):
+    """Each GEMM tile variant (forced through CONVROT_GEMM_TILE) on ragged M/N/K tails."""
+    monkeypatch.setenv("CONVROT_GEMM_TILE", tile)
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    b = rng.normal(size=(N,)).astype(np.float32)
+    expected = orc.w4a4_matmul_codes(a, w, xs, ws, b, "bfloat16")
+    for got, name in zip(_run_both(orc, dev, a, w, xs, ws, b, "bfloat16"), ("packed", "int8")):
+        _assert_exact(got, expected, f"{name} tile {tile}")
+
+
 def test_kn_layout_entry_matches(orc, dev):
     """mpp_w4a4_matmul with the reference's K x packed-N weight (repacked on device)."""
     api = _api()
