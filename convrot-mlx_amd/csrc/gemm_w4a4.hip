@@ -202,6 +202,226 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_kernel(
   }
 }
 
+
+typedef int i32x4_sgpr __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (stride 0): accesses at or beyond `bytes` read as zero.
+// Built from wave-uniform values so it lives in SGPRs.
+__device__ __forceinline__ i32x4_sgpr buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  return (i32x4_sgpr){__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                      __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)),
+                      __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+
+// One wave-wide 16-byte-per-lane load from a buffer straight into LDS at
+// lds_addr + 16 * lane (buffer_load_dwordx4 ... lds, address in M0).  Issued
+// through asm so the compiler does not add conservative vmcnt waits before
+// LDS reads; the kernel orders these loads with explicit waits + barriers.
+__device__ __forceinline__ void dma16(i32x4_sgpr rsrc, uint32_t voffset, uint32_t lds_addr) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc), "{m0}"(lds_addr) : "memory");
+}
+
+// s_waitcnt on vmcnt only (expcnt and lgkmcnt left at "no wait").
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+  asm volatile("" ::: "memory");
+}
+
+// LDS position of a 16-byte chunk of activation row r (128 bytes per row):
+// XOR with the row's low three bits and bit 3 keeps 16 consecutive rows of one
+// fragment read on distinct banks.
+__device__ __forceinline__ int a_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// INT8-activation GEMM with direct-to-LDS loads: each 1 KB piece of a
+// k-block (8 activation rows x 128 features, or one CDNA4 weight block) is
+// fetched by one wave instruction (buffer_load_dwordx4 ... lds) straight into
+// a STAGES-deep LDS ring, so no registers stage the data and loads run
+// STAGES-1 blocks ahead of the MFMAs.  Every activation load reads whole
+// 128-byte lines; inside LDS the 16-byte chunks of each row are permuted by
+// a_swizzle so that the MFMA fragment reads (16 rows x 16 bytes) are
+// bank-conflict free.  Out-of-range rows/blocks read as zero through the
+// buffer range check (no branches in the loop).
+template <int BM, int BN, int WM, int WN, int STAGES, int ODT>
+__global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
+    const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
+    const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
+    int K, int nblocks, int kblocks, int tiles_m, int tiles_n) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  constexpr int A_FRAGS = (BM / 16) * 2, B_FRAGS = BN / 16;
+  constexpr int LOADS = A_FRAGS + B_FRAGS;
+  constexpr int STAGE_BYTES = LOADS * 1024;
+  static_assert(LOADS % NW == 0, "fragment loads must split evenly over waves");
+  constexpr int LPW = LOADS / NW;
+  constexpr int SHIFT = 4;  // weights unpacked x16
+
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int tiles = tiles_m * tiles_n;
+  int logical = blockIdx.x;
+  const int per_xcd = tiles / kXcds;
+  if (logical < per_xcd * kXcds) logical = (logical % kXcds) * per_xcd + logical / kXcds;
+  const int group = logical / (kGroupM * tiles_n);
+  const int first_m = group * kGroupM;
+  const int group_rows = min(kGroupM, tiles_m - first_m);
+  const int in_group = logical - group * kGroupM * tiles_n;
+  const int m0 = (first_m + in_group % group_rows) * BM;
+  const int n0 = (in_group / group_rows) * BN;
+
+  const int rows_valid = min(BM, M - m0);
+  const i32x4_sgpr ra = buffer_rsrc(act + (int64_t)m0 * K, (uint32_t)rows_valid * (uint32_t)K);
+  const uint8_t* wbase = wq + (int64_t)(n0 / 16) * 1024;
+  const uint32_t wbytes = (uint32_t)(((int64_t)kblocks * nblocks - n0 / 16) * 1024);
+  const i32x4_sgpr rw = buffer_rsrc(wbase, wbytes);
+  const uint32_t smem_addr = (uint32_t)(uintptr_t)smem;
+
+  // This wave's fragment loads: resource, per-lane byte offset at k-block 0
+  // and byte stride per k-block (selected once, branch-free in the loop).
+  i32x4_sgpr rs[LPW];
+  uint32_t voff[LPW], kstride[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int j = wave * LPW + i;
+    const bool is_a = j < A_FRAGS;
+    // A: instruction j covers rows 8j .. 8j+7 of the tile, 128 bytes each (full
+    // cache lines).  LDS slot p of row r holds 16-byte chunk p ^ swz(r).
+    const int r = 8 * j + (lane >> 3);
+    const int chunk = (lane & 7) ^ a_swizzle(r);
+    const uint32_t va = (uint32_t)(r * K + 16 * chunk);
+    const uint32_t vb = (uint32_t)((j - A_FRAGS) * 1024 + lane * 16);
+    voff[i] = is_a ? va : vb;
+    kstride[i] = is_a ? 128u : (uint32_t)nblocks * 1024u;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) rs[i][c] = is_a ? ra[c] : rw[c];
+  }
+  auto issue = [&](int kb, int stage) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const uint32_t dst = smem_addr + (uint32_t)(stage * STAGE_BYTES + (wave * LPW + i) * 1024);
+      dma16(rs[i], voff[i] + (uint32_t)kb * kstride[i], dst);
+    }
+  };
+
+  i32x4 acc[FN][FM];
+#pragma unroll
+  for (int a = 0; a < FN; ++a)
+#pragma unroll
+    for (int b = 0; b < FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
+
+  // Fragments of one k-block held in registers: packed weights (both k-steps)
+  // and int8 activations for k-steps 0 and 1.
+  struct Frags {
+    uint4 b[FN];
+    i32x4 a[2][FM];
+  };
+  auto read_frags = [&](int stage, Frags& f) {
+    const uint8_t* st = smem + stage * STAGE_BYTES;
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) f.b[fn] = *(const uint4*)(st + (A_FRAGS + wn * FN + fn) * 1024 + lane * 16);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        // row m of 16-row group g, features 32q + 16ks .. +16 = chunk 2q + ks
+        const int row = (wm * FM + fm) * 16 + (lane & 15);
+        const int chunk = (2 * (lane >> 4) + ks) ^ a_swizzle(row);
+        f.a[ks][fm] = *(const i32x4*)(st + row * 128 + chunk * 16);
+      }
+  };
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      i32x4 bop[FN];
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const uint32_t w0 = ks ? f.b[fn].z : f.b[fn].x;
+        const uint32_t w1 = ks ? f.b[fn].w : f.b[fn].y;
+        uint32_t l0, h0, l1, h1;
+        nibbles_x16(w0, l0, h0);
+        nibbles_x16(w1, l1, h1);
+        bop[fn] = (i32x4){(int)l0, (int)h0, (int)l1, (int)h1};
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+          acc[fn][fm] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bop[fn], f.a[ks][fm], acc[fn][fm], 0, 0, 0);
+    }
+  };
+
+  // Pipeline: DMA runs STAGES-1 blocks ahead; fragments of block kb+1 are
+  // read from LDS into the spare register set while block kb's MFMAs run.
+  // One barrier per block: it publishes DMA(kb+1) and retires all reads of
+  // stage kb % STAGES, which the next DMA then refills.
+  static_assert(STAGES == 3, "pipeline written for three LDS stages");
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s) issue(s, s);
+  wait_vmcnt<2 * LPW>();
+  __syncthreads();
+  Frags f0, f1;
+  read_frags(0, f0);
+
+  auto step = [&](int kb, Frags& cur, Frags& nxt) {
+    wait_vmcnt<LPW>();
+    __syncthreads();
+    issue(kb + STAGES, kb % STAGES);
+    if (kb + 1 < kblocks) read_frags((kb + 1) % STAGES, nxt);
+    mma(cur);
+  };
+  int kb = 0;
+  for (; kb + 1 < kblocks; kb += 2) {
+    step(kb, f0, f1);
+    step(kb + 1, f1, f0);
+  }
+  if (kb < kblocks) step(kb, f0, f1);
+  wait_vmcnt<0>();
+
+  const bool vec_ok = (N & 3) == 0;
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) {
+    const int n = n0 + wn * TN + fn * 16 + 4 * (lane >> 4);
+    if (n >= N) continue;
+    float wsv[4], bv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int nn = n + r < N ? n + r : N - 1;
+      wsv[r] = wscales[nn];
+      bv[r] = bias ? bias[nn] : 0.0f;
+    }
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int m = m0 + wm * TM + fm * 16 + (lane & 15);
+      if (m >= M) continue;
+      const float xs = xscales[m];
+      float o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = (float)(acc[fn][fm][r] >> SHIFT);
+        v = v * xs;
+        v = v * wsv[r];
+        v = v + bv[r];
+        o[r] = v;
+      }
+      const int64_t idx = (int64_t)m * N + n;
+      if (vec_ok) {
+        store_out4<ODT>(out, idx, o[0], o[1], o[2], o[3]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) store_out<ODT>(out, idx + r, o[r]);
+      }
+    }
+  }
+}
+
 struct Tile {
   int bm, bn, wm, wn;
 };
@@ -224,7 +444,7 @@ Tile choose_tile(int64_t M, int64_t N) {
     int bm = 0, bn = 0, wm = 2, wn = 2;
     if (sscanf(env, "%dx%dw%dx%d", &bm, &bn, &wm, &wn) >= 2) return {bm, bn, wm, wn};
   }
-  const Tile cands[4] = {{256, 256, 2, 4}, {256, 128, 2, 2}, {128, 256, 2, 2}, {128, 128, 2, 2}};
+  const Tile cands[3] = {{128, 256, 2, 4}, {256, 128, 4, 2}, {128, 128, 2, 2}};
   Tile best = {128, 128, 2, 2};
   double best_score = -1.0;
   for (const Tile& t : cands) {
@@ -242,10 +462,32 @@ Tile choose_tile(int64_t M, int64_t N) {
   return best;
 }
 
+template <int BM, int BN, int WM, int WN, int ODT>
+hipError_t launch_dma(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
+                      int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+  const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
+  const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
+  hipLaunchKernelGGL((w4a4_gemm_dma_kernel<BM, BN, WM, WN, 3, ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
+                     0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks,
+                     tm, tn);
+  return hipGetLastError();
+}
+
 template <bool APACK, int ODT>
 hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
                     int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
   const Tile t = choose_tile(M, N);
+  if constexpr (!APACK) {
+    if (!getenv("CONVROT_GEMM_NO_DMA")) {
+#define CONVROT_DMA(BM_, BN_, WM_, WN_)                        \
+  if (t.bm == BM_ && t.bn == BN_ && t.wm == WM_ && t.wn == WN_) \
+    return launch_dma<BM_, BN_, WM_, WN_, ODT>(act, xs, wq, ws, bias, M, N, K, out, stream);
+      CONVROT_DMA(256, 128, 4, 2)
+      CONVROT_DMA(128, 256, 2, 4)
+      CONVROT_DMA(128, 128, 2, 2)
+#undef CONVROT_DMA
+    }
+  }
 #define CONVROT_TILE(BM_, BN_, WM_, WN_)                    \
   if (t.bm == BM_ && t.bn == BN_ && t.wm == WM_ && t.wn == WN_) \
     return launch_tile<BM_, BN_, WM_, WN_, APACK, ODT>(act, xs, wq, ws, bias, M, N, K, out, stream);
