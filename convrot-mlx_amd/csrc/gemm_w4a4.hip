@@ -230,6 +230,102 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("" ::: "memory");
 }
 
+// Fused epilogue of one wave's TM x TN accumulator tile:
+//   out = dtype(((float(acc >> SHIFT) * xs[m]) * ws[n]) + bias[n])   (core.py:1168-1171)
+// 16-bit outputs are staged through the wave's LDS region (row stride TN*2+16
+// bytes) and written back as 16-byte stores covering whole row segments; the
+// MFMA accumulator layout (4 consecutive n of one m per lane) would otherwise
+// produce 32-byte write fragments.  float32 outputs store 4 values per lane.
+template <int ODT, int TM, int TN, int SHIFT>
+__device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], uint8_t* region, int lane,
+                                         int mw, int nw, int M, int N, const float* __restrict__ xscales,
+                                         const float* __restrict__ wscales, const float* __restrict__ bias,
+                                         void* __restrict__ out) {
+  constexpr int FM = TM / 16, FN = TN / 16;
+  float xs[FM];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+    const int m = mw + fm * 16 + (lane & 15);
+    xs[fm] = xscales[m < M ? m : M - 1];
+  }
+  if constexpr (ODT == kF32) {
+    const bool vec_ok = (N & 3) == 0;
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int n = nw + fn * 16 + 4 * (lane >> 4);
+      if (n >= N) continue;
+      float wsv[4], bv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int nn = n + r < N ? n + r : N - 1;
+        wsv[r] = wscales[nn];
+        bv[r] = bias ? bias[nn] : 0.0f;
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int m = mw + fm * 16 + (lane & 15);
+        if (m >= M) continue;
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = (((float)(acc[fn][fm][r] >> SHIFT) * xs[fm]) * wsv[r]) + bv[r];
+        const int64_t idx = (int64_t)m * N + n;
+        if (vec_ok) {
+          store_out4<ODT>(out, idx, o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) store_out<ODT>(out, idx + r, o[r]);
+        }
+      }
+    }
+  } else {
+    constexpr int RS = TN * 2 + 16;  // LDS row stride in bytes
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int nl = fn * 16 + 4 * (lane >> 4);
+      float wsv[4], bv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int nn = min(nw + nl + r, N - 1);
+        wsv[r] = wscales[nn];
+        bv[r] = bias ? bias[nn] : 0.0f;
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = (((float)(acc[fn][fm][r] >> SHIFT) * xs[fm]) * wsv[r]) + bv[r];
+        const uint2 w = ODT == kBF16 ? make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]))
+                                     : make_uint2(pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3]));
+        *(uint2*)(region + (fm * 16 + (lane & 15)) * RS + nl * 2) = w;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    constexpr int CPR = TN / 8;        // 16-byte chunks per row
+    constexpr int RPI = 64 / CPR;      // rows per wave instruction
+    const int cr = lane / CPR, cc = lane % CPR;
+    const bool vec_ok = (N & 7) == 0;
+#pragma unroll
+    for (int r0 = 0; r0 < TM; r0 += RPI) {
+      const int rl = r0 + cr;
+      const int m = mw + rl, n = nw + cc * 8;
+      if (m >= M || n >= N) continue;
+      const uint4 v = *(const uint4*)(region + rl * RS + cc * 16);
+      uint16_t* dst = (uint16_t*)out + (int64_t)m * N + n;
+      if (vec_ok && n + 8 <= N) {
+        *(uint4*)dst = v;
+      } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (n + j < N) dst[j] = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+      }
+    }
+  }
+}
+
 // LDS position of a 16-byte chunk of activation row r (128 bytes per row):
 // XOR with the row's low three bits and bit 3 keeps 16 consecutive rows of one
 // fragment read on distinct banks.
@@ -244,7 +340,7 @@ __device__ __forceinline__ int a_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1
 // a_swizzle so that the MFMA fragment reads (16 rows x 16 bytes) are
 // bank-conflict free.  Out-of-range rows/blocks read as zero through the
 // buffer range check (no branches in the loop).
-template <int BM, int BN, int WM, int WN, int STAGES, int ODT>
+template <int BM, int BN, int WM, int WN, int STAGES, bool PINGPONG, int ODT>
 __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
     const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
@@ -362,64 +458,50 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
   // One barrier per block: it publishes DMA(kb+1) and retires all reads of
   // stage kb % STAGES, which the next DMA then refills.
   static_assert(STAGES == 3, "pipeline written for three LDS stages");
+  Frags f0;
+  [[maybe_unused]] Frags f1;
+  if constexpr (PINGPONG) {
+    // DMA three blocks ahead; block kb+1's fragments are read into the spare
+    // register set while block kb's MFMAs run.  The barrier of step kb
+    // publishes DMA(kb+1) and retires every wave's reads of stage kb % 3
+    // (issued in step kb-1), which DMA(kb+3) then refills.
 #pragma unroll
-  for (int s = 0; s < STAGES; ++s) issue(s, s);
-  wait_vmcnt<2 * LPW>();
-  __syncthreads();
-  Frags f0, f1;
-  read_frags(0, f0);
-
-  auto step = [&](int kb, Frags& cur, Frags& nxt) {
-    wait_vmcnt<LPW>();
+    for (int s = 0; s < STAGES; ++s) issue(s, s);
+    wait_vmcnt<2 * LPW>();
     __syncthreads();
-    issue(kb + STAGES, kb % STAGES);
-    if (kb + 1 < kblocks) read_frags((kb + 1) % STAGES, nxt);
-    mma(cur);
-  };
-  int kb = 0;
-  for (; kb + 1 < kblocks; kb += 2) {
-    step(kb, f0, f1);
-    step(kb + 1, f1, f0);
+    read_frags(0, f0);
+    auto step = [&](int kb, Frags& cur, Frags& nxt) {
+      wait_vmcnt<LPW>();
+      __syncthreads();
+      issue(kb + STAGES, kb % STAGES);
+      if (kb + 1 < kblocks) read_frags((kb + 1) % STAGES, nxt);
+      mma(cur);
+    };
+    int kb = 0;
+    for (; kb + 1 < kblocks; kb += 2) {
+      step(kb, f0, f1);
+      step(kb + 1, f1, f0);
+    }
+    if (kb < kblocks) step(kb, f0, f1);
+  } else {
+    // One register set: DMA two blocks ahead.  The barrier of iteration kb
+    // publishes DMA(kb) and retires every wave's reads of stage (kb-1) % 3,
+    // which DMA(kb+2) then refills.
+    issue(0, 0);
+    issue(1, 1);
+    for (int kb = 0; kb < kblocks; ++kb) {
+      wait_vmcnt<LPW>();
+      __syncthreads();
+      issue(kb + 2, (kb + 2) % STAGES);
+      read_frags(kb % STAGES, f0);
+      mma(f0);
+    }
   }
-  if (kb < kblocks) step(kb, f0, f1);
   wait_vmcnt<0>();
-
-  const bool vec_ok = (N & 3) == 0;
-#pragma unroll
-  for (int fn = 0; fn < FN; ++fn) {
-    const int n = n0 + wn * TN + fn * 16 + 4 * (lane >> 4);
-    if (n >= N) continue;
-    float wsv[4], bv[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int nn = n + r < N ? n + r : N - 1;
-      wsv[r] = wscales[nn];
-      bv[r] = bias ? bias[nn] : 0.0f;
-    }
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-      const int m = m0 + wm * TM + fm * 16 + (lane & 15);
-      if (m >= M) continue;
-      const float xs = xscales[m];
-      float o[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float v = (float)(acc[fn][fm][r] >> SHIFT);
-        v = v * xs;
-        v = v * wsv[r];
-        v = v + bv[r];
-        o[r] = v;
-      }
-      const int64_t idx = (int64_t)m * N + n;
-      if (vec_ok) {
-        store_out4<ODT>(out, idx, o[0], o[1], o[2], o[3]);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (n + r < N) store_out<ODT>(out, idx + r, o[r]);
-      }
-    }
-  }
+  __syncthreads();  // all waves done with the LDS ring before it is reused for output staging
+  static_assert(NW * TM * (TN * 2 + 16) <= STAGES * STAGE_BYTES, "epilogue staging exceeds LDS");
+  epilogue<ODT, TM, TN, SHIFT>(acc, smem + wave * TM * (TN * 2 + 16), lane, m0 + wm * TM, n0 + wn * TN, M, N,
+                               xscales, wscales, bias, out);
 }
 
 struct Tile {
@@ -437,26 +519,33 @@ hipError_t launch_tile(const void* act, const float* xs, const uint8_t* wq, cons
   return hipGetLastError();
 }
 
-// Tile choice: the largest tile whose grid still fills the 256 CUs about
-// evenly; CONVROT_GEMM_TILE=BMxBN overrides (tuning sweeps).
+// Tile choice: maximise (busy fraction of the last round of workgroups) x
+// (measured per-tile efficiency of the tile).  256x256 moves half the L2 bytes
+// per MFMA of 128x128 but runs one workgroup per CU; 128x128 fits two per CU.
+// CONVROT_GEMM_TILE=BMxBN[wWMxWN] overrides (tuning sweeps).
 Tile choose_tile(int64_t M, int64_t N) {
   if (const char* env = getenv("CONVROT_GEMM_TILE")) {
     int bm = 0, bn = 0, wm = 2, wn = 2;
     if (sscanf(env, "%dx%dw%dx%d", &bm, &bn, &wm, &wn) >= 2) return {bm, bn, wm, wn};
   }
-  const Tile cands[3] = {{128, 256, 2, 4}, {256, 128, 4, 2}, {128, 128, 2, 2}};
+  struct Cand {
+    Tile t;
+    int per_cu;
+    double eff;
+  };
+  const Cand cands[4] = {{{256, 256, 2, 4}, 1, 1.0}, {{128, 256, 2, 4}, 1, 0.85}, {{256, 128, 4, 2}, 1, 0.8},
+                         {{128, 128, 2, 2}, 2, 0.8}};
   Tile best = {128, 128, 2, 2};
   double best_score = -1.0;
-  for (const Tile& t : cands) {
-    const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
-    const double waves = (double)tiles / 256.0;
-    const double fill = waves / (double)((tiles + 255) / 256);  // fraction of the last round that is busy
-    // larger tiles move fewer bytes per MFMA; require a reasonably full machine
-    const double size_gain = (t.bm * t.bn) / (128.0 * 128.0);
-    const double score = fill * (1.0 + 0.15 * size_gain) * (waves >= 0.75 ? 1.0 : waves);
-    if (score > best_score) {
+  for (const Cand& c : cands) {
+    const int64_t tiles = ((M + c.t.bm - 1) / c.t.bm) * ((N + c.t.bn - 1) / c.t.bn);
+    const int64_t slots = 256 * (int64_t)c.per_cu;
+    const double rounds = (double)tiles / (double)slots;
+    const double fill = rounds / (double)((tiles + slots - 1) / slots);
+    const double score = fill * c.eff;
+    if (score > best_score + 1e-9) {
       best_score = score;
-      best = t;
+      best = c.t;
     }
   }
   return best;
@@ -467,7 +556,7 @@ hipError_t launch_dma(const void* act, const float* xs, const uint8_t* wq, const
                       int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
   const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
-  hipLaunchKernelGGL((w4a4_gemm_dma_kernel<BM, BN, WM, WN, 3, ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
+  hipLaunchKernelGGL((w4a4_gemm_dma_kernel<BM, BN, WM, WN, 3, (BM * BN < 65536), ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
                      0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks,
                      tm, tn);
   return hipGetLastError();
@@ -482,6 +571,7 @@ hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const f
 #define CONVROT_DMA(BM_, BN_, WM_, WN_)                        \
   if (t.bm == BM_ && t.bn == BN_ && t.wm == WM_ && t.wn == WN_) \
     return launch_dma<BM_, BN_, WM_, WN_, ODT>(act, xs, wq, ws, bias, M, N, K, out, stream);
+      CONVROT_DMA(256, 256, 2, 4)
       CONVROT_DMA(256, 128, 4, 2)
       CONVROT_DMA(128, 256, 2, 4)
       CONVROT_DMA(128, 128, 2, 2)
