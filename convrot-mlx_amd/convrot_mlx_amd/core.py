@@ -283,19 +283,26 @@ def _check_cdna4(qweight: torch.Tensor, n: int, k: int) -> None:
 # ------------------------------------------------------------------ GEMMs
 
 
-def _weight_cdna4(qweight: torch.Tensor, k: int) -> tuple[torch.Tensor, int]:
-    """Accept the reference's K x packed-N layout (2-D) or CDNA4 blocks (3-D).
-
-    Returns (CDNA4 tensor, N).  A KN weight is repacked on device per call;
-    ConvRotLinear caches the repacked tensor instead.
-    """
+def _weight_n(qweight: torch.Tensor, k: int) -> int:
+    """Output features of a W4 weight given as CDNA4 blocks (3-D) or the reference's
+    K x packed-N layout (2-D, validated as in core.py:1030-1039)."""
     if qweight.ndim == 3:
         kb, nb, blk = qweight.shape
         if blk != 1024 or kb != -(-k // 128):
             raise ValueError(f"CDNA4 W4 weight {tuple(qweight.shape)} does not match activation K={k}")
-        return qweight.contiguous(), nb * 16
-    n = _validate_mpp_weight_layout(qweight, k)
-    return repack_mpp_weight_for_cdna4(qweight), n
+        return nb * 16
+    return _validate_mpp_weight_layout(qweight, k)
+
+
+def _as_cdna4(qweight: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """CDNA4 blocks for the GEMMs; a K x packed-N weight is repacked on device per call
+    (ConvRotLinear caches the repacked tensor instead)."""
+    if qweight.ndim == 3:
+        _check_cdna4(qweight, n, k)
+        return qweight.contiguous()
+    if qweight.shape[1] * 2 != n:
+        raise ValueError(f"MPP W4 weight {tuple(qweight.shape)} does not hold {n} output features")
+    return repack_mpp_weight_for_cdna4(qweight)
 
 
 def _validate_mpp_weight_layout(qweight: torch.Tensor, k: int) -> int:
@@ -327,16 +334,13 @@ def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
 
 def _w4a4(act: torch.Tensor, act_format: int, k: int, qweight, xscales, wscales, bias, output_dtype, n=None):
     m = act.shape[0]
-    if qweight.ndim == 3 and n is not None:
-        _check_cdna4(qweight, n, k)
-        w = qweight.contiguous()
-    else:
-        w, n_pad = _weight_cdna4(qweight, k)
-        n = n if n is not None else n_pad
+    n_layout = _weight_n(qweight, k)
+    n = n if n is not None else n_layout
     if k % 32:
         raise ValueError(f"MPP W4 TensorOp requires K divisible by 32, got {k}")
     _validate_mpp_epilogue(m, n, xscales, wscales, bias)
-    nat.require_device(act, w, xscales, wscales, bias)
+    nat.require_device(act, qweight, xscales, wscales, bias)
+    w = _as_cdna4(qweight, n, k)
     out = torch.empty((m, n), dtype=output_dtype, device=act.device)
     xs, ws, b = _f32(xscales), _f32(wscales), _f32(bias)
     nat.check(
@@ -378,17 +382,14 @@ def hip_w4a16_matmul(activations, qweight, wscales, bias, *, output_dtype, out_f
     if activations.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError(f"MPP W4A16 requires float16 or bfloat16 activation, got {activations.dtype}")
     m, k = activations.shape
-    if qweight.ndim == 3 and out_features is not None:
-        _check_cdna4(qweight, out_features, k)
-        w, n = qweight.contiguous(), out_features
-    else:
-        w, n_pad = _weight_cdna4(qweight, k)
-        n = out_features if out_features is not None else n_pad
+    n_layout = _weight_n(qweight, k)
+    n = out_features if out_features is not None else n_layout
     if k % 32:
         raise ValueError(f"MPP W4 TensorOp requires K divisible by 32, got {k}")
     _validate_mpp_epilogue(m, n, None, wscales, bias)
+    nat.require_device(activations, qweight, wscales, bias)
     act = activations.contiguous()
-    nat.require_device(act, w, wscales, bias)
+    w = _as_cdna4(qweight, n, k)
     out = torch.empty((m, n), dtype=output_dtype, device=act.device)
     ws, b = _f32(wscales), _f32(bias)
     nat.check(

@@ -1,0 +1,125 @@
+"""CPU: the C-ABI library loads, exports every symbol include/convrot_amd.h declares,
+and rejects invalid arguments with the documented status codes and messages before any
+launch (no GPU is touched by these calls)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "convrot_amd.h"
+
+
+def header_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(convrot_[a-z0-9_]+)\s*\(", text)))
+
+
+def header_constants() -> dict[str, int]:
+    return {k: int(v, 0) for k, v in re.findall(r"#define\s+(CONVROT_[A-Z0-9_]+)\s+(0x[0-9a-fA-F]+|\d+)", HEADER.read_text())}
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from convrot_mlx_amd import _native
+
+    return _native.load()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    from convrot_mlx_amd import _native
+
+    names = header_functions()
+    assert len(names) >= 9
+    for name in names:
+        assert hasattr(lib, name), f"{name} missing from {_native.LIB_PATH.name}"
+    assert set(names) == set(_native.SIGNATURES), "ctypes binding and header disagree"
+
+
+def test_constants_match_binding():
+    from convrot_mlx_amd import _native as n
+
+    c = header_constants()
+    assert (c["CONVROT_DTYPE_F32"], c["CONVROT_DTYPE_F16"], c["CONVROT_DTYPE_BF16"]) == (n.DTYPE_F32, n.DTYPE_F16, n.DTYPE_BF16)
+    assert (c["CONVROT_PREP_PACKED"], c["CONVROT_PREP_INT8"], c["CONVROT_PREP_ROTATE"], c["CONVROT_PREP_NO_ROTATE"]) == (
+        n.PREP_PACKED, n.PREP_INT8, n.PREP_ROTATE, n.PREP_NO_ROTATE)
+    assert (c["CONVROT_LAYOUT_NK"], c["CONVROT_LAYOUT_KN"], c["CONVROT_LAYOUT_CDNA4"]) == (n.LAYOUT_NK, n.LAYOUT_KN, n.LAYOUT_CDNA4)
+    assert (c["CONVROT_ACT_PACKED"], c["CONVROT_ACT_INT8"]) == (n.ACT_PACKED, n.ACT_INT8)
+    assert (c["CONVROT_OK"], c["CONVROT_ERR_INVALID"], c["CONVROT_ERR_UNSUPPORTED"], c["CONVROT_ERR_LAUNCH"]) == (
+        n.OK, n.ERR_INVALID, n.ERR_UNSUPPORTED, n.ERR_LAUNCH)
+
+
+def test_version_and_sizes(lib):
+    assert b"gfx950" in lib.convrot_version()
+    assert lib.convrot_cdna4_bytes(3072, 12288) == 12288 * 3072 // 2
+    assert lib.convrot_cdna4_bytes(46, 64) == 3 * 1 * 1024  # N padded to 48, K to 128
+    assert lib.convrot_cdna4_bytes(-1, 5) == -1
+
+
+def _err(lib):
+    return lib.convrot_last_error().decode()
+
+
+BF16 = 2
+
+
+@pytest.mark.parametrize("G,msg", [(128, "Regular Hadamard size must be a power of 4, got 128"),
+                                    (2, "Regular Hadamard size must be a power of 4, got 2"),
+                                    (4096, "fused ConvRot supports groups [4, 16, 64, 256, 1024], got 4096")])
+def test_prepare_rejects_group_sizes(lib, G, msg):
+    rc = lib.convrot_prepare(None, BF16, 4, 4096, G, 0, None, None, None)
+    assert rc in (1, 2) and _err(lib) == msg
+
+
+def test_prepare_rejects_shapes(lib):
+    assert lib.convrot_prepare(None, BF16, 4, 320, 256, 0, None, None, None) == 1
+    assert _err(lib) == "features 320 not divisible by ConvRot group size 256"
+    assert lib.convrot_prepare(None, BF16, 4, 8, 4, 0, None, None, None) == 2
+    assert "divisible by 16" in _err(lib)
+    assert lib.convrot_prepare(None, BF16, 1, 131072, 256, 0, None, None, None) == 2
+    assert "at most 65536 features" in _err(lib)
+    assert lib.convrot_prepare(None, 7, 1, 256, 256, 0, None, None, None) == 1
+    assert lib.convrot_prepare(None, BF16, 1, 256, 256, 9, None, None, None) == 1
+    assert lib.convrot_prepare(None, BF16, 1, 256, 256, 2 | 0x10, None, None, None) == 1
+    # valid shape, nothing to do
+    assert lib.convrot_prepare(None, BF16, 0, 256, 256, 0, None, None, None) == 0
+    # valid shape, null buffers
+    assert lib.convrot_prepare(None, BF16, 2, 256, 256, 0, None, None, None) == 1
+    assert _err(lib) == "null pointer argument"
+
+
+def test_gemm_validation(lib):
+    assert lib.convrot_w4a4_gemm(None, 1, None, None, None, None, 4, 8, 48, None, BF16, None) == 1
+    assert _err(lib) == "W4A4 GEMM requires K divisible by 32, got 48"
+    assert lib.convrot_w4a4_gemm(None, 5, None, None, None, None, 4, 8, 64, None, BF16, None) == 1
+    assert lib.convrot_w4a4_gemm(None, 1, None, None, None, None, 0, 8, 64, None, BF16, None) == 0
+    assert lib.convrot_w4a16_gemm(None, 0, None, None, None, 4, 8, 64, None, BF16, None) == 1
+    assert _err(lib) == "MPP W4A16 requires float16 or bfloat16 activation, got float32"
+    assert lib.convrot_w4a16_gemm(None, BF16, None, None, None, 4, 8, 65600, None, BF16, None) == 2
+
+
+def test_repack_validation(lib):
+    assert lib.convrot_repack_weight(None, 0, None, 1, 33, 64, None) == 1
+    assert _err(lib) == "MPP int4 packing requires even out_features, got 33"
+    assert lib.convrot_repack_weight(None, 1, None, 0, 34, 63, None) == 1
+    assert lib.convrot_repack_weight(None, 0, None, 5, 34, 64, None) == 1
+    assert lib.convrot_pack_int4(None, 0, 8, None, None) == 0
+
+
+def test_errors_are_thread_local(lib):
+    import threading
+
+    lib.convrot_w4a4_gemm(None, 1, None, None, None, None, 4, 8, 48, None, BF16, None)
+    seen = {}
+
+    def other():
+        seen["msg"] = lib.convrot_last_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == "" and _err(lib).startswith("W4A4 GEMM requires")
