@@ -10,7 +10,7 @@
 
 namespace convrot {
 
-bool prep_plan(int64_t K, int* ni_out, int* waves_out);
+bool prep_plan(int64_t rows, int64_t K, int* ni_out, int* waves_out);
 
 hipError_t launch_prep(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode, void* out,
                        float* scales, hipStream_t stream);

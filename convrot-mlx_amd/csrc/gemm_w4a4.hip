@@ -33,6 +33,10 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
 #include "convrot_device.h"
 #include "convrot_launch.h"
 
@@ -334,83 +338,42 @@ __device__ __forceinline__ int a_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1
 // INT8-activation GEMM with direct-to-LDS loads: each 1 KB piece of a
 // k-block (8 activation rows x 128 features, or one CDNA4 weight block) is
 // fetched by one wave instruction (buffer_load_dwordx4 ... lds) straight into
-// a STAGES-deep LDS ring, so no registers stage the data and loads run
-// STAGES-1 blocks ahead of the MFMAs.  Every activation load reads whole
-// 128-byte lines; inside LDS the 16-byte chunks of each row are permuted by
-// a_swizzle so that the MFMA fragment reads (16 rows x 16 bytes) are
-// bank-conflict free.  Out-of-range rows/blocks read as zero through the
-// buffer range check (no branches in the loop).
-template <int BM, int BN, int WM, int WN, int STAGES, bool PINGPONG, int ODT>
-__global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
-    const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
-    const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
-    int K, int nblocks, int kblocks, int tiles_m, int tiles_n) {
-  constexpr int NW = WM * WN;
-  constexpr int TM = BM / WM, TN = BN / WN;
-  constexpr int FM = TM / 16, FN = TN / 16;
-  constexpr int A_FRAGS = (BM / 16) * 2, B_FRAGS = BN / 16;
-  constexpr int LOADS = A_FRAGS + B_FRAGS;
-  constexpr int STAGE_BYTES = LOADS * 1024;
+// a 3-deep LDS ring, so no registers stage the data and loads run ahead of
+// the MFMAs.  Every activation load reads whole 128-byte lines; inside LDS
+// the 16-byte chunks of each row are permuted by a_swizzle so that the MFMA
+// fragment reads (16 rows x 16 bytes) are bank-conflict free.  Out-of-range
+// rows/blocks read as zero through the buffer range check (no branches in the
+// loop).
+//
+// DmaEngine runs any k-range of one BM x BN output tile; the data-parallel
+// kernel runs whole tiles with it and the stream-K kernel runs tile pieces.
+//
+// Fragment pipelines (how LDS reads overlap the MFMAs):
+//  kSingle   one register set, read just before the block's MFMAs (the 8-wave
+//            256x256 tile: two waves per SIMD cover each other's reads);
+//  kPingPong two full sets, block i+1 read during block i's MFMAs.
+// (A 4-wave 256x256 tile with one wave per SIMD and the accumulator in the
+// AGPRs, fed by k-step-split reads, measured 1.8x slower: the compiler cannot
+// keep a 256-register accumulator in place and spills inside the loop.)
+enum Pipe : int { kSingle = 0, kPingPong = 1 };
+
+template <int BM, int BN, int WM, int WN, int PIPE>
+struct DmaEngine {
+  static constexpr int NW = WM * WN;
+  static constexpr int TM = BM / WM, TN = BN / WN;
+  static constexpr int FM = TM / 16, FN = TN / 16;
+  static constexpr int A_FRAGS = (BM / 16) * 2, B_FRAGS = BN / 16;
+  static constexpr int LOADS = A_FRAGS + B_FRAGS;
+  static constexpr int STAGES = 3;
+  static constexpr int STAGE_BYTES = LOADS * 1024;
+  static constexpr int SMEM_BYTES = STAGES * STAGE_BYTES;
+  static constexpr int LPW = LOADS / NW;  // DMA instructions per wave per k-block
+  static constexpr int APW = A_FRAGS / NW, BPW = B_FRAGS / NW;  // of which activation / weight
+  static constexpr int SHIFT = 4;         // weights unpacked x16: acc = 16 * dot
+  static constexpr int STAGING = TM * (TN * 2 + 16);  // epilogue LDS bytes per wave
   static_assert(LOADS % NW == 0, "fragment loads must split evenly over waves");
-  constexpr int LPW = LOADS / NW;
-  constexpr int SHIFT = 4;  // weights unpacked x16
-
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / WN, wn = wave % WN;
-
-  const int tiles = tiles_m * tiles_n;
-  int logical = blockIdx.x;
-  const int per_xcd = tiles / kXcds;
-  if (logical < per_xcd * kXcds) logical = (logical % kXcds) * per_xcd + logical / kXcds;
-  const int group = logical / (kGroupM * tiles_n);
-  const int first_m = group * kGroupM;
-  const int group_rows = min(kGroupM, tiles_m - first_m);
-  const int in_group = logical - group * kGroupM * tiles_n;
-  const int m0 = (first_m + in_group % group_rows) * BM;
-  const int n0 = (in_group / group_rows) * BN;
-
-  const int rows_valid = min(BM, M - m0);
-  const i32x4_sgpr ra = buffer_rsrc(act + (int64_t)m0 * K, (uint32_t)rows_valid * (uint32_t)K);
-  const uint8_t* wbase = wq + (int64_t)(n0 / 16) * 1024;
-  const uint32_t wbytes = (uint32_t)(((int64_t)kblocks * nblocks - n0 / 16) * 1024);
-  const i32x4_sgpr rw = buffer_rsrc(wbase, wbytes);
-  const uint32_t smem_addr = (uint32_t)(uintptr_t)smem;
-
-  // This wave's fragment loads: resource, per-lane byte offset at k-block 0
-  // and byte stride per k-block (selected once, branch-free in the loop).
-  i32x4_sgpr rs[LPW];
-  uint32_t voff[LPW], kstride[LPW];
-#pragma unroll
-  for (int i = 0; i < LPW; ++i) {
-    const int j = wave * LPW + i;
-    const bool is_a = j < A_FRAGS;
-    // A: instruction j covers rows 8j .. 8j+7 of the tile, 128 bytes each (full
-    // cache lines).  LDS slot p of row r holds 16-byte chunk p ^ swz(r).
-    const int r = 8 * j + (lane >> 3);
-    const int chunk = (lane & 7) ^ a_swizzle(r);
-    const uint32_t va = (uint32_t)(r * K + 16 * chunk);
-    const uint32_t vb = (uint32_t)((j - A_FRAGS) * 1024 + lane * 16);
-    voff[i] = is_a ? va : vb;
-    kstride[i] = is_a ? 128u : (uint32_t)nblocks * 1024u;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) rs[i][c] = is_a ? ra[c] : rw[c];
-  }
-  auto issue = [&](int kb, int stage) {
-#pragma unroll
-    for (int i = 0; i < LPW; ++i) {
-      const uint32_t dst = smem_addr + (uint32_t)(stage * STAGE_BYTES + (wave * LPW + i) * 1024);
-      dma16(rs[i], voff[i] + (uint32_t)kb * kstride[i], dst);
-    }
-  };
-
-  i32x4 acc[FN][FM];
-#pragma unroll
-  for (int a = 0; a < FN; ++a)
-#pragma unroll
-    for (int b = 0; b < FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
+  static_assert(A_FRAGS % NW == 0 && B_FRAGS % NW == 0 && APW % 2 == 0, "each wave loads APW (even) + BPW pieces");
+  static_assert(NW * STAGING <= SMEM_BYTES, "epilogue staging exceeds LDS");
 
   // Fragments of one k-block held in registers: packed weights (both k-steps)
   // and int8 activations for k-steps 0 and 1.
@@ -418,21 +381,89 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
     uint4 b[FN];
     i32x4 a[2][FM];
   };
-  auto read_frags = [&](int stage, Frags& f) {
+
+  uint8_t* smem;
+  uint32_t smem_addr;
+  int lane, wave, wm, wn;
+  // This wave's loads: activation pieces j = wave APW + i (rows 8j .. 8j+7)
+  // and weight blocks j = wave BPW + i.  Per-lane byte offsets: va[j & 1]
+  // for activations (the row swizzle flips with the parity of j, which is
+  // i's since APW is even), vb for weights; the rest of each offset is
+  // wave-uniform and added at issue time (it changes with k, so the sums are
+  // never hoisted into registers).
+  i32x4_sgpr ra, rw;
+  uint32_t va[2], vb;
+  uint32_t a_kstride, w_kstride, krow;
+
+  __device__ __forceinline__ explicit DmaEngine(uint8_t* s) : smem(s) {
+    smem_addr = (uint32_t)(uintptr_t)s;
+    lane = threadIdx.x & 63;
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    wm = wave / WN;
+    wn = wave % WN;
+  }
+
+  __device__ __forceinline__ uint8_t* staging() const { return smem + wave * STAGING; }
+
+  // Point the loads at the output tile whose top-left corner is (m0, n0).
+  __device__ __forceinline__ void set_tile(const int8_t* act, const uint8_t* wq, int M, int K, int nblocks,
+                                           int kblocks, int m0, int n0) {
+    const int rows_valid = min(BM, M - m0);
+    ra = buffer_rsrc(act + (int64_t)m0 * K, (uint32_t)rows_valid * (uint32_t)K);
+    const uint8_t* wbase = wq + (int64_t)(n0 / 16) * 1024;
+    const uint32_t wbytes = (uint32_t)(((int64_t)kblocks * nblocks - n0 / 16) * 1024);
+    rw = buffer_rsrc(wbase, wbytes);
+    // Activation piece j: lane L reads row 8j + (L >> 3), 16-byte chunk
+    // (L & 7) ^ swz(row) of the row's 128 bytes (whole cache lines), where
+    // swz(row) = (L >> 3) ^ (j & 1).  The row term 8 j K stays in the
+    // per-lane offset so rows at or beyond M fail the buffer range check.
+    const int rl = lane >> 3, c = lane & 7;
+    va[0] = (uint32_t)(rl * K + 16 * (c ^ rl));
+    va[1] = (uint32_t)(rl * K + 16 * (c ^ rl ^ 1));
+    vb = (uint32_t)lane * 16u;
+    krow = 8u * (uint32_t)K;
+    a_kstride = 128u;
+    w_kstride = (uint32_t)nblocks * 1024u;
+  }
+
+  __device__ __forceinline__ void issue(int kb, int stage) {
+    const uint32_t base = smem_addr + (uint32_t)(stage * STAGE_BYTES);
+    // The scalar parts go through an empty asm so the compiler cannot split
+    // off their loop-invariant share and keep one register per load.
+#pragma unroll
+    for (int i = 0; i < APW; ++i) {
+      const uint32_t j = (uint32_t)(wave * APW + i);
+      uint32_t so = j * krow + (uint32_t)kb * a_kstride;
+      asm volatile("" : "+s"(so));
+      dma16(ra, va[i & 1] + so, base + j * 1024u);
+    }
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+      const uint32_t j = (uint32_t)(wave * BPW + i);
+      uint32_t so = j * 1024u + (uint32_t)kb * w_kstride;
+      asm volatile("" : "+s"(so));
+      dma16(rw, vb + so, base + (uint32_t)(A_FRAGS + j) * 1024u);
+    }
+  }
+
+  __device__ __forceinline__ void read_frags(int stage, Frags& f) const {
     const uint8_t* st = smem + stage * STAGE_BYTES;
+    const uint8_t* sb = st + (A_FRAGS + wn * FN) * 1024 + lane * 16;
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) f.b[fn] = *(const uint4*)(st + (A_FRAGS + wn * FN + fn) * 1024 + lane * 16);
+    for (int fn = 0; fn < FN; ++fn) f.b[fn] = *(const uint4*)(sb + fn * 1024);
+    // Row (wm FM + fm) 16 + (lane & 15) holds features 32q + 16ks .. +16 in
+    // chunk (2q + ks) ^ swz(row); swz depends on row & 15 = lane & 15 only, so
+    // one address per k-step serves every fm (fm adds 2 KB, an immediate).
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < 2; ++ks) {
+      const int r = lane & 15;
+      const uint8_t* sa = st + (wm * FM * 16 + r) * 128 + (((2 * (lane >> 4) + ks) ^ a_swizzle(r)) * 16);
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm) {
-        // row m of 16-row group g, features 32q + 16ks .. +16 = chunk 2q + ks
-        const int row = (wm * FM + fm) * 16 + (lane & 15);
-        const int chunk = (2 * (lane >> 4) + ks) ^ a_swizzle(row);
-        f.a[ks][fm] = *(const i32x4*)(st + row * 128 + chunk * 16);
-      }
-  };
-  auto mma = [&](const Frags& f) {
+      for (int fm = 0; fm < FM; ++fm) f.a[ks][fm] = *(const i32x4*)(sa + fm * 2048);
+    }
+  }
+
+  __device__ __forceinline__ static void mma(const Frags& f, i32x4 (&acc)[FN][FM]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       i32x4 bop[FN];
@@ -451,62 +482,542 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
         for (int fn = 0; fn < FN; ++fn)
           acc[fn][fm] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bop[fn], f.a[ks][fm], acc[fn][fm], 0, 0, 0);
     }
-  };
+  }
 
-  // Pipeline: DMA runs STAGES-1 blocks ahead; fragments of block kb+1 are
-  // read from LDS into the spare register set while block kb's MFMAs run.
-  // One barrier per block: it publishes DMA(kb+1) and retires all reads of
-  // stage kb % STAGES, which the next DMA then refills.
-  static_assert(STAGES == 3, "pipeline written for three LDS stages");
-  Frags f0;
-  [[maybe_unused]] Frags f1;
-  if constexpr (PINGPONG) {
-    // DMA three blocks ahead; block kb+1's fragments are read into the spare
-    // register set while block kb's MFMAs run.  The barrier of step kb
-    // publishes DMA(kb+1) and retires every wave's reads of stage kb % 3
-    // (issued in step kb-1), which DMA(kb+3) then refills.
-#pragma unroll
-    for (int s = 0; s < STAGES; ++s) issue(s, s);
-    wait_vmcnt<2 * LPW>();
-    __syncthreads();
-    read_frags(0, f0);
-    auto step = [&](int kb, Frags& cur, Frags& nxt) {
-      wait_vmcnt<LPW>();
-      __syncthreads();
-      issue(kb + STAGES, kb % STAGES);
-      if (kb + 1 < kblocks) read_frags((kb + 1) % STAGES, nxt);
-      mma(cur);
+  // acc += the products over k-blocks kb0 .. kb0+n-1 (n >= 1).  Every DMA has
+  // retired on return; the caller puts a barrier between this and any reuse
+  // of the ring (epilogue staging or the next run).
+  __device__ __forceinline__ void run(int kb0, int n, i32x4 (&acc)[FN][FM]) {
+    prologue(kb0, n);
+    body(kb0, n, acc, nullptr);
+  }
+
+  // First DMAs of a run: k-blocks kb0 .. kb0+2 (kPingPong) or kb0 .. kb0+1
+  // into stages 0, 1(, 2).  The ring must be free (barrier after its last reads).
+  __device__ __forceinline__ void prologue(int kb0, int n) {
+    issue(kb0, 0);
+    if (n > 1) issue(kb0 + 1, 1);
+    if constexpr (PIPE == kPingPong)
+      if (n > 2) issue(kb0 + 2, 2);
+  }
+
+  // The rest of a run after prologue(kb0, n).  The prologue's DMAs must be the
+  // newest vector-memory operations of the wave.  vmcnt retires in issue
+  // order, so the first wait also retires everything the wave issued before
+  // the prologue; if `flag` is set, lane 0 raises it right after that wait.
+  __device__ __forceinline__ void body(int kb0, int n, i32x4 (&acc)[FN][FM], int* flag) {
+    auto raise = [&]() {
+      if (flag && lane == 0) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
-    int kb = 0;
-    for (; kb + 1 < kblocks; kb += 2) {
-      step(kb, f0, f1);
-      step(kb + 1, f1, f0);
-    }
-    if (kb < kblocks) step(kb, f0, f1);
-  } else {
-    // One register set: DMA two blocks ahead.  The barrier of iteration kb
-    // publishes DMA(kb) and retires every wave's reads of stage (kb-1) % 3,
-    // which DMA(kb+2) then refills.
-    issue(0, 0);
-    issue(1, 1);
-    for (int kb = 0; kb < kblocks; ++kb) {
-      wait_vmcnt<LPW>();
+    Frags f0;
+    if constexpr (PIPE == kPingPong) {
+      // DMA three blocks ahead; block i+1's fragments are read into the spare
+      // register set while block i's MFMAs run.  The barrier of step i
+      // publishes DMA(i+1) and retires every wave's reads of stage i % 3
+      // (issued in step i-1), which DMA(i+3) then refills.
+      Frags f1;
+      if (n > 2) wait_vmcnt<2 * LPW>();
+      else if (n > 1) wait_vmcnt<LPW>();
+      else wait_vmcnt<0>();
+      raise();
       __syncthreads();
-      issue(kb + 2, (kb + 2) % STAGES);
-      read_frags(kb % STAGES, f0);
-      mma(f0);
+      read_frags(0, f0);
+      auto step = [&](int i, Frags& cur, Frags& nxt) {
+        // outstanding: blocks i+1 and i+2 (those below n); block i+1 must land
+        if (i + 2 < n) wait_vmcnt<LPW>();
+        else wait_vmcnt<0>();
+        __syncthreads();
+        if (i + 3 < n) issue(kb0 + i + 3, i % 3);
+        if (i + 1 < n) read_frags((i + 1) % 3, nxt);
+        mma(cur, acc);
+      };
+      int i = 0;
+      for (; i + 1 < n; i += 2) {
+        step(i, f0, f1);
+        step(i + 1, f1, f0);
+      }
+      if (i < n) step(i, f0, f1);
+    } else {
+      // One register set: DMA two blocks ahead.  The barrier of iteration i
+      // publishes DMA(i) and retires every wave's reads of stage (i-1) % 3,
+      // which DMA(i+2) then refills.
+      for (int i = 0; i < n; ++i) {
+        if (i + 1 < n) wait_vmcnt<LPW>();
+        else wait_vmcnt<0>();
+        if (i == 0) raise();
+        __syncthreads();
+        if (i + 2 < n) issue(kb0 + i + 2, (i + 2) % 3);
+        read_frags(i % 3, f0);
+        // Issue all of the block's fragment reads before its MFMAs; left to
+        // itself the compiler reads two fragments at a time just before use
+        // and the MFMA pipe waits out each LDS round trip.
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f0, acc);
+      }
     }
   }
-  wait_vmcnt<0>();
-  __syncthreads();  // all waves done with the LDS ring before it is reused for output staging
-  static_assert(NW * TM * (TN * 2 + 16) <= STAGES * STAGE_BYTES, "epilogue staging exceeds LDS");
-  epilogue<ODT, TM, TN, SHIFT>(acc, smem + wave * TM * (TN * 2 + 16), lane, m0 + wm * TM, n0 + wn * TN, M, N,
-                               xscales, wscales, bias, out);
+};
+
+// Top-left corner of logical tile `t`: tiles are walked kGroupM tile rows at
+// a time, N-major inside a group, so consecutive tiles share activation rows.
+__device__ __forceinline__ void tile_origin(int t, int tiles_m, int tiles_n, int bm, int bn, int& m0, int& n0) {
+  const int group = t / (kGroupM * tiles_n);
+  const int first_m = group * kGroupM;
+  const int group_rows = min(kGroupM, tiles_m - first_m);
+  const int in_group = t - group * kGroupM * tiles_n;
+  m0 = (first_m + in_group % group_rows) * bm;
+  n0 = (in_group / group_rows) * bn;
 }
+
+// One workgroup per output tile.  Workgroups are renumbered so that the
+// tiles one XCD (one L2) runs are adjacent in the grouped tile order.
+template <int BM, int BN, int WM, int WN, int PIPE, int ODT>
+__global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
+    const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
+    const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
+    int K, int nblocks, int kblocks, int tiles_m, int tiles_n) {
+  using E = DmaEngine<BM, BN, WM, WN, PIPE>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
+  E e(smem);
+
+  const int tiles = tiles_m * tiles_n;
+  int logical = blockIdx.x;
+  const int per_xcd = tiles / kXcds;
+  if (logical < per_xcd * kXcds) logical = (logical % kXcds) * per_xcd + logical / kXcds;
+  int m0, n0;
+  tile_origin(logical, tiles_m, tiles_n, BM, BN, m0, n0);
+
+  e.set_tile(act, wq, M, K, nblocks, kblocks, m0, n0);
+  i32x4 acc[E::FN][E::FM];
+#pragma unroll
+  for (int a = 0; a < E::FN; ++a)
+#pragma unroll
+    for (int b = 0; b < E::FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
+  e.run(0, kblocks, acc);
+  __syncthreads();  // all waves done with the LDS ring before it is reused for output staging
+  epilogue<ODT, E::TM, E::TN, E::SHIFT>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M, N,
+                                        xscales, wscales, bias, out);
+}
+
+// ---- stream-K
+//
+// Workspace (device memory owned by the launcher, one per device and stream):
+//   int32 words [0, 8)       ticket counter of each workgroup group
+//   int32 words [8, 16)      finished-workgroup counter of each group
+//   int32 words [64, 64+G*NW) partial-ready flag of each (workgroup slot, wave)
+//   bytes [kSkPartialOffset, ...)  one int32 partial tile per workgroup slot
+// Every counter and flag is back at zero when a launch ends, so consecutive
+// launches on one stream share the workspace; launches that overlap in time
+// (two streams) must not.
+constexpr int kSkCtlWords = 64;
+constexpr int64_t kSkPartialOffset = 32768;
+constexpr int kSkMaxGrid = 512;  // <= 64 workgroups per group: one lane per contributor when polling
+constexpr int kSkMaxWaves = 8;
+static_assert(kSkCtlWords + kSkMaxGrid * kSkMaxWaves <= kSkPartialOffset / 4, "flags overflow the control block");
+constexpr int kSkSpinLimit = 1 << 22;  // ~1 s of s_sleep: a lost flag ends the wait instead of hanging
+
+// Partials and flags are exchanged with device-scope (sc1) accesses only:
+// each is coherent across CUs (and XCDs) by itself, and order is kept by
+// waiting for the partial's stores to complete (vmcnt 0) before its flag is
+// raised and by issuing the loads only after the flag was seen.  Acquire /
+// release fences would also work but write back and invalidate the whole L2
+// of the XCD, which evicts the operand tiles every other workgroup is using.
+// The partial's loads are issued through asm: as C++ atomics the compiler
+// waits for each load before issuing the next (one round trip per 8 bytes).
+// Its stores stay C++ atomics (64-bit): the compiler must see every store to
+// keep the wait state a VMEM store of more than 64 bits needs before its data
+// registers are rewritten, which it cannot do for a store inside asm.
+template <int OFF>
+__device__ __forceinline__ i32x4 load_dev16(const void* p) {
+  i32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off offset:%2 sc1" : "=v"(v) : "v"(p), "i"(OFF) : "memory");
+  return v;
+}
+
+// One wave's partial tile: fragment f = fn * FM + fm at byte 1024 f + 16 lane.
+template <int FN, int FM>
+__device__ __forceinline__ void sk_store_partial(uint8_t* dst, int lane, const i32x4 (&acc)[FN][FM]) {
+  uint64_t* p = (uint64_t*)(dst + lane * 16);
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const i32x4 a = acc[fn][fm];
+      uint64_t* q = p + (fn * FM + fm) * 128;
+      __hip_atomic_store(q, (uint64_t)(uint32_t)a[0] | ((uint64_t)(uint32_t)a[1] << 32), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(q + 1, (uint64_t)(uint32_t)a[2] | ((uint64_t)(uint32_t)a[3] << 32), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// acc += one wave's partial tile: loads in batches of up to 16 fragments
+// (8 beside a 32-fragment accumulator), one wait per batch.
+template <int FN, int FM>
+__device__ __forceinline__ void sk_add_partial(const uint8_t* src, int lane, i32x4 (&acc)[FN][FM]) {
+  constexpr int NF = FN * FM;
+  constexpr int BATCH = NF >= 32 ? 8 : NF;
+  static_assert(NF % 4 == 0 && NF % BATCH == 0, "fragment batches");
+  const uint8_t* p = src + lane * 16;
+#pragma unroll
+  for (int b = 0; b < NF; b += BATCH) {
+    i32x4 v[BATCH];
+#pragma unroll
+    for (int j = 0; j < BATCH; j += 4) {
+      const uint8_t* q = p + (b + j) * 1024;
+      v[j] = load_dev16<0>(q);
+      v[j + 1] = load_dev16<1024>(q);
+      v[j + 2] = load_dev16<2048>(q);
+      v[j + 3] = load_dev16<3072>(q);
+    }
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      asm volatile("" : "+v"(v[j]));  // the adds stay behind the wait
+      acc[(b + j) / FM][(b + j) % FM] += v[j];
+    }
+  }
+}
+
+// Lane i < n waits for flag first[i * stride] (all in parallel), then clears it.
+__device__ __forceinline__ void sk_wait_flags(int* first, int stride, int n, int lane) {
+  int* f = first + (int64_t)lane * stride;
+  bool seen = lane >= n;
+  for (int it = 0; it < kSkSpinLimit; ++it) {
+    if (!seen) seen = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    if (__ballot(!seen) == 0) break;
+    __builtin_amdgcn_s_sleep(4);
+  }
+  if (lane < n) __hip_atomic_store(f, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Persistent stream-K GEMM (Osama et al., "Stream-K: Work-centric Parallel
+// Decomposition for Dense Matrix-Matrix Multiplication on the GPU", 2023), in
+// its data-parallel + stream-K hybrid form, run per XCD.
+//
+// The grid is G = 8 P workgroups; workgroup b belongs to group b % 8 (the XCD
+// it is dispatched to) and takes a ticket 0..P-1 inside its group at start,
+// so ticket order is start order.  Group x owns a contiguous run of Tx tiles
+// of the grouped tile order (the same tiles the data-parallel kernel gives
+// XCD x).  When Tx is not a multiple of P, all but the last one-to-two rounds
+// of tiles run whole (data-parallel) and the remaining tiles' k-blocks are
+// split into psk contiguous ranges, one per ticket.  Each workgroup walks its
+// range from the top down, so the piece holding a tile's last k-blocks --
+// whose workgroup owns the tile -- is the last piece that workgroup runs,
+// while every other piece of the tile is the first stream-K piece of its
+// (lower-ticket) workgroup.  Non-owners store their int32 partial sums and
+// raise one flag per wave; each wave of the owner waits for the matching
+// waves of the lower tickets that share its tile, adds their partials
+// (integer addition: the result is bit-identical to a single pass) and the
+// workgroup runs the fused epilogue.  Waits only ever point at lower tickets,
+// i.e. at workgroups that have already started and that wait only on lower
+// tickets themselves, so the kernel finishes whatever the residency.
+template <int BM, int BN, int WM, int WN, int PIPE, int ODT>
+__global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
+    const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
+    const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
+    int K, int nblocks, int kblocks, int tiles_m, int tiles_n, uint8_t* __restrict__ work, int min_iters) {
+  using E = DmaEngine<BM, BN, WM, WN, PIPE>;
+  constexpr int FN = E::FN, FM = E::FM, NW = E::NW;
+  static_assert(NW <= kSkMaxWaves, "flag block sized for 8 waves");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
+  __shared__ int s_ticket;
+
+  int* ctl = (int*)work;
+  int* flags = ctl + kSkCtlWords;
+  uint8_t* partials = work + kSkPartialOffset;
+  const int group = blockIdx.x % kXcds;
+  const int P = gridDim.x / kXcds;
+  if (threadIdx.x == 0) s_ticket = atomicAdd(&ctl[group], 1);
+  __syncthreads();
+  const int p = __builtin_amdgcn_readfirstlane(s_ticket);
+  E e(smem);
+
+  const int tiles = tiles_m * tiles_n;
+  const int base = tiles / kXcds, extra = tiles % kXcds;
+  const int tb = group * base + min(group, extra);
+  const int tx = base + (group < extra ? 1 : 0);
+  const int rounds = tx / P, rem = tx % P;
+  const int dp = rem == 0 ? tx : (rounds > 0 ? (rounds - 1) * P : 0);
+
+  // Work items of this workgroup, in order: whole tiles p, p+P, ... < dp,
+  // then the pieces of its stream-K range [lo, hi) from the top down.
+  // (Range arithmetic fits 32 bits: fewer than 2P tiles of <= 512 k-blocks.)
+  const int sk_iters = (tx - dp) * kblocks;
+  const int psk = min(P, max(1, sk_iters / max(1, min_iters)));
+  const bool in_sk = sk_iters > 0 && p < psk;
+  const int lo = in_sk ? sk_iters * p / psk : 0;
+  int hi = in_sk ? sk_iters * (p + 1) / psk : 0;
+  int next_dp = p;
+  auto next_item = [&](int& t, int& k0, int& k1) {
+    if (next_dp < dp) {
+      t = next_dp;
+      k0 = 0;
+      k1 = kblocks;
+      next_dp += P;
+      return true;
+    }
+    if (hi > lo) {
+      const int ts = (hi - 1) / kblocks;
+      const int seg = max(lo, ts * kblocks);
+      t = dp + ts;
+      k0 = seg - ts * kblocks;
+      k1 = hi - ts * kblocks;
+      hi = seg;
+      return true;
+    }
+    return false;
+  };
+
+  i32x4 acc[FN][FM];
+  int t = 0, k0 = 0, k1 = 0;
+  bool have = next_item(t, k0, k1);
+  bool prefetched = false;  // the item's tile is set and its prologue DMAs issued
+  int* pending = nullptr;   // this wave's partial-ready flag, raised by the next body
+  while (have) {
+    // Opaque per item: keeps the compiler from hoisting lane-derived epilogue
+    // and partial addresses out of the loop, where they would stay live
+    // (and spill) across the MFMA pipeline.
+    asm volatile("" : "+v"(e.lane));
+    int m0, n0;
+    tile_origin(tb + t, tiles_m, tiles_n, BM, BN, m0, n0);
+    if (!prefetched) {
+      e.set_tile(act, wq, M, K, nblocks, kblocks, m0, n0);
+      e.prologue(k0, k1 - k0);
+    }
+#pragma unroll
+    for (int a = 0; a < FN; ++a)
+#pragma unroll
+      for (int b = 0; b < FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
+    e.body(k0, k1 - k0, acc, pending);
+    pending = nullptr;
+
+    int nt = 0, nk0 = 0, nk1 = 0;
+    const bool more = next_item(nt, nk0, nk1);
+    prefetched = false;
+    // Partial tile of slot s: BM * BN * 4 bytes at partials + s * BM * BN * 4.
+    const int64_t wave_off = (int64_t)e.wave * (FN * FM * 1024);
+    if (k1 < kblocks) {
+      // Not the tile's last k-blocks: publish the partial sums for the owner.
+      // The stores go out first, then the next item's first DMAs, and the
+      // next body raises the flag once its first wait has retired both (so
+      // the store round trip overlaps the DMA one and the MFMAs after it).
+      sk_store_partial<FN, FM>(partials + (int64_t)(group * P + p) * (BM * BN * 4) + wave_off, e.lane, acc);
+      int* flag = &flags[(group * P + p) * NW + e.wave];
+      if (more) {
+        __syncthreads();  // every wave done reading the ring
+        int nm0, nn0;
+        tile_origin(tb + nt, tiles_m, tiles_n, BM, BN, nm0, nn0);
+        e.set_tile(act, wq, M, K, nblocks, kblocks, nm0, nn0);
+        e.prologue(nk0, nk1 - nk0);
+        prefetched = true;
+        pending = flag;
+      } else {
+        wait_vmcnt<0>();
+        if (e.lane == 0) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } else {
+      if (k0 > 0) {
+        // Lower tickets qf .. p-1 hold the tile's earlier k-blocks; ticket q's
+        // range starts at sk_iters * q / psk.
+        const int tstart = (t - dp) * kblocks;
+        int qf = p - 1;
+        while (sk_iters * qf / psk > tstart) --qf;
+        sk_wait_flags(&flags[(group * P + qf) * NW + e.wave], NW, p - qf, e.lane);
+        for (int q = qf; q < p; ++q)
+          sk_add_partial<FN, FM>(partials + (int64_t)(group * P + q) * (BM * BN * 4) + wave_off, e.lane, acc);
+      }
+      __syncthreads();  // ring -> epilogue staging
+      epilogue<ODT, E::TM, E::TN, E::SHIFT>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M, N,
+                                            xscales, wscales, bias, out);
+      __syncthreads();  // staging -> next item's DMA
+    }
+    t = nt;
+    k0 = nk0;
+    k1 = nk1;
+    have = more;
+  }
+
+  // The last workgroup of the group to finish rearms the ticket counters.
+  if (threadIdx.x == 0) {
+    if (atomicAdd(&ctl[kXcds + group], 1) == P - 1) {
+      __hip_atomic_store(&ctl[group], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ctl[kXcds + group], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// ---- host side: plan choice, stream-K workspace, launches
 
 struct Tile {
   int bm, bn, wm, wn;
 };
+
+struct Plan {
+  Tile t;
+  bool sk;        // stream-K kernel (else one workgroup per tile)
+  int grid;       // stream-K grid size (multiple of 8)
+  int min_iters;  // shortest stream-K range, in k-blocks
+};
+
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Candidate tiles with the relative MFMA efficiency each sustains in steady
+// state on MI355X (256x256 moves half the L2 bytes per MFMA of 128x128 but
+// runs one workgroup per CU; 128x128 fits two per CU).  `sk` marks the tiles
+// the stream-K kernel runs well: the 256x256 one spills registers there and
+// 128x128 pieces are too short.
+struct Cand {
+  Tile t;
+  int per_cu;
+  double eff;
+  bool sk;
+};
+constexpr Cand kCands[4] = {{{256, 256, 2, 4}, 1, 1.0, false},
+                            {{128, 256, 2, 4}, 1, 0.85, true},
+                            {{256, 128, 4, 2}, 1, 0.8, true},
+                            {{128, 128, 2, 2}, 2, 0.8, false}};
+// Fixed cost of the stream-K fix-up (ticket, partial store and reload, the
+// extra pipeline ramp of each piece, the idle tail while owners wait), in
+// units of one 256x256 k-block; fitted to M = 512 .. 4608 FLUX shapes.
+constexpr double kSkFixupBlocks = 10.0;
+constexpr int kSkMinIters = 4;
+
+// Time of one k-block of the candidate's tile on a CU, in units of a 256x256
+// k-block at full efficiency.
+double block_cost(const Cand& c) { return (double)c.t.bm * c.t.bn / 65536.0 / c.eff; }
+
+// Modelled run time of the busiest CU, in units of one 256x256 k-block.  With
+// per_cu workgroups resident on a CU they share it, so a CU's load counts in
+// steps of 1/per_cu of a tile.
+double dp_time(const Cand& c, int64_t tiles, int64_t kb, int cus) {
+  const int64_t steps = (tiles * c.per_cu + cus - 1) / cus;  // ceil(tiles per CU * per_cu)
+  return (double)steps / c.per_cu * (double)kb * block_cost(c);
+}
+
+double sk_time(const Cand& c, int64_t tiles, int64_t kb, int cus, int min_iters) {
+  const int64_t P = (int64_t)cus * c.per_cu / kXcds;
+  if (P < 1) return 1e300;
+  const int64_t tx = (tiles + kXcds - 1) / kXcds;
+  const int64_t rounds = tx / P, rem = tx % P;
+  const int64_t dp = rem == 0 ? tx : (rounds > 0 ? (rounds - 1) * P : 0);
+  const int64_t iters = (tx - dp) * kb;
+  const int64_t psk = std::min<int64_t>(P, std::max<int64_t>(1, iters / min_iters));
+  const double per = (double)(dp / P) * kb + (double)((iters + psk - 1) / psk);
+  return (per * c.per_cu * block_cost(c)) + (iters > 0 ? kSkFixupBlocks : 0.0);
+}
+
+// Pick the tile and kernel with the least modelled time.  Overrides for
+// tuning sweeps and tests: CONVROT_GEMM_TILE=BMxBN[wWMxWN] forces the tile,
+// CONVROT_GEMM_SK=0|1 forces the kernel kind, CONVROT_GEMM_SK_MIN sets the
+// shortest stream-K range.
+Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_sk) {
+  const int cus = device_cus();
+  const int64_t kb = (K + 127) / 128;
+  int min_iters = kSkMinIters;
+  if (const char* env = getenv("CONVROT_GEMM_SK_MIN")) min_iters = std::max(1, atoi(env));
+  int force_sk = -1;
+  if (const char* env = getenv("CONVROT_GEMM_SK")) force_sk = atoi(env) != 0;
+  if (!allow_sk) force_sk = 0;
+
+  const Tile* forced = nullptr;
+  Tile ft{};
+  if (const char* env = getenv("CONVROT_GEMM_TILE")) {
+    int bm = 0, bn = 0, wm = 2, wn = 2;
+    if (sscanf(env, "%dx%dw%dx%d", &bm, &bn, &wm, &wn) >= 2) {
+      ft = {bm, bn, wm, wn};
+      forced = &ft;
+    }
+  }
+  Plan best{{128, 128, 2, 2}, false, 0, min_iters};
+  double best_time = 1e300;
+  for (const Cand& c : kCands) {
+    const bool match = forced && c.t.bm == forced->bm && c.t.bn == forced->bn && c.t.wm == forced->wm &&
+                       c.t.wn == forced->wn;
+    if (forced && !match) continue;
+    const int64_t tiles = ((M + c.t.bm - 1) / c.t.bm) * ((N + c.t.bn - 1) / c.t.bn);
+    const double td = dp_time(c, tiles, kb, cus);
+    const double ts = sk_time(c, tiles, kb, cus, min_iters);
+    const int grid = std::min(kSkMaxGrid, cus * c.per_cu) / kXcds * kXcds;
+    const bool sk = grid >= kXcds && (force_sk == 1 || (force_sk == -1 && c.sk && ts < td));
+    const double tt = sk ? ts : td;
+    if (tt < best_time * (1.0 - 1e-9)) {
+      best_time = tt;
+      best = {c.t, sk, grid, min_iters};
+    }
+  }
+  if (forced && best_time == 1e300) best = {*forced, false, 0, min_iters};  // a tile only the register path has
+  return best;
+}
+
+// Stream-K workspace, one per (device, stream): launches on one stream are
+// ordered and leave the control words zeroed, so they share it.
+struct SkBuffer {
+  int dev;
+  hipStream_t stream;
+  uint8_t* ptr;
+  size_t bytes;
+};
+std::mutex g_sk_mu;
+std::vector<SkBuffer> g_sk_buffers;
+
+// Returns nullptr (and the caller runs the data-parallel kernel) when the
+// buffer cannot be made: allocation failure, or a stream under graph capture
+// that has no buffer yet.
+uint8_t* sk_workspace(hipStream_t stream, size_t bytes) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_sk_mu);
+  SkBuffer* slot = nullptr;
+  for (SkBuffer& b : g_sk_buffers)
+    if (b.dev == dev && b.stream == stream) slot = &b;
+  if (slot && slot->bytes >= bytes) return slot->ptr;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+  if (slot) {  // grow: earlier launches on this stream may still use the old buffer
+    if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+    (void)hipFree(slot->ptr);
+    slot->ptr = nullptr;
+    slot->bytes = 0;
+  } else {
+    g_sk_buffers.push_back({dev, stream, nullptr, 0});
+    slot = &g_sk_buffers.back();
+  }
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (hipMemsetAsync(p, 0, (size_t)kSkPartialOffset, stream) != hipSuccess || hipStreamSynchronize(stream) != hipSuccess) {
+    (void)hipFree(p);
+    return nullptr;
+  }
+  slot->ptr = (uint8_t*)p;
+  slot->bytes = bytes;
+  return slot->ptr;
+}
+
+// Sized for the largest partial set any candidate can need, so that one
+// allocation per (device, stream) serves every shape.
+size_t sk_workspace_bytes() {
+  const int cus = device_cus();
+  size_t most = 0;
+  for (const Cand& c : kCands) {
+    const size_t grid = (size_t)(std::min(kSkMaxGrid, cus * c.per_cu) / kXcds * kXcds);
+    most = std::max(most, grid * (size_t)c.t.bm * (size_t)c.t.bn * 4);
+  }
+  return (size_t)kSkPartialOffset + most;
+}
 
 template <int BM, int BN, int WM, int WN, bool APACK, int ODT>
 hipError_t launch_tile(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
@@ -519,44 +1030,23 @@ hipError_t launch_tile(const void* act, const float* xs, const uint8_t* wq, cons
   return hipGetLastError();
 }
 
-// Tile choice: maximise (busy fraction of the last round of workgroups) x
-// (measured per-tile efficiency of the tile).  256x256 moves half the L2 bytes
-// per MFMA of 128x128 but runs one workgroup per CU; 128x128 fits two per CU.
-// CONVROT_GEMM_TILE=BMxBN[wWMxWN] overrides (tuning sweeps).
-Tile choose_tile(int64_t M, int64_t N) {
-  if (const char* env = getenv("CONVROT_GEMM_TILE")) {
-    int bm = 0, bn = 0, wm = 2, wn = 2;
-    if (sscanf(env, "%dx%dw%dx%d", &bm, &bn, &wm, &wn) >= 2) return {bm, bn, wm, wn};
-  }
-  struct Cand {
-    Tile t;
-    int per_cu;
-    double eff;
-  };
-  const Cand cands[4] = {{{256, 256, 2, 4}, 1, 1.0}, {{128, 256, 2, 4}, 1, 0.85}, {{256, 128, 4, 2}, 1, 0.8},
-                         {{128, 128, 2, 2}, 2, 0.8}};
-  Tile best = {128, 128, 2, 2};
-  double best_score = -1.0;
-  for (const Cand& c : cands) {
-    const int64_t tiles = ((M + c.t.bm - 1) / c.t.bm) * ((N + c.t.bn - 1) / c.t.bn);
-    const int64_t slots = 256 * (int64_t)c.per_cu;
-    const double rounds = (double)tiles / (double)slots;
-    const double fill = rounds / (double)((tiles + slots - 1) / slots);
-    const double score = fill * c.eff;
-    if (score > best_score + 1e-9) {
-      best_score = score;
-      best = c.t;
-    }
-  }
-  return best;
-}
-
 template <int BM, int BN, int WM, int WN, int ODT>
-hipError_t launch_dma(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
-                      int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+hipError_t launch_dma(const Plan& plan, const void* act, const float* xs, const uint8_t* wq, const float* ws,
+                      const float* bias, int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
   const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
-  hipLaunchKernelGGL((w4a4_gemm_dma_kernel<BM, BN, WM, WN, 3, (BM * BN < 65536), ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
+  // Double-buffered fragments except on the 8-wave 256x256 tile, whose
+  // 128-register accumulator leaves no room for a second set.
+  constexpr int kPP = (BM == 256 && BN == 256) ? kSingle : kPingPong;
+  if (plan.sk) {
+    if (uint8_t* work = sk_workspace(stream, sk_workspace_bytes())) {
+      hipLaunchKernelGGL((w4a4_gemm_sk_kernel<BM, BN, WM, WN, kPP, ODT>), dim3((unsigned)plan.grid),
+                         dim3(WM * WN * 64), 0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N,
+                         (int)K, nblocks, kblocks, tm, tn, work, plan.min_iters);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((w4a4_gemm_dma_kernel<BM, BN, WM, WN, kPP, ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
                      0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks,
                      tm, tn);
   return hipGetLastError();
@@ -565,18 +1055,18 @@ hipError_t launch_dma(const void* act, const float* xs, const uint8_t* wq, const
 template <bool APACK, int ODT>
 hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
                     int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
-  const Tile t = choose_tile(M, N);
-  if constexpr (!APACK) {
-    if (!getenv("CONVROT_GEMM_NO_DMA")) {
+  const bool dma = !APACK && !getenv("CONVROT_GEMM_NO_DMA");
+  const Plan plan = choose_plan(M, N, K, dma);
+  const Tile t = plan.t;
+  if (dma) {
 #define CONVROT_DMA(BM_, BN_, WM_, WN_)                        \
   if (t.bm == BM_ && t.bn == BN_ && t.wm == WM_ && t.wn == WN_) \
-    return launch_dma<BM_, BN_, WM_, WN_, ODT>(act, xs, wq, ws, bias, M, N, K, out, stream);
-      CONVROT_DMA(256, 256, 2, 4)
-      CONVROT_DMA(256, 128, 4, 2)
-      CONVROT_DMA(128, 256, 2, 4)
-      CONVROT_DMA(128, 128, 2, 2)
+    return launch_dma<BM_, BN_, WM_, WN_, ODT>(plan, act, xs, wq, ws, bias, M, N, K, out, stream);
+    CONVROT_DMA(256, 256, 2, 4)
+    CONVROT_DMA(256, 128, 4, 2)
+    CONVROT_DMA(128, 256, 2, 4)
+    CONVROT_DMA(128, 128, 2, 2)
 #undef CONVROT_DMA
-    }
   }
 #define CONVROT_TILE(BM_, BN_, WM_, WN_)                    \
   if (t.bm == BM_ && t.bn == BN_ && t.wm == WM_ && t.wn == WN_) \

@@ -24,6 +24,8 @@
 //    reciprocal, which is exact for bf16 operands (r/scale can never lie
 //    within 2^-16.8 of a bf16 rounding midpoint, so an error below 2^-23
 //    cannot change the rounded ratio).  f16/f32 inputs use a true division.
+#include <stdlib.h>
+
 #include "convrot_device.h"
 #include "convrot_launch.h"
 
@@ -334,9 +336,27 @@ hipError_t launch_prep_s(int s, int ni, int mode, const void* x, void* out, floa
 }  // namespace
 
 // Pick (iterations per wave, waves per row) so that 1024*NI*W covers K with
-// the fewest idle 1024-feature blocks; NI in {3, 4, 1}, W <= 16.
-bool prep_plan(int64_t K, int* ni_out, int* waves_out) {
+// the fewest idle 1024-feature blocks; NI in {3, 4, 1}, W <= 16.  Few rows
+// (M <= 2048) take one iteration per wave and more waves per row instead, so
+// that enough waves are in flight to cover the load latency.
+bool prep_plan(int64_t rows, int64_t K, int* ni_out, int* waves_out) {
   const int64_t blocks = (K + 1023) / 1024;
+  if (const char* env = getenv("CONVROT_PREP_NI")) {  // tuning sweeps: force iterations per wave
+    const int ni = atoi(env);
+    if (ni == 1 || ni == 3 || ni == 4) {
+      const int64_t w = (blocks + ni - 1) / ni;
+      if (w <= kMaxWaves) {
+        *ni_out = ni;
+        *waves_out = (int)w;
+        return true;
+      }
+    }
+  }
+  if (rows <= 2048 && blocks <= kMaxWaves) {
+    *ni_out = 1;
+    *waves_out = (int)blocks;
+    return true;
+  }
   int best_ni = 0, best_w = 0;
   int64_t best_idle = -1;
   const int cand[3] = {3, 4, 1};
@@ -360,7 +380,7 @@ bool prep_plan(int64_t K, int* ni_out, int* waves_out) {
 hipError_t launch_prep(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode, void* out,
                        float* scales, hipStream_t stream) {
   int ni = 0, waves = 0;
-  if (!prep_plan(K, &ni, &waves)) return hipErrorInvalidValue;
+  if (!prep_plan(rows, K, &ni, &waves)) return hipErrorInvalidValue;
   if (rows == 0) return hipSuccess;
   switch (dtype) {
     case kF32: return launch_prep_s<kF32>(log4g, ni, mode, x, out, scales, rows, (int)K, waves, stream);

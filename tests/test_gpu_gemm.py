@@ -106,11 +106,23 @@ def test_odd_shapes_bf16(orc, dev, seed, M, K, N):
         _assert_exact(got, expected, f"{name} seed {seed}")
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128"])
+# Tiles the automatic choice picks (BMxBN, waves WMxWN), plus 2x2-wave register-staged
+# variants that are only reached through the override.
+_TILES = ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2", "256x256w2x2", "256x128w2x2",
+          "128x256w2x2", "256x256w4x2"]
+
+
+@pytest.mark.parametrize("no_dma", [False, True], ids=["dma", "regstaged"])
+@pytest.mark.parametrize("tile", _TILES)
 @pytest.mark.parametrize("seed,M,K,N", [(41, 300, 384, 530), (42, 17, 2688, 46), (43, 520, 256, 264)])
-def test_every_tile_config(orc, dev, monkeypatch, tile, seed, M, K, N):
-    """Each GEMM tile variant (forced through CONVROT_GEMM_TILE) on ragged M/N/K tails."""
+def test_every_tile_config(orc, dev, monkeypatch, tile, no_dma, seed, M, K, N):
+    """Each GEMM tile variant (forced through CONVROT_GEMM_TILE; CONVROT_GEMM_NO_DMA selects the
+    register-staged int8 kernel) on ragged M/N/K tails."""
     monkeypatch.setenv("CONVROT_GEMM_TILE", tile)
+    if no_dma:
+        monkeypatch.setenv("CONVROT_GEMM_NO_DMA", "1")
+    else:
+        monkeypatch.delenv("CONVROT_GEMM_NO_DMA", raising=False)
     rng = np.random.default_rng(seed)
     a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
     w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
@@ -120,6 +132,38 @@ def test_every_tile_config(orc, dev, monkeypatch, tile, seed, M, K, N):
     expected = orc.w4a4_matmul_codes(a, w, xs, ws, b, "bfloat16")
     for got, name in zip(_run_both(orc, dev, a, w, xs, ws, b, "bfloat16"), ("packed", "int8")):
         _assert_exact(got, expected, f"{name} tile {tile}")
+
+
+@pytest.mark.parametrize("tile", ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2"])
+@pytest.mark.parametrize(
+    "seed,M,K,N,sk_min",
+    [(51, 300, 2688, 530, 1),    # tiles split into up to 21 one-k-block pieces
+     (52, 37, 64, 46, 1),        # a single k-block: pieces are whole tiles
+     (53, 2100, 384, 16384, 4)],  # whole-tile rounds followed by a stream-K remainder
+)
+def test_stream_k(orc, dev, monkeypatch, tile, seed, M, K, N, sk_min):
+    """Stream-K kernel forced on: partial tiles summed across workgroups must give the
+    single-pass result bit for bit; two launches in a row check the re-armed counters."""
+    api = _api()
+    monkeypatch.setenv("CONVROT_GEMM_TILE", tile)
+    monkeypatch.setenv("CONVROT_GEMM_SK", "1")
+    monkeypatch.setenv("CONVROT_GEMM_SK_MIN", str(sk_min))
+    monkeypatch.delenv("CONVROT_GEMM_NO_DMA", raising=False)
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    b = rng.normal(size=(N,)).astype(np.float32)
+    rows = np.arange(M) if M * N <= 200_000 else np.sort(rng.choice(M, size=64, replace=False))
+    expected = orc.w4a4_matmul_codes(a[rows], w, xs[rows], ws, b, "bfloat16")
+    wq = _dev_u8(orc.codes_to_cdna4(w), dev)
+    a8 = torch.from_numpy(a).to(dev)
+    args = (torch.from_numpy(xs).to(dev), torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev))
+    for call in range(2):
+        out = api.hip_w4a4_int8_matmul(a8, wq, *args, output_dtype=torch.bfloat16, out_features=N)
+        torch.cuda.synchronize()
+        _assert_exact(from_dev(out)[rows], expected, f"tile {tile} call {call}")
 
 
 def test_kn_layout_entry_matches(orc, dev):
