@@ -961,7 +961,10 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_sk) {
 }
 
 // Stream-K workspace, one per (device, stream): launches on one stream are
-// ordered and leave the control words zeroed, so they share it.
+// ordered and leave the control words zeroed, so they share it.  It is the
+// library's only allocation (32 MiB for the 8-wave tiles on 256 CUs), made on
+// the first stream-K launch of a stream and kept for the process;
+// CONVROT_GEMM_SK=0 keeps every launch data-parallel and allocation-free.
 struct SkBuffer {
   int dev;
   hipStream_t stream;
@@ -1007,16 +1010,10 @@ uint8_t* sk_workspace(hipStream_t stream, size_t bytes) {
   return slot->ptr;
 }
 
-// Sized for the largest partial set any candidate can need, so that one
-// allocation per (device, stream) serves every shape.
-size_t sk_workspace_bytes() {
-  const int cus = device_cus();
-  size_t most = 0;
-  for (const Cand& c : kCands) {
-    const size_t grid = (size_t)(std::min(kSkMaxGrid, cus * c.per_cu) / kXcds * kXcds);
-    most = std::max(most, grid * (size_t)c.t.bm * (size_t)c.t.bn * 4);
-  }
-  return (size_t)kSkPartialOffset + most;
+// Bytes a stream-K launch of the plan needs: the control block plus one int32
+// partial tile per workgroup.  The buffer of a (device, stream) only grows.
+size_t sk_workspace_bytes(const Plan& plan) {
+  return (size_t)kSkPartialOffset + (size_t)plan.grid * (size_t)plan.t.bm * (size_t)plan.t.bn * 4;
 }
 
 template <int BM, int BN, int WM, int WN, bool APACK, int ODT>
@@ -1039,7 +1036,7 @@ hipError_t launch_dma(const Plan& plan, const void* act, const float* xs, const 
   // 128-register accumulator leaves no room for a second set.
   constexpr int kPP = (BM == 256 && BN == 256) ? kSingle : kPingPong;
   if (plan.sk) {
-    if (uint8_t* work = sk_workspace(stream, sk_workspace_bytes())) {
+    if (uint8_t* work = sk_workspace(stream, sk_workspace_bytes(plan))) {
       hipLaunchKernelGGL((w4a4_gemm_sk_kernel<BM, BN, WM, WN, kPP, ODT>), dim3((unsigned)plan.grid),
                          dim3(WM * WN * 64), 0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N,
                          (int)K, nblocks, kblocks, tm, tn, work, plan.min_iters);

@@ -134,21 +134,26 @@ __device__ __forceinline__ void rotate16(float (&v)[16], float* region, int p) {
   if constexpr (S >= 5) exchange_and_stage<DT, S, 4>(v, region, p);
 }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16 consecutive elements at byte `off` of the row's buffer (16-byte loads);
+// offsets at or beyond the row's end read as zero (buffer range check).
 template <int DT>
-__device__ __forceinline__ void load16(const void* x, int64_t idx, float (&v)[16]) {
+__device__ __forceinline__ void load16(__amdgpu_buffer_rsrc_t row, uint32_t off, float (&v)[16]) {
   if constexpr (DT == kF32) {
-    const float4* p = (const float4*)((const float*)x + idx);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float4 t = p[q];
-      v[4 * q] = t.x;
-      v[4 * q + 1] = t.y;
-      v[4 * q + 2] = t.z;
-      v[4 * q + 3] = t.w;
+      const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(row, (int)(off + 16 * q), 0, 0);
+      // __uint_as_float, not __builtin_bit_cast: this compiler bit_casts a
+      // vector-element operand from element 0's storage
+      v[4 * q] = __uint_as_float(t.x);
+      v[4 * q + 1] = __uint_as_float(t.y);
+      v[4 * q + 2] = __uint_as_float(t.z);
+      v[4 * q + 3] = __uint_as_float(t.w);
     }
   } else {
-    const uint4* p = (const uint4*)((const uint16_t*)x + idx);
-    const uint4 a = p[0], b = p[1];
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(row, (int)off, 0, 0);
+    const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(row, (int)(off + 16), 0, 0);
     const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
@@ -163,6 +168,30 @@ __device__ __forceinline__ void load16(const void* x, int64_t idx, float (&v)[16
       }
     }
   }
+}
+
+// max(m, |a|, |b|) in one v_max3_f32 with |.| source modifiers (m >= 0).  As
+// C++ the compiler inserts canonicalizing moves and separate abs masks.
+__device__ __forceinline__ float absmax3(float m, float a, float b) {
+  float r;
+  asm("v_max3_f32 %0, |%1|, |%2|, %3" : "=v"(r) : "v"(a), "v"(b), "v"(m));
+  return r;
+}
+
+// Maximum over the wave of a non-negative float (bit patterns of non-negative
+// floats order like unsigned integers): DPP quad swaps and row mirrors leave
+// every lane of a 16-lane row with the row maximum, then four readlanes.
+__device__ __forceinline__ float wave_max_nonneg(float x) {
+  uint32_t v = __builtin_bit_cast(uint32_t, x);
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));   // quad_perm [1,0,3,2]
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));   // quad_perm [2,3,0,1]
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, true));  // row_half_mirror
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, true));  // row_mirror
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return __builtin_bit_cast(float, max(max(r0, r1), max(r2, r3)));
 }
 
 // Signed code in [-7, 7] of a ratio: clamp, then round half to even by adding
@@ -204,6 +233,9 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
   const int nwaves = blockDim.x >> 6;
   const int64_t row = blockIdx.x;
   const int chunks = K >> 4;
+  constexpr int kEsize = DT == kF32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t xrow = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const char*)x + row * K * kEsize), (short)0, K * kEsize, 0x00020000);
   float* region = lds + wave * kRegionFloats + (lane / LG) * (G + G / 4);
   const int p = lane % LG;
 
@@ -214,14 +246,8 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
   for (int it = 0; it < NI; ++it) {
     const int block = wave * NI + it;
     const int chunk = block * 64 + lane;
-    const bool active = chunk < chunks;
     float (&v)[16] = keep[it];
-    if (active) {
-      load16<DT>(x, row * K + (int64_t)chunk * 16, v);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = 0.0f;
-    }
+    load16<DT>(xrow, (uint32_t)chunk * (16u * kEsize), v);  // chunks past the row end read zeros
     rotate16<DT, S>(v, region, p);
     if constexpr (!kImplicitNorm && S > 0 && MODE != CONVROT_PREP_ROTATE) {
 #pragma unroll
@@ -229,15 +255,14 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
     }
     if constexpr (MODE != CONVROT_PREP_ROTATE) {
 #pragma unroll
-      for (int j = 0; j < 16; j += 2) amax = fmaxf(amax, fmaxf(fabsf(v[j]), fabsf(v[j + 1])));
+      for (int j = 0; j < 16; j += 2) amax = absmax3(amax, v[j], v[j + 1]);
     }
   }
 
   // ---- row scale (core.py:154-156)
   float inv = 0.0f, scale = 0.0f;
   if constexpr (MODE != CONVROT_PREP_ROTATE) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    amax = wave_max_nonneg(amax);
     if (nwaves > 1) {
       if (lane == 0) wave_max[wave] = amax;
       __syncthreads();

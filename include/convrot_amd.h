@@ -8,8 +8,10 @@
  * and argument meaning it takes over.
  *
  * Conventions
- *  - Every pointer is a device pointer the caller allocated (the library never
- *    allocates or frees); tensors are dense row-major unless stated.
+ *  - Every pointer is a device pointer the caller allocated; tensors are dense
+ *    row-major unless stated.  The library's only allocation is the stream-K
+ *    GEMM workspace (32 MiB per device and stream, made on the first
+ *    stream-K launch of that stream and kept; CONVROT_GEMM_SK=0 disables it).
  *  - `stream` is a hipStream_t passed as void* (NULL = the default stream).
  *    Work is enqueued asynchronously; nothing synchronizes the host.
  *  - Return value: CONVROT_OK or a nonzero status.  convrot_last_error()
