@@ -16,6 +16,8 @@ Prints ONE JSON line (the driver's contract).  Extra keys:
   cpu_baseline   the CPU oracle (C restatement, 1 thread) on a bounded row sample
   dense_bf16_control  torch bf16 linear (hipBLASLt) on the same shapes
   flux_m4608     config 3's 4608x3072->12288 G=256 complete-path figure
+  w4a16_config4  config 4 (W4A16, M in {1, 8, 32}): int4-weight GB/s of the GEMM and
+                 the complete path (rotation + GEMM), replayed from a HIP graph
 """
 
 from __future__ import annotations
@@ -39,6 +41,7 @@ HBM_PEAK_GBPS = 8000.0
 
 CONFIG2 = {"M": 1536, "G": 64, "shapes": [(3072, 9216), (3072, 3072), (3072, 12288), (12288, 3072)]}
 CONFIG3_MLP = {"M": 4608, "G": 256, "K": 3072, "N": 12288}
+CONFIG4 = {"G": 256, "Ms": (1, 8, 32), "shapes": [(3072, 12288), (12288, 3072)]}
 TRAFFIC_FILE = ROOT / "profiles" / "gemm_w4a4_flux_m1536_traffic.json"
 
 
@@ -216,6 +219,7 @@ def main() -> int:
         result["dense_bf16_control"]["convrot_speedup"] = round(
             result["dense_bf16_control"]["ms_per_step"] / ms_per_step, 3)
         result["flux_m4608"] = config3_figure(torch, core, nat, dev)
+        result["w4a16_config4"] = w4a16_figure(torch, core, nat, dev)
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(np, sets[0], M, G, args.cpu_rows, shapes)
@@ -284,6 +288,73 @@ def config3_figure(torch, core, nat, dev):
     tops = 2 * M * N * K / (us * 1e-6) / 1e12
     return {"shape": "4608x3072->12288 G=256", "us_per_linear": round(us, 2), "tops": round(tops, 2),
             "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2)}
+
+
+def w4a16_figure(torch, core, nat, dev):
+    """Config 4: W4A16 (rotation prep -> int4-weight GEMM with the scale/bias epilogue), G=256,
+    bf16, M in {1, 8, 32}.  A ~10 us launch is shorter than the host's launch interval, so the
+    launches are captured in a HIP graph and replayed; every replay's output is checked against
+    the eager one.  Weights cycle through > 512 MB so each launch streams its int4 weights from
+    HBM.  Headline bytes per GEMM launch: N*K/2 (int4 weights)."""
+    lib, stream_fn = nat.load(), nat.stream_of
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    G = CONFIG4["G"]
+    figures = []
+    for K, N in CONFIG4["shapes"]:
+        wbytes = N * K // 2
+        nsets = max(2, -(-600 * 2 ** 20 // wbytes))
+        weights = [torch.randint(0, 256, core.cdna4_shape(N, K), dtype=torch.uint8, device=dev, generator=gen)
+                   for _ in range(nsets)]
+        ws = torch.rand(N, generator=gen, device=dev) * 0.01
+        bias = torch.randn(N, generator=gen, device=dev) * 0.02
+        for M in CONFIG4["Ms"]:
+            x = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+            rot = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+            def prep():
+                nat.check(lib.convrot_prepare(nat.ptr(x), nat.DTYPE_BF16, M, K, G, nat.PREP_ROTATE, nat.ptr(rot),
+                                              None, stream_fn(dev)))
+
+            def gemm(i):
+                nat.check(lib.convrot_w4a16_gemm(nat.ptr(rot), nat.DTYPE_BF16, nat.ptr(weights[i]), nat.ptr(ws),
+                                                 nat.ptr(bias), M, N, K, nat.ptr(y), nat.DTYPE_BF16, stream_fn(dev)))
+
+            timings = {}
+            for name, with_prep in (("gemm", False), ("path", True)):
+                prep()
+                gemm(nsets - 1)
+                torch.cuda.synchronize()
+                ref = y.clone()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    for i in range(nsets):
+                        if with_prep:
+                            prep()
+                        gemm(i)
+                for _ in range(2):
+                    graph.replay()
+                    torch.cuda.synchronize()
+                    if not torch.equal(y, ref):
+                        raise RuntimeError("W4A16 graph replay differs from the eager result")
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                reps = 4
+                e0.record()
+                for _ in range(reps):
+                    graph.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                timings[name] = e0.elapsed_time(e1) * 1e3 / (reps * nsets)
+                del graph
+            gbps = wbytes / (timings["gemm"] * 1e-6) / 1e9
+            figures.append({"M": M, "K": K, "N": N, "gemm_us": round(timings["gemm"], 2),
+                            "path_us": round(timings["path"], 2), "int4_weight_GBps": round(gbps, 1),
+                            "pct_hbm": round(100 * gbps / HBM_PEAK_GBPS, 1)})
+        del weights
+    return {"what": "W4A16 GEMM (int4 weights N*K/2 bytes per launch) and complete path, G=256, bf16; "
+                    "HIP-graph replays, weights cycled through > 512 MB",
+            "shapes": figures}
 
 
 def cpu_baseline(np, layers, M, G, rows, shapes):

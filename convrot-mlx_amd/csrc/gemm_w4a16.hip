@@ -11,8 +11,14 @@
 // sums are exactly 16x those of unscaled codes.
 //
 // Work split: a workgroup owns NB consecutive 16-row weight tiles and a tile
-// of 16*FM tokens; its SPLIT waves stride over the 128-feature blocks of K and
-// their partial sums are reduced through LDS in a fixed order (deterministic).
+// of 16*FM tokens; its SPLIT waves take KPW consecutive 128-feature blocks of
+// K each (then every SPLIT*KPW) and their partial sums are reduced through
+// LDS in a fixed order (deterministic).  A wave issues every load of its KPW
+// blocks before the first MFMA: at these M the kernel streams the weights
+// from HBM, and the whole matrix has to be in flight at once to cover the
+// memory latency (18.9 MB for 3072x12288).
+#include <stdlib.h>
+
 #include "convrot_device.h"
 #include "convrot_launch.h"
 
@@ -49,8 +55,11 @@ __device__ __forceinline__ f32x4 mfma16(i32x4 a, i32x4 b, f32x4 c) {
                                                   0, 0);
 }
 
-template <int ADT, int ODT, int FM, int NB, int SPLIT>
-__global__ __launch_bounds__(SPLIT * 64) void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
+// Single token tile: four waves per SIMD (at most 128 VGPRs), so that the
+// whole grid's weight loads can be in flight at once.
+template <int ADT, int ODT, int FM, int NB, int SPLIT, int KPW>
+__global__ __launch_bounds__(SPLIT * 64) __attribute__((amdgpu_waves_per_eu(FM == 1 ? 4 : 1)))
+void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
                                                                 const uint8_t* __restrict__ wq,
                                                                 const float* __restrict__ wscales,
                                                                 const float* __restrict__ bias,
@@ -68,35 +77,52 @@ __global__ __launch_bounds__(SPLIT * 64) void w4a16_gemm_kernel(const uint16_t* 
 #pragma unroll
     for (int b = 0; b < FM; ++b) acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  for (int kb = wave; kb < kblocks; kb += SPLIT) {
-    // activation operands: lane (m = r, q) -> 8 values at features kb*128 + 32q + 8c
-    i32x4 aop[FM][4];
+  // Branch-free loads through buffer resources (the range check zero-fills
+  // past the end), so the compiler can wait for each block separately and the
+  // weight expansion of early blocks overlaps the later loads.  Weight tile
+  // rows past N read wrapped (valid) blocks; their outputs are never stored.
+  // Activation rows are based at m0 (32-bit offsets for any M).
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const int rows_valid = min(16 * FM, M - m0);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(act + (int64_t)m0 * K), (short)0, rows_valid * K * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(wq + (int64_t)nb0 * 1024), (short)0, (int)(((int64_t)kblocks * nblocks - nb0) * 1024), 0x00020000);
+  for (int kb0 = wave * KPW; kb0 < kblocks; kb0 += SPLIT * KPW) {
+    uint4 w[KPW][NB];
+    i32x4 aop[KPW][FM][4];  // lane (m = r, q) -> 8 values at features kb*128 + 32q + 8c
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-      const int m = m0 + fm * 16 + r;
+    for (int i = 0; i < KPW; ++i) {
+      const int kb = kb0 + i;  // blocks at or past kblocks read zeros
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int k = kb * 128 + 32 * q + 8 * c;
-        aop[fm][c] = (m < M && k < K) ? *(const i32x4*)(act + (int64_t)m * K + k) : (i32x4){0, 0, 0, 0};
+      for (int t = 0; t < NB; ++t) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+            rw, (int)(((uint32_t)kb * (uint32_t)nblocks + (uint32_t)t) * 1024u + (uint32_t)lane * 16u), 0, 0);
+        w[i][t] = make_uint4(v.x, v.y, v.z, v.w);
       }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int k = kb * 128 + 32 * q + 8 * c;
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+              ra, (int)((uint32_t)(fm * 16 + r) * (uint32_t)K * 2u + (uint32_t)k * 2u), 0, 0);
+          // a ragged K end would read the next row: zero it (K is a multiple of 8)
+          aop[i][fm][c] = k < K ? (i32x4){(int)v.x, (int)v.y, (int)v.z, (int)v.w} : (i32x4){0, 0, 0, 0};
+        }
     }
-    uint4 w[NB];
 #pragma unroll
-    for (int t = 0; t < NB; ++t) {
-      const int nb = nb0 + t;
-      w[t] = nb < nblocks ? *(const uint4*)(wq + ((int64_t)kb * nblocks + nb) * 1024 + lane * 16)
-                          : make_uint4(0, 0, 0, 0);
-    }
+    for (int i = 0; i < KPW; ++i)
 #pragma unroll
-    for (int t = 0; t < NB; ++t) {
-      const uint32_t wd[4] = {w[t].x, w[t].y, w[t].z, w[t].w};
+      for (int t = 0; t < NB; ++t) {
+        const uint32_t wd[4] = {w[i][t].x, w[i][t].y, w[i][t].z, w[i][t].w};
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const i32x4 bop = expand8<ADT>(wd[c]);
+        for (int c = 0; c < 4; ++c) {
+          const i32x4 bop = expand8<ADT>(wd[c]);
 #pragma unroll
-        for (int fm = 0; fm < FM; ++fm) acc[t][fm] = mfma16<ADT>(bop, aop[fm][c], acc[t][fm]);
+          for (int fm = 0; fm < FM; ++fm) acc[t][fm] = mfma16<ADT>(bop, aop[i][fm][c], acc[t][fm]);
+        }
       }
-    }
   }
 
   if constexpr (SPLIT > 1) {
@@ -146,31 +172,38 @@ __global__ __launch_bounds__(SPLIT * 64) void w4a16_gemm_kernel(const uint16_t* 
   }
 }
 
-template <int ADT, int ODT, int FM, int NB, int SPLIT>
+template <int ADT, int ODT, int FM, int NB, int SPLIT, int KPW>
 hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M, int64_t N,
                     int64_t K, void* out, hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
   dim3 grid((unsigned)((nblocks + NB - 1) / NB), (unsigned)((M + 16 * FM - 1) / (16 * FM)));
-  hipLaunchKernelGGL((w4a16_gemm_kernel<ADT, ODT, FM, NB, SPLIT>), grid, dim3(64 * SPLIT), 0, stream,
+  hipLaunchKernelGGL((w4a16_gemm_kernel<ADT, ODT, FM, NB, SPLIT, KPW>), grid, dim3(64 * SPLIT), 0, stream,
                      (const uint16_t*)act, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks);
   return hipGetLastError();
 }
 
+// Configurations (FM token tiles, NB weight tiles, SPLIT waves, KPW blocks
+// per wave), measured on the config-4 shapes (M = 1, 8, 32; 3072->12288 and
+// 12288->3072):
+//   A (1,2,8,3)  many weight tiles, or 16 < M <= 32 (two token tiles)
+//   B (1,1,16,4) few weight tiles and long K, M <= 16
+//   F (4,2,4,2)  M > 32
+// At M = 1 both stream the 18.9 MB weight matrix in ~8 us (~2.3 TB/s), where
+// a plain 19 MB device copy takes ~10 us; the rest is weight expansion
+// (~2 VALU ops per code) and the launch/tail.  CONVROT_W4A16_CFG=A|B|F
+// overrides (tuning sweeps).
 template <int ADT, int ODT>
 hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
                         int64_t N, int64_t K, void* out, hipStream_t stream) {
-  const int64_t kblocks = (K + 127) / 128;
-  // split K across waves when there are few weight tiles per token tile
-  const bool deep = kblocks >= 32;
-  if (M <= 16) {
-    return deep ? launch_t<ADT, ODT, 1, 2, 8>(act, wq, ws, bias, M, N, K, out, stream)
-                : launch_t<ADT, ODT, 1, 2, 4>(act, wq, ws, bias, M, N, K, out, stream);
+  const int64_t nblocks = (N + 15) / 16;
+  char cfg = M > 32 ? 'F' : (M <= 16 && nblocks < 512 ? 'B' : 'A');
+  if (const char* env = getenv("CONVROT_W4A16_CFG"))
+    if (env[0] == 'A' || env[0] == 'B' || env[0] == 'F') cfg = env[0];
+  switch (cfg) {
+    case 'A': return launch_t<ADT, ODT, 1, 2, 8, 3>(act, wq, ws, bias, M, N, K, out, stream);
+    case 'B': return launch_t<ADT, ODT, 1, 1, 16, 4>(act, wq, ws, bias, M, N, K, out, stream);
+    default: return launch_t<ADT, ODT, 4, 2, 4, 2>(act, wq, ws, bias, M, N, K, out, stream);
   }
-  if (M <= 32) {
-    return deep ? launch_t<ADT, ODT, 2, 2, 8>(act, wq, ws, bias, M, N, K, out, stream)
-                : launch_t<ADT, ODT, 2, 2, 4>(act, wq, ws, bias, M, N, K, out, stream);
-  }
-  return launch_t<ADT, ODT, 4, 2, 4>(act, wq, ws, bias, M, N, K, out, stream);
 }
 
 template <int ADT>

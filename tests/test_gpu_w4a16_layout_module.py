@@ -67,6 +67,20 @@ def test_w4a16_config4(orc, dev, M, K, N):
     _w4a16_check(orc, dev, act, "bfloat16", w, ws, b, "bfloat16")
 
 
+@pytest.mark.parametrize("cfg", ["A", "B", "F"])
+@pytest.mark.parametrize("M,K,N", [(17, 96, 46), (37, 2688, 530), (1, 4000, 33), (5, 12288, 3072)])
+def test_w4a16_every_split(orc, dev, monkeypatch, cfg, M, K, N):
+    """Each W4A16 work split (forced through CONVROT_W4A16_CFG) on ragged M/N and on K that is
+    not a multiple of the 128-feature block (the tail features must read as zero)."""
+    monkeypatch.setenv("CONVROT_W4A16_CFG", cfg)
+    rng = np.random.default_rng(M * 131 + K + N)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.01, size=(N,)).astype(np.float32)
+    b = rng.normal(0, 0.02, size=(N,)).astype(np.float32)
+    act = normal_input(M + K + N, (M, K), "bfloat16", orc)
+    _w4a16_check(orc, dev, act, "bfloat16", w, ws, b, "bfloat16")
+
+
 # ---------------------------------------------------------------- layouts
 
 def test_pack_literal_bytes(orc, dev):
