@@ -18,6 +18,9 @@ Prints ONE JSON line (the driver's contract).  Extra keys:
   flux_m4608     config 3's 4608x3072->12288 G=256 complete-path figure
   w4a16_config4  config 4 (W4A16, M in {1, 8, 32}): int4-weight GB/s of the GEMM and
                  the complete path (rotation + GEMM), replayed from a HIP graph
+  flux_dit_config5  config 5: one step of a random-init FLUX.1-dev DiT (1536 tokens),
+                 dense bf16 vs every Linear as W4A4 ConvRotLinear G=64 -- eager and
+                 HIP-graph step latency, relative L2 / cosine deviation
 """
 
 from __future__ import annotations
@@ -53,7 +56,9 @@ def parse():
     ap.add_argument("--sets", type=int, default=3, help="buffer sets cycled to defeat the Infinity Cache")
     ap.add_argument("--cpu-rows", type=int, default=96, help="rows per linear in the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-extras", action="store_true", help="skip the dense control and the config-3 figure")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the dense control and the config-3/4/5 figures")
+    ap.add_argument("--no-config5", action="store_true", help="skip the FLUX DiT step (config 5)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run one 256 MiB device copy first (counter calibration for rocprofv3 --pmc)")
     return ap.parse_args()
@@ -186,7 +191,7 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) activations with 0.5% x20 channels, N(0,0.02^2) weights with 1% x10 "
                 "input channels; random init)",
         "config": {
-            "workload": "BASELINE configs[1]: FLUX double-block W4A4 linears, M=1536, group 64, bf16, with bias: "
+            "workload": "benchmark configs[1]: FLUX double-block W4A4 linears, M=1536, group 64, bf16, with bias: "
                         "3072->9216, 3072->3072, 3072->12288, 12288->3072; complete path prep+GEMM+epilogue",
             "M": M, "group_size": G, "shapes_KxN": shapes, "buffer_sets": args.sets,
             "pct_int8_peak": round(100.0 * tops / INT8_PEAK_TOPS, 2),
@@ -220,6 +225,12 @@ def main() -> int:
             result["dense_bf16_control"]["ms_per_step"] / ms_per_step, 3)
         result["flux_m4608"] = config3_figure(torch, core, nat, dev)
         result["w4a16_config4"] = w4a16_figure(torch, core, nat, dev)
+        if not args.no_config5:
+            from examples.flux1_dev.dit import config5_figure
+
+            torch.cuda.empty_cache()
+            result["flux_dit_config5"] = config5_figure(steps=5)
+            torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(np, sets[0], M, G, args.cpu_rows, shapes)

@@ -1,0 +1,383 @@
+"""Random-init FLUX.1-dev-architecture DiT in torch, and the config-5 measurement.
+
+The reference runs FLUX.1 Dev through Apple's MLX example runtime and swaps its
+Linears for ConvRotLinear (/root/reference/examples/flux1_dev/adapter.py:45-70,
+load_flow_convrot :73-106).  That runtime, the checkpoints and diffusers are
+not available here, so this module restates the public FLUX.1 architecture
+(the published "flux-dev" parameters: 19 double-stream and 38 single-stream
+blocks, hidden 3072, 24 heads of 128, MLP ratio 4, 3-axis RoPE (16, 56, 56),
+guidance embedding) with random weights, enough to time one denoising step and
+measure how far the W4A4 model drifts from the dense one (benchmark config 5).
+
+On the GPU attention is torch's fused flash / memory-efficient SDPA kernel in
+bf16 (the unfused math backend, which issues batched bf16 products on transposed
+views, is excluded); on the CPU it is written out in float32.  Everything else
+runs in bf16.
+
+    python examples/flux1_dev/dit.py            # prints one JSON line
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import sys
+import time
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+ROOT = Path(__file__).resolve().parents[2]
+if str(ROOT / "convrot-mlx_amd") not in sys.path:
+    sys.path.insert(0, str(ROOT / "convrot-mlx_amd"))
+
+
+@dataclass
+class FluxParams:
+    in_channels: int = 64
+    vec_in_dim: int = 768
+    context_in_dim: int = 4096
+    hidden_size: int = 3072
+    mlp_ratio: float = 4.0
+    num_heads: int = 24
+    depth: int = 19
+    depth_single_blocks: int = 38
+    axes_dim: tuple = field(default=(16, 56, 56))
+    theta: int = 10000
+    qkv_bias: bool = True
+    guidance_embed: bool = True
+
+
+def timestep_embedding(t: torch.Tensor, dim: int, max_period: float = 10000.0, time_factor: float = 1000.0):
+    t = time_factor * t.float()
+    half = dim // 2
+    freqs = torch.exp(-math.log(max_period) * torch.arange(half, dtype=torch.float32, device=t.device) / half)
+    args = t[:, None] * freqs[None]
+    return torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
+
+
+def rope(pos: torch.Tensor, dim: int, theta: int) -> torch.Tensor:
+    """[B, L] positions -> [B, L, dim/2, 2, 2] rotation matrices (float32)."""
+    scale = torch.arange(0, dim, 2, dtype=torch.float64, device=pos.device) / dim
+    omega = 1.0 / (theta ** scale)
+    ang = pos.to(torch.float64)[..., None] * omega  # outer product, no batched matmul
+    rot = torch.stack([torch.cos(ang), -torch.sin(ang), torch.sin(ang), torch.cos(ang)], dim=-1)
+    return rot.reshape(*ang.shape, 2, 2).float()
+
+
+def apply_rope(x: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
+    """x [B, H, L, D] -> float32, rotated pairwise by freqs [B, 1, L, D/2, 2, 2]."""
+    xf = x.float().reshape(*x.shape[:-1], -1, 1, 2)
+    out = freqs[..., 0] * xf[..., 0] + freqs[..., 1] * xf[..., 1]
+    return out.reshape(*x.shape)
+
+
+def attention(q, k, v, pe):
+    """Joint attention over [B, H, L, D] heads, RoPE applied in float32, heads merged.
+
+    On the GPU this is torch's fused scaled-dot-product attention restricted to its flash /
+    memory-efficient kernels (the unfused math backend is excluded, so an unsupported case
+    raises instead of falling back).  Elsewhere it is written out in float32."""
+    q, k = apply_rope(q, pe).to(v.dtype), apply_rope(k, pe).to(v.dtype)
+    if q.is_cuda:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            out = F.scaled_dot_product_attention(q, k, v)
+    else:
+        scores = torch.matmul(q.float(), k.float().transpose(-1, -2).contiguous()) / math.sqrt(q.shape[-1])
+        out = torch.matmul(torch.softmax(scores, dim=-1), v.float()).to(v.dtype)
+    b, h, l, d = out.shape
+    return out.transpose(1, 2).reshape(b, l, h * d)
+
+
+class EmbedND(nn.Module):
+    def __init__(self, theta: int, axes_dim):
+        super().__init__()
+        self.theta, self.axes_dim = theta, axes_dim
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        emb = torch.cat([rope(ids[..., i], self.axes_dim[i], self.theta) for i in range(ids.shape[-1])], dim=-3)
+        return emb.unsqueeze(1)
+
+
+class MLPEmbedder(nn.Module):
+    def __init__(self, in_dim: int, hidden: int):
+        super().__init__()
+        self.in_layer = nn.Linear(in_dim, hidden)
+        self.out_layer = nn.Linear(hidden, hidden)
+
+    def forward(self, x):
+        return self.out_layer(F.silu(self.in_layer(x)))
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int):
+        super().__init__()
+        self.scale = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(x.dtype) * self.scale
+
+
+class QKNorm(nn.Module):
+    def __init__(self, dim: int):
+        super().__init__()
+        self.query_norm, self.key_norm = RMSNorm(dim), RMSNorm(dim)
+
+    def forward(self, q, k):
+        return self.query_norm(q), self.key_norm(k)
+
+
+class Modulation(nn.Module):
+    def __init__(self, dim: int, double: bool):
+        super().__init__()
+        self.multiplier = 6 if double else 3
+        self.lin = nn.Linear(dim, self.multiplier * dim)
+
+    def forward(self, vec):
+        out = self.lin(F.silu(vec))[:, None, :].chunk(self.multiplier, dim=-1)
+        first = out[:3]
+        second = out[3:] if self.multiplier == 6 else None
+        return first, second  # (shift, scale, gate)
+
+
+def _split_heads(qkv: torch.Tensor, heads: int):
+    b, l, _ = qkv.shape
+    q, k, v = qkv.reshape(b, l, 3, heads, -1).permute(2, 0, 3, 1, 4).unbind(0)
+    return q, k, v
+
+
+class DoubleStreamBlock(nn.Module):
+    def __init__(self, hidden: int, heads: int, mlp_ratio: float, qkv_bias: bool):
+        super().__init__()
+        mlp_hidden = int(hidden * mlp_ratio)
+        self.heads = heads
+        for side in ("img", "txt"):
+            setattr(self, f"{side}_mod", Modulation(hidden, double=True))
+            setattr(self, f"{side}_qkv", nn.Linear(hidden, 3 * hidden, bias=qkv_bias))
+            setattr(self, f"{side}_qknorm", QKNorm(hidden // heads))
+            setattr(self, f"{side}_proj", nn.Linear(hidden, hidden))
+            setattr(self, f"{side}_mlp", nn.Sequential(nn.Linear(hidden, mlp_hidden), nn.GELU(approximate="tanh"),
+                                                       nn.Linear(mlp_hidden, hidden)))
+
+    def _ln(self, x):
+        return F.layer_norm(x, (x.shape[-1],), eps=1e-6)
+
+    def forward(self, img, txt, vec, pe):
+        (i_shift1, i_scale1, i_gate1), (i_shift2, i_scale2, i_gate2) = self.img_mod(vec)
+        (t_shift1, t_scale1, t_gate1), (t_shift2, t_scale2, t_gate2) = self.txt_mod(vec)
+        iq, ik, iv = _split_heads(self.img_qkv((1 + i_scale1) * self._ln(img) + i_shift1), self.heads)
+        tq, tk, tv = _split_heads(self.txt_qkv((1 + t_scale1) * self._ln(txt) + t_shift1), self.heads)
+        iq, ik = self.img_qknorm(iq, ik)
+        tq, tk = self.txt_qknorm(tq, tk)
+        attn = attention(torch.cat([tq, iq], 2), torch.cat([tk, ik], 2), torch.cat([tv, iv], 2), pe)
+        t_attn, i_attn = attn[:, : txt.shape[1]], attn[:, txt.shape[1]:]
+        img = img + i_gate1 * self.img_proj(i_attn)
+        img = img + i_gate2 * self.img_mlp((1 + i_scale2) * self._ln(img) + i_shift2)
+        txt = txt + t_gate1 * self.txt_proj(t_attn)
+        txt = txt + t_gate2 * self.txt_mlp((1 + t_scale2) * self._ln(txt) + t_shift2)
+        return img, txt
+
+
+class SingleStreamBlock(nn.Module):
+    def __init__(self, hidden: int, heads: int, mlp_ratio: float):
+        super().__init__()
+        self.hidden, self.heads = hidden, heads
+        self.mlp_hidden = int(hidden * mlp_ratio)
+        self.linear1 = nn.Linear(hidden, 3 * hidden + self.mlp_hidden)
+        self.linear2 = nn.Linear(hidden + self.mlp_hidden, hidden)
+        self.norm = QKNorm(hidden // heads)
+        self.modulation = Modulation(hidden, double=False)
+
+    def forward(self, x, vec, pe):
+        (shift, scale, gate), _ = self.modulation(vec)
+        h = self.linear1((1 + scale) * F.layer_norm(x, (x.shape[-1],), eps=1e-6) + shift)
+        qkv, mlp = torch.split(h, [3 * self.hidden, self.mlp_hidden], dim=-1)
+        q, k, v = _split_heads(qkv, self.heads)
+        q, k = self.norm(q, k)
+        out = self.linear2(torch.cat([attention(q, k, v, pe), F.gelu(mlp, approximate="tanh")], dim=-1))
+        return x + gate * out
+
+
+class Flux(nn.Module):
+    def __init__(self, p: FluxParams):
+        super().__init__()
+        self.p = p
+        h = p.hidden_size
+        self.pe_embedder = EmbedND(p.theta, p.axes_dim)
+        self.img_in = nn.Linear(p.in_channels, h)
+        self.time_in = MLPEmbedder(256, h)
+        self.vector_in = MLPEmbedder(p.vec_in_dim, h)
+        self.guidance_in = MLPEmbedder(256, h) if p.guidance_embed else None
+        self.txt_in = nn.Linear(p.context_in_dim, h)
+        self.double_blocks = nn.ModuleList(
+            [DoubleStreamBlock(h, p.num_heads, p.mlp_ratio, p.qkv_bias) for _ in range(p.depth)])
+        self.single_blocks = nn.ModuleList(
+            [SingleStreamBlock(h, p.num_heads, p.mlp_ratio) for _ in range(p.depth_single_blocks)])
+        self.final_adaln = nn.Linear(h, 2 * h)
+        self.final_linear = nn.Linear(h, p.in_channels)
+
+    def forward(self, img, img_ids, txt, txt_ids, timesteps, y, guidance=None):
+        img = self.img_in(img)
+        vec = self.time_in(timestep_embedding(timesteps, 256).to(img.dtype))
+        if self.guidance_in is not None:
+            vec = vec + self.guidance_in(timestep_embedding(guidance, 256).to(img.dtype))
+        vec = vec + self.vector_in(y)
+        txt = self.txt_in(txt)
+        pe = self.pe_embedder(torch.cat([txt_ids, img_ids], dim=1))
+        for block in self.double_blocks:
+            img, txt = block(img, txt, vec, pe)
+        x = torch.cat([txt, img], dim=1)
+        for block in self.single_blocks:
+            x = block(x, vec, pe)
+        img = x[:, txt.shape[1]:]
+        shift, scale = self.final_adaln(F.silu(vec))[:, None, :].chunk(2, dim=-1)
+        return self.final_linear((1 + scale) * F.layer_norm(img, (img.shape[-1],), eps=1e-6) + shift)
+
+
+def make_inputs(p: FluxParams, img_tokens: int, txt_tokens: int, device, seed: int = 5):
+    """Latent tokens ~N(0,1) on a square patch grid, text embeddings ~N(0,1), pooled vector
+    ~N(0,1), timestep 0.5, guidance 3.5 (batch 1)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    side = int(math.isqrt(img_tokens))
+    assert side * side == img_tokens, "image tokens must form a square grid"
+    img_ids = torch.zeros((side, side, 3), device=device)
+    img_ids[..., 1] = torch.arange(side, device=device)[:, None]
+    img_ids[..., 2] = torch.arange(side, device=device)[None, :]
+    return dict(
+        img=torch.randn((1, img_tokens, p.in_channels), generator=g, device=device).to(torch.bfloat16),
+        img_ids=img_ids.reshape(1, img_tokens, 3),
+        txt=torch.randn((1, txt_tokens, p.context_in_dim), generator=g, device=device).to(torch.bfloat16),
+        txt_ids=torch.zeros((1, txt_tokens, 3), device=device),
+        timesteps=torch.full((1,), 0.5, device=device),
+        y=torch.randn((1, p.vec_in_dim), generator=g, device=device).to(torch.bfloat16),
+        guidance=torch.full((1,), 3.5, device=device),
+    )
+
+
+def build(p: FluxParams, device, seed: int = 0) -> Flux:
+    """torch's default Linear init, drawn directly in bf16 on `device` (no float32 copy of
+    the 12B parameters)."""
+    torch.manual_seed(seed)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(device):
+            model = Flux(p)
+    finally:
+        torch.set_default_dtype(prev)
+    return model.eval()
+
+
+def _median_ms(fn, steps: int) -> float:
+    times = []
+    for _ in range(steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2] * 1e3
+
+
+def time_step(model, inputs, steps: int) -> tuple[torch.Tensor, float, float]:
+    """(eager output, eager ms, HIP-graph replay ms) of one forward, medians over `steps`.
+
+    The graph is captured on the stream the warm-up ran on (so any per-stream workspace
+    already exists) and every replay is checked bit-for-bit against the eager output."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.no_grad(), torch.cuda.stream(stream):
+        for _ in range(2):
+            out = model(**inputs)
+        eager_ms = _median_ms(lambda: model(**inputs), steps)
+        out = model(**inputs)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            static = model(**inputs)
+        graph_ms = _median_ms(graph.replay, steps)
+        torch.cuda.synchronize()
+        if not torch.equal(static, out):
+            raise RuntimeError("HIP-graph replay of the step differs from the eager step")
+    torch.cuda.current_stream().wait_stream(stream)
+    del graph, static
+    return out, eager_ms, graph_ms
+
+
+def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_tokens: int = 512,
+                   group_size: int = 64, steps: int = 5) -> dict:
+    """One denoising step, dense bf16 vs every eligible Linear as W4A4 ConvRotLinear."""
+    from convrot_mlx_amd import replace_convrot_linears
+
+    p = p or FluxParams()
+    dev = torch.device("cuda:0")
+    model = build(p, dev)
+    inputs = make_inputs(p, img_tokens, txt_tokens, dev)
+    dense, dense_ms, dense_graph_ms = time_step(model, inputs, steps)
+    dense = dense.float()
+    linears = sum(1 for m in model.modules() if isinstance(m, nn.Linear))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    names = replace_convrot_linears(model, backend="hip-w4a4", group_size=group_size)
+    torch.cuda.synchronize()
+    convert_s = time.perf_counter() - t0
+    torch.cuda.empty_cache()
+    quant, quant_ms, quant_graph_ms = time_step(model, inputs, steps)
+    quant = quant.float()
+    diff = quant - dense
+    rel = (diff.norm() / dense.norm()).item()
+    cos = F.cosine_similarity(quant.flatten(), dense.flatten(), dim=0).item()
+    return {
+        "what": "random-init FLUX.1-dev DiT, one denoising step, batch 1, "
+                f"{img_tokens} image + {txt_tokens} text tokens, bf16",
+        "linears": linears, "converted": len(names), "group_size": group_size,
+        "dense_bf16_ms": round(dense_ms, 2), "convrot_w4a4_ms": round(quant_ms, 2),
+        "speedup": round(dense_ms / quant_ms, 3),
+        "dense_bf16_graph_ms": round(dense_graph_ms, 2), "convrot_w4a4_graph_ms": round(quant_graph_ms, 2),
+        "graph_speedup": round(dense_graph_ms / quant_graph_ms, 3), "convert_s": round(convert_s, 3),
+        "rel_l2_vs_dense": round(rel, 4), "cosine_vs_dense": round(cos, 5),
+        "max_abs_diff": round(diff.abs().max().item(), 4),
+    }
+
+
+def profile_variant(variant: str, steps: int, group_size: int = 64) -> dict:
+    """Eager steps of one variant only (for a kernel trace whose statistics cover one model)."""
+    from convrot_mlx_amd import replace_convrot_linears
+
+    p = FluxParams()
+    dev = torch.device("cuda:0")
+    model = build(p, dev)
+    inputs = make_inputs(p, 1024, 512, dev)
+    if variant == "convrot":
+        replace_convrot_linears(model, backend="hip-w4a4", group_size=group_size)
+    with torch.no_grad():
+        model(**inputs)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(1000)  # a marker kernel: the timed steps are the dispatches after it
+        ms = _median_ms(lambda: model(**inputs), steps)
+    return {"variant": variant, "timed_steps": steps, "eager_ms": round(ms, 2)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--group-size", type=int, default=64)
+    ap.add_argument("--variant", choices=["both", "dense", "convrot"], default="both",
+                    help="'dense' or 'convrot' runs eager steps of that model only, for profiling")
+    args = ap.parse_args()
+    if args.variant == "both":
+        print(json.dumps(config5_figure(group_size=args.group_size, steps=args.steps)), flush=True)
+    else:
+        print(json.dumps(profile_variant(args.variant, args.steps, args.group_size)), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

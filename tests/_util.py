@@ -31,7 +31,7 @@ def normal_input(seed: int, shape, dtype: str, orc) -> np.ndarray:
 
 
 def outlier_input(seed: int, shape, dtype: str, orc, std=1.0, frac=0.005, factor=20.0) -> np.ndarray:
-    """Heavy-tailed activations/weights of the BASELINE configs: a fixed seeded subset of
+    """Heavy-tailed activations/weights of the benchmark configs: a fixed seeded subset of
     channels (columns) scaled by `factor`."""
     rng = np.random.default_rng(seed)
     x = rng.normal(0.0, std, size=shape).astype(np.float32)

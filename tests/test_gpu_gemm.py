@@ -185,7 +185,7 @@ def test_kn_layout_entry_matches(orc, dev):
 
 @pytest.mark.parametrize("K,N", [(3072, 9216), (3072, 3072), (3072, 12288), (12288, 3072), (3072, 21504), (15360, 3072)])
 def test_flux_shapes_complete_path(orc, dev, K, N):
-    """BASELINE configs 2/3 at full size: prep (HIP) -> GEMM (HIP).  Codes and scales must equal
+    """benchmark configs 2/3 at full size: prep (HIP) -> GEMM (HIP).  Codes and scales must equal
     the oracle's everywhere; outputs are compared exactly on a seeded sample of 48 rows x all columns."""
     api = _api()
     M, G = 1536, 64

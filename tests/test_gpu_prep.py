@@ -1,7 +1,7 @@
 """GPU parity: fused preparation kernel vs the CPU oracle, bit for bit.
 
 Seeds and shapes follow /root/reference/tests/test_core.py (:54-137), plus
-the BASELINE FLUX shapes, every supported group size and dtype, and edge rows.
+the benchmark FLUX shapes, every supported group size and dtype, and edge rows.
 """
 
 from __future__ import annotations
@@ -83,7 +83,7 @@ def test_groups_and_dtypes(orc, dev, G, dtype):
      (5, 64, 64), (3, 256, 256), (4, 65536, 256), (6, 21504 - 21504 % 256, 256)],
 )
 def test_baseline_feature_counts(orc, dev, M, K, G):
-    """Every K of the BASELINE configs (single- and multi-wave rows), heavy-tailed inputs."""
+    """Every K of the benchmark configs (single- and multi-wave rows), heavy-tailed inputs."""
     x = outlier_input(M * 131 + K, (M, K), "bfloat16", orc)
     _check_prepare(orc, dev, x, "bfloat16", G, f"M={M} K={K} G={G}")
 

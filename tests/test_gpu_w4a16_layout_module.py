@@ -58,7 +58,7 @@ def test_w4a16_edges(orc, dev, act_dtype):
 @pytest.mark.parametrize("M", [1, 8, 32])
 @pytest.mark.parametrize("K,N", [(3072, 12288), (12288, 3072)])
 def test_w4a16_config4(orc, dev, M, K, N):
-    """BASELINE config 4 shapes: small M, int4 weights with per-row scales, bf16 output."""
+    """benchmark config 4 shapes: small M, int4 weights with per-row scales, bf16 output."""
     rng = np.random.default_rng(M * 7 + K)
     w = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
     ws = rng.uniform(0.001, 0.01, size=(N,)).astype(np.float32)
@@ -199,7 +199,7 @@ def test_w4a4_layer_group64_k2688(orc, dev):
 
 
 def test_config1_end_to_end(orc, dev):
-    """K=N=1024, M=64, G=64, W~N(0,0.02^2), X~N(0,1), no bias, seed 0."""
+    """benchmark config 1: K=N=1024, M=64, G=64, W~N(0,0.02^2), X~N(0,1), no bias, seed 0."""
     api = _api()
     rng = np.random.default_rng(0)
     w = orc.from_f32(rng.normal(0.0, 0.02, size=(1024, 1024)).astype(np.float32), "bfloat16")
