@@ -338,8 +338,10 @@ __device__ __forceinline__ int a_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1
 // INT8-activation GEMM with direct-to-LDS loads: each 1 KB piece of a
 // k-block (8 activation rows x 128 features, or one CDNA4 weight block) is
 // fetched by one wave instruction (buffer_load_dwordx4 ... lds) straight into
-// a 3-deep LDS ring, so no registers stage the data and loads run ahead of
-// the MFMAs.  Every activation load reads whole 128-byte lines; inside LDS
+// an LDS ring of STAGES k-blocks, so no registers stage the data and loads
+// run ahead of the MFMAs.  (Three stages suffice: a lone 128x128 workgroup
+// runs a k-block in the same ~0.45 us with a 6-deep ring, so it is not
+// bound by the bytes in flight.)  Every activation load reads whole 128-byte lines; inside LDS
 // the 16-byte chunks of each row are permuted by a_swizzle so that the MFMA
 // fragment reads (16 rows x 16 bytes) are bank-conflict free.  Out-of-range
 // rows/blocks read as zero through the buffer range check (no branches in the
@@ -357,14 +359,13 @@ __device__ __forceinline__ int a_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1
 // keep a 256-register accumulator in place and spills inside the loop.)
 enum Pipe : int { kSingle = 0, kPingPong = 1 };
 
-template <int BM, int BN, int WM, int WN, int PIPE>
+template <int BM, int BN, int WM, int WN, int PIPE, int STAGES = 3>
 struct DmaEngine {
   static constexpr int NW = WM * WN;
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int FM = TM / 16, FN = TN / 16;
   static constexpr int A_FRAGS = (BM / 16) * 2, B_FRAGS = BN / 16;
   static constexpr int LOADS = A_FRAGS + B_FRAGS;
-  static constexpr int STAGES = 3;
   static constexpr int STAGE_BYTES = LOADS * 1024;
   static constexpr int SMEM_BYTES = STAGES * STAGE_BYTES;
   static constexpr int LPW = LOADS / NW;  // DMA instructions per wave per k-block
@@ -374,6 +375,7 @@ struct DmaEngine {
   static_assert(LOADS % NW == 0, "fragment loads must split evenly over waves");
   static_assert(A_FRAGS % NW == 0 && B_FRAGS % NW == 0 && APW % 2 == 0, "each wave loads APW (even) + BPW pieces");
   static_assert(NW * STAGING <= SMEM_BYTES, "epilogue staging exceeds LDS");
+  static_assert(STAGES >= 3 && (STAGES - 1) * LPW <= 63, "ring depth: vmcnt counts at most 63 DMAs");
 
   // Fragments of one k-block held in registers: packed weights (both k-steps)
   // and int8 activations for k-steps 0 and 1.
@@ -492,13 +494,26 @@ struct DmaEngine {
     body(kb0, n, acc, nullptr);
   }
 
-  // First DMAs of a run: k-blocks kb0 .. kb0+2 (kPingPong) or kb0 .. kb0+1
-  // into stages 0, 1(, 2).  The ring must be free (barrier after its last reads).
+  // Wait until at most `ahead` k-blocks of this wave's DMAs (LPW each) are in
+  // flight (`ahead` <= J; wave-uniform, so the branches are scalar).
+  template <int J>
+  __device__ __forceinline__ static void wait_blocks(int ahead) {
+    if constexpr (J <= 0) {
+      wait_vmcnt<0>();
+    } else {
+      if (ahead >= J) wait_vmcnt<J * LPW>();
+      else wait_blocks<J - 1>(ahead);
+    }
+  }
+
+  // First DMAs of a run: k-blocks kb0 .. kb0+STAGES-1 (kPingPong) or
+  // kb0 .. kb0+STAGES-2 (kSingle) into stages 0, 1, ...  The ring must be free
+  // (barrier after its last reads).
   __device__ __forceinline__ void prologue(int kb0, int n) {
-    issue(kb0, 0);
-    if (n > 1) issue(kb0 + 1, 1);
-    if constexpr (PIPE == kPingPong)
-      if (n > 2) issue(kb0 + 2, 2);
+    constexpr int AHEAD = PIPE == kPingPong ? STAGES : STAGES - 1;
+#pragma unroll
+    for (int s = 0; s < AHEAD; ++s)
+      if (s < n) issue(kb0 + s, s);
   }
 
   // The rest of a run after prologue(kb0, n).  The prologue's DMAs must be the
@@ -511,24 +526,21 @@ struct DmaEngine {
     };
     Frags f0;
     if constexpr (PIPE == kPingPong) {
-      // DMA three blocks ahead; block i+1's fragments are read into the spare
+      // DMA STAGES blocks ahead; block i+1's fragments are read into the spare
       // register set while block i's MFMAs run.  The barrier of step i
-      // publishes DMA(i+1) and retires every wave's reads of stage i % 3
-      // (issued in step i-1), which DMA(i+3) then refills.
+      // publishes DMA(i+1) and retires every wave's reads of stage i % STAGES
+      // (issued in step i-1), which DMA(i+STAGES) then refills.
       Frags f1;
-      if (n > 2) wait_vmcnt<2 * LPW>();
-      else if (n > 1) wait_vmcnt<LPW>();
-      else wait_vmcnt<0>();
+      wait_blocks<STAGES - 1>(min(n, STAGES) - 1);
       raise();
       __syncthreads();
       read_frags(0, f0);
       auto step = [&](int i, Frags& cur, Frags& nxt) {
-        // outstanding: blocks i+1 and i+2 (those below n); block i+1 must land
-        if (i + 2 < n) wait_vmcnt<LPW>();
-        else wait_vmcnt<0>();
+        // in flight: blocks i+1 .. min(n, i+STAGES)-1; block i+1 must land
+        wait_blocks<STAGES - 2>(min(n - i - 2, STAGES - 2));
         __syncthreads();
-        if (i + 3 < n) issue(kb0 + i + 3, i % 3);
-        if (i + 1 < n) read_frags((i + 1) % 3, nxt);
+        if (i + STAGES < n) issue(kb0 + i + STAGES, i % STAGES);
+        if (i + 1 < n) read_frags((i + 1) % STAGES, nxt);
         mma(cur, acc);
       };
       int i = 0;
@@ -538,16 +550,15 @@ struct DmaEngine {
       }
       if (i < n) step(i, f0, f1);
     } else {
-      // One register set: DMA two blocks ahead.  The barrier of iteration i
-      // publishes DMA(i) and retires every wave's reads of stage (i-1) % 3,
-      // which DMA(i+2) then refills.
+      // One register set: DMA STAGES-1 blocks ahead.  The barrier of
+      // iteration i publishes DMA(i) and retires every wave's reads of stage
+      // (i-1) % STAGES, which DMA(i+STAGES-1) then refills.
       for (int i = 0; i < n; ++i) {
-        if (i + 1 < n) wait_vmcnt<LPW>();
-        else wait_vmcnt<0>();
+        wait_blocks<STAGES - 2>(min(n - i - 1, STAGES - 2));
         if (i == 0) raise();
         __syncthreads();
-        if (i + 2 < n) issue(kb0 + i + 2, (i + 2) % 3);
-        read_frags(i % 3, f0);
+        if (i + STAGES - 1 < n) issue(kb0 + i + STAGES - 1, (i + STAGES - 1) % STAGES);
+        read_frags(i % STAGES, f0);
         // Issue all of the block's fragment reads before its MFMAs; left to
         // itself the compiler reads two fragments at a time just before use
         // and the MFMA pipe waits out each LDS round trip.
@@ -571,12 +582,12 @@ __device__ __forceinline__ void tile_origin(int t, int tiles_m, int tiles_n, int
 
 // One workgroup per output tile.  Workgroups are renumbered so that the
 // tiles one XCD (one L2) runs are adjacent in the grouped tile order.
-template <int BM, int BN, int WM, int WN, int PIPE, int ODT>
+template <int BM, int BN, int WM, int WN, int PIPE, int STAGES, int ODT>
 __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
     const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
     int K, int nblocks, int kblocks, int tiles_m, int tiles_n) {
-  using E = DmaEngine<BM, BN, WM, WN, PIPE>;
+  using E = DmaEngine<BM, BN, WM, WN, PIPE, STAGES>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
   E e(smem);
 
@@ -602,14 +613,19 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
 // ---- stream-K
 //
 // Workspace (device memory owned by the launcher, one per device and stream):
-//   int32 words [0, 8)       ticket counter of each workgroup group
-//   int32 words [8, 16)      finished-workgroup counter of each group
-//   int32 words [64, 64+G*NW) partial-ready flag of each (workgroup slot, wave)
+//   int32 word 32 g          ticket counter of workgroup group g (one group per XCD)
+//   int32 word 256 + 32 g    finished-workgroup counter of group g
+//   int32 words [512, 512+G*NW) partial-ready flag of each (workgroup slot, wave)
 //   bytes [kSkPartialOffset, ...)  one int32 partial tile per workgroup slot
+// Each counter has a 128-byte line to itself: every workgroup of the launch
+// performs two device-scope atomics on its group's counters, and atomics on
+// one line are serialized.
 // Every counter and flag is back at zero when a launch ends, so consecutive
 // launches on one stream share the workspace; launches that overlap in time
 // (two streams) must not.
-constexpr int kSkCtlWords = 64;
+constexpr int kSkLineWords = 32;
+constexpr int kSkDoneWord = kXcds * kSkLineWords;
+constexpr int kSkCtlWords = 2 * kSkDoneWord;
 constexpr int64_t kSkPartialOffset = 32768;
 constexpr int kSkMaxGrid = 512;  // <= 64 workgroups per group: one lane per contributor when polling
 constexpr int kSkMaxWaves = 8;
@@ -712,12 +728,12 @@ __device__ __forceinline__ void sk_wait_flags(int* first, int stride, int n, int
 // workgroup runs the fused epilogue.  Waits only ever point at lower tickets,
 // i.e. at workgroups that have already started and that wait only on lower
 // tickets themselves, so the kernel finishes whatever the residency.
-template <int BM, int BN, int WM, int WN, int PIPE, int ODT>
+template <int BM, int BN, int WM, int WN, int PIPE, int STAGES, int ODT>
 __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
     const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
     int K, int nblocks, int kblocks, int tiles_m, int tiles_n, uint8_t* __restrict__ work, int min_iters) {
-  using E = DmaEngine<BM, BN, WM, WN, PIPE>;
+  using E = DmaEngine<BM, BN, WM, WN, PIPE, STAGES>;
   constexpr int FN = E::FN, FM = E::FM, NW = E::NW;
   static_assert(NW <= kSkMaxWaves, "flag block sized for 8 waves");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
@@ -728,7 +744,7 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
   uint8_t* partials = work + kSkPartialOffset;
   const int group = blockIdx.x % kXcds;
   const int P = gridDim.x / kXcds;
-  if (threadIdx.x == 0) s_ticket = atomicAdd(&ctl[group], 1);
+  if (threadIdx.x == 0) s_ticket = atomicAdd(&ctl[group * kSkLineWords], 1);
   __syncthreads();
   const int p = __builtin_amdgcn_readfirstlane(s_ticket);
   E e(smem);
@@ -840,9 +856,9 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
 
   // The last workgroup of the group to finish rearms the ticket counters.
   if (threadIdx.x == 0) {
-    if (atomicAdd(&ctl[kXcds + group], 1) == P - 1) {
-      __hip_atomic_store(&ctl[group], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&ctl[kXcds + group], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (atomicAdd(&ctl[kSkDoneWord + group * kSkLineWords], 1) == P - 1) {
+      __hip_atomic_store(&ctl[group * kSkLineWords], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ctl[kSkDoneWord + group * kSkLineWords], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -851,6 +867,7 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
 
 struct Tile {
   int bm, bn, wm, wn;
+  int stages;  // LDS ring depth of the DMA kernels
 };
 
 struct Plan {
@@ -883,10 +900,10 @@ struct Cand {
   double eff;
   bool sk;
 };
-constexpr Cand kCands[4] = {{{256, 256, 2, 4}, 1, 1.0, false},
-                            {{128, 256, 2, 4}, 1, 0.85, true},
-                            {{256, 128, 4, 2}, 1, 0.8, true},
-                            {{128, 128, 2, 2}, 2, 0.8, false}};
+constexpr Cand kCands[4] = {{{256, 256, 2, 4, 3}, 1, 1.0, false},
+                            {{128, 256, 2, 4, 3}, 1, 0.85, true},
+                            {{256, 128, 4, 2, 3}, 1, 0.8, true},
+                            {{128, 128, 2, 2, 3}, 2, 0.8, false}};
 // Fixed cost of the stream-K fix-up (ticket, partial store and reload, the
 // extra pipeline ramp of each piece, the idle tail while owners wait), in
 // units of one 256x256 k-block; fitted to M = 512 .. 4608 FLUX shapes.
@@ -933,17 +950,17 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_sk) {
   const Tile* forced = nullptr;
   Tile ft{};
   if (const char* env = getenv("CONVROT_GEMM_TILE")) {
-    int bm = 0, bn = 0, wm = 2, wn = 2;
-    if (sscanf(env, "%dx%dw%dx%d", &bm, &bn, &wm, &wn) >= 2) {
-      ft = {bm, bn, wm, wn};
+    int bm = 0, bn = 0, wm = 2, wn = 2, stages = 3;
+    if (sscanf(env, "%dx%dw%dx%ds%d", &bm, &bn, &wm, &wn, &stages) >= 2) {
+      ft = {bm, bn, wm, wn, stages};
       forced = &ft;
     }
   }
-  Plan best{{128, 128, 2, 2}, false, 0, min_iters};
+  Plan best{{128, 128, 2, 2, 3}, false, 0, min_iters};
   double best_time = 1e300;
   for (const Cand& c : kCands) {
     const bool match = forced && c.t.bm == forced->bm && c.t.bn == forced->bn && c.t.wm == forced->wm &&
-                       c.t.wn == forced->wn;
+                       c.t.wn == forced->wn && c.t.stages == forced->stages;
     if (forced && !match) continue;
     const int64_t tiles = ((M + c.t.bm - 1) / c.t.bm) * ((N + c.t.bn - 1) / c.t.bn);
     const double td = dp_time(c, tiles, kb, cus);
@@ -1027,7 +1044,7 @@ hipError_t launch_tile(const void* act, const float* xs, const uint8_t* wq, cons
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN, int ODT>
+template <int BM, int BN, int WM, int WN, int STAGES, int ODT>
 hipError_t launch_dma(const Plan& plan, const void* act, const float* xs, const uint8_t* wq, const float* ws,
                       const float* bias, int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
@@ -1037,13 +1054,13 @@ hipError_t launch_dma(const Plan& plan, const void* act, const float* xs, const 
   constexpr int kPP = (BM == 256 && BN == 256) ? kSingle : kPingPong;
   if (plan.sk) {
     if (uint8_t* work = sk_workspace(stream, sk_workspace_bytes(plan))) {
-      hipLaunchKernelGGL((w4a4_gemm_sk_kernel<BM, BN, WM, WN, kPP, ODT>), dim3((unsigned)plan.grid),
+      hipLaunchKernelGGL((w4a4_gemm_sk_kernel<BM, BN, WM, WN, kPP, STAGES, ODT>), dim3((unsigned)plan.grid),
                          dim3(WM * WN * 64), 0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N,
                          (int)K, nblocks, kblocks, tm, tn, work, plan.min_iters);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((w4a4_gemm_dma_kernel<BM, BN, WM, WN, kPP, ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
+  hipLaunchKernelGGL((w4a4_gemm_dma_kernel<BM, BN, WM, WN, kPP, STAGES, ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
                      0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks,
                      tm, tn);
   return hipGetLastError();
@@ -1056,13 +1073,13 @@ hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const f
   const Plan plan = choose_plan(M, N, K, dma);
   const Tile t = plan.t;
   if (dma) {
-#define CONVROT_DMA(BM_, BN_, WM_, WN_)                        \
-  if (t.bm == BM_ && t.bn == BN_ && t.wm == WM_ && t.wn == WN_) \
-    return launch_dma<BM_, BN_, WM_, WN_, ODT>(plan, act, xs, wq, ws, bias, M, N, K, out, stream);
-    CONVROT_DMA(256, 256, 2, 4)
-    CONVROT_DMA(256, 128, 4, 2)
-    CONVROT_DMA(128, 256, 2, 4)
-    CONVROT_DMA(128, 128, 2, 2)
+#define CONVROT_DMA(BM_, BN_, WM_, WN_, S_)                                       \
+  if (t.bm == BM_ && t.bn == BN_ && t.wm == WM_ && t.wn == WN_ && t.stages == S_) \
+    return launch_dma<BM_, BN_, WM_, WN_, S_, ODT>(plan, act, xs, wq, ws, bias, M, N, K, out, stream);
+    CONVROT_DMA(256, 256, 2, 4, 3)
+    CONVROT_DMA(256, 128, 4, 2, 3)
+    CONVROT_DMA(128, 256, 2, 4, 3)
+    CONVROT_DMA(128, 128, 2, 2, 3)
 #undef CONVROT_DMA
   }
 #define CONVROT_TILE(BM_, BN_, WM_, WN_)                    \
