@@ -19,6 +19,12 @@ hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscale
                             const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
                             void* out, int out_dtype, hipStream_t stream);
 
+// Few-row W4A4 kernel (int8 activation codes only); launch_w4a4_gemm routes
+// small M here.
+hipError_t launch_w4a4_smallm(const int8_t* act, const float* xscales, const uint8_t* qweight,
+                              const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K, void* out,
+                              int out_dtype, hipStream_t stream);
+
 hipError_t launch_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales,
                              const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
                              hipStream_t stream);

@@ -1108,12 +1108,24 @@ hipError_t launch_odt(int odt, const void* act, const float* xs, const uint8_t* 
 
 }  // namespace
 
+constexpr int64_t kSmallMMax = 32;
+constexpr int64_t kSmallMMaxWide = 64;
+constexpr int64_t kSmallMWideElems = 40000000;  // N * K, i.e. 20 MB of int4 weights
+
 hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
                             const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
                             void* out, int out_dtype, hipStream_t stream) {
   if (M == 0 || N == 0) return hipSuccess;
   if (act_format == CONVROT_ACT_PACKED)
     return launch_odt<true>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, stream);
+  // Few rows: the weight-streaming kernel (same results bit for bit).  It
+  // wins up to M = 32 everywhere measured, and up to 64 while the int4 weight
+  // is at most ~20 MB (beyond that the tiled kernel's 16-17 us floor is lower).
+  // CONVROT_GEMM_SMALLM_MAX sets the largest M it takes (0: never).
+  int64_t small_max = N * K <= kSmallMWideElems ? kSmallMMaxWide : kSmallMMax;
+  if (const char* env = getenv("CONVROT_GEMM_SMALLM_MAX")) small_max = atoll(env);
+  if (M <= small_max)
+    return launch_w4a4_smallm((const int8_t*)act, xscales, qweight, wscales, bias, M, N, K, out, out_dtype, stream);
   return launch_odt<false>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, stream);
 }
 

@@ -203,3 +203,32 @@ def test_flux_shapes_complete_path(orc, dev, K, N):
     assert np.array_equal(from_dev(ws), wscales)
     expected = orc.w4a4_matmul_codes(a_codes, w_codes, xs, wscales, bias, "bfloat16")
     _assert_exact(y[rows], expected, f"{M}x{K}->{N}")
+
+
+@pytest.mark.parametrize("cfg", ["A", "B", "C", "F"])
+@pytest.mark.parametrize("out_dtype", ["bfloat16", "float32", "float16"])
+@pytest.mark.parametrize("seed,M,K,N", [(61, 1, 3072, 530), (62, 5, 64, 46), (63, 16, 2688, 18432 // 8),
+                                        (64, 17, 384, 100), (65, 32, 1024, 1024), (66, 47, 256, 33)])
+def test_small_m_kernel(orc, dev, monkeypatch, cfg, out_dtype, seed, M, K, N):
+    """The few-row W4A4 kernel (every work split, forced) against the oracle bit for bit,
+    on ragged N and K tails, one to three token tiles."""
+    api = _api()
+    monkeypatch.setenv("CONVROT_GEMM_SMALLM_MAX", "64")
+    monkeypatch.setenv("CONVROT_W4A4_SMALLM_CFG", cfg)
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    b = rng.normal(size=(N,)).astype(np.float32)
+    expected = orc.w4a4_matmul_codes(a, w, xs, ws, b, out_dtype)
+    wq = _dev_u8(orc.codes_to_cdna4(w), dev)
+    a8 = torch.from_numpy(a).to(dev)
+    dt = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}[out_dtype]
+    args = (torch.from_numpy(xs).to(dev), torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev))
+    for _ in range(2):
+        out = api.hip_w4a4_int8_matmul(a8, wq, *args, output_dtype=dt, out_features=N)
+        _assert_exact(from_dev(out), expected, f"small-M cfg {cfg}")
+    no_bias = api.hip_w4a4_int8_matmul(a8, wq, args[0], args[1], None, output_dtype=dt, out_features=N)
+    _assert_exact(from_dev(no_bias), orc.w4a4_matmul_codes(a, w, xs, ws, np.zeros(N, np.float32), out_dtype),
+                  f"small-M cfg {cfg} without bias")
