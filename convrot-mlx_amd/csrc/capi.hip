@@ -96,6 +96,7 @@ int convrot_prepare(const void* x, int dtype, int64_t rows, int64_t features, in
   if (features > kMaxFeatures)
     return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot preparation supports at most %lld features, got %lld",
                 (long long)kMaxFeatures, (long long)features);
+  if (rows > 0x7fffffff) return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot preparation supports at most 2^31-1 rows");
   if (rows == 0) return ok();
   if (!x || !out || (kind != CONVROT_PREP_ROTATE && !scales))
     return fail(CONVROT_ERR_INVALID, "null pointer argument");
