@@ -26,6 +26,8 @@ ACT_PACKED, ACT_INT8 = 0, 1
 _vp, _i64, _i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
 SIGNATURES = {
     "convrot_prepare": (_i32, [_vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "convrot_prepare_modulated": (_i32, [_vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _i64, ctypes.c_float, _vp,
+                                         _vp, _vp]),
     "convrot_w4a4_gemm": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_w4a16_gemm": (_i32, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_pack_int4": (_i32, [_vp, _i64, _i64, _vp, _vp]),

@@ -109,6 +109,74 @@ def _prepare(x: torch.Tensor, group_size: int, mode: int) -> tuple[torch.Tensor,
     return out, scales
 
 
+def _modulation_rows(rows: int, features: int, shift: torch.Tensor, scale: torch.Tensor):
+    """shift / scale as [V, K] rows of the activation dtype, and the rows of x per vector."""
+    if shift.shape[-1] != features or scale.shape[-1] != features:
+        raise ValueError(f"shift and scale must end in {features} features, got {tuple(shift.shape)} and "
+                         f"{tuple(scale.shape)}")
+    sh, sc = shift.reshape(-1, features), scale.reshape(-1, features)
+    if sh.shape[0] != sc.shape[0]:
+        raise ValueError(f"shift has {sh.shape[0]} rows but scale has {sc.shape[0]}")
+    vectors = sh.shape[0]
+    if vectors == 0 or rows % vectors:
+        raise ValueError(f"{rows} activation rows do not split evenly over {vectors} modulation vectors")
+    return sh, sc, rows // vectors
+
+
+def _prepare_modulated(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, group_size: int, mode: int,
+                       eps: float) -> tuple[torch.Tensor, torch.Tensor | None]:
+    nat.require_device(x, shift, scale)
+    x = x.contiguous()
+    rows, features = x.shape
+    sh, sc, per_vector = _modulation_rows(rows, features, shift, scale)
+    sh = sh.to(x.dtype).contiguous()
+    sc = sc.to(x.dtype).contiguous()
+    if mode == nat.PREP_PACKED:
+        out = torch.empty((rows, features // 2), dtype=torch.uint8, device=x.device)
+    elif mode == nat.PREP_INT8:
+        out = torch.empty((rows, features), dtype=torch.int8, device=x.device)
+    else:
+        out = torch.empty_like(x)
+    scales = None if mode == nat.PREP_ROTATE else torch.empty((rows,), dtype=torch.float32, device=x.device)
+    nat.check(
+        nat.load().convrot_prepare_modulated(
+            nat.ptr(x), nat.dtype_code(x.dtype), rows, features, group_size, mode, nat.ptr(sh), nat.ptr(sc),
+            per_vector, float(eps), nat.ptr(out), nat.ptr(scales), nat.stream_of(x.device),
+        )
+    )
+    return out, scales
+
+
+def hip_fused_modulated_prepare(
+    x: torch.Tensor,
+    shift: torch.Tensor,
+    scale: torch.Tensor,
+    group_size: int = CONVROT_GROUP_SIZE,
+    *,
+    eps: float = 1e-6,
+    output: str = "int8",
+):
+    """Fused producer: ConvRot preparation of `(1 + scale) * layer_norm(x) + shift`.
+
+    One kernel computes a LayerNorm without affine parameters (moments from
+    float64 sums), the adaLN modulation with a dtype rounding after every op,
+    the regular-Hadamard rotation and the A4 quantization.  No counterpart in
+    the reference, which runs the normalization and modulation as separate ops
+    before ConvRotLinear (examples/flux1_dev/adapter.py:45-70).
+
+    x: [rows, K] (or [..., K]); shift, scale: [V, K] (or [V, 1, K]) with rows
+    divisible by V -- rows r*rows/V .. use vector r, as x [B, L, K] with
+    shift [B, 1, K] does.  output: "int8" (int8 codes + f32 scales), "packed"
+    (uint8 [rows, K/2] + scales) or "rotate" (rotated activation of x's dtype).
+    """
+    modes = {"int8": nat.PREP_INT8, "packed": nat.PREP_PACKED, "rotate": nat.PREP_ROTATE}
+    if output not in modes:
+        raise ValueError(f"output must be one of {sorted(modes)}, got {output!r}")
+    _validate_fused(x.reshape(-1, x.shape[-1]), group_size, "modulated activation preparation")
+    out, scales = _prepare_modulated(x.reshape(-1, x.shape[-1]), shift, scale, group_size, modes[output], eps)
+    return out if output == "rotate" else (out, scales)
+
+
 def hip_fused_prepare_convrot_activation(x: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE):
     """Rotation + absmax + A4 quantize + pack in one pass.
 
@@ -531,6 +599,25 @@ class ConvRotLinear(nn.Module):
                         self.out_features)
         else:
             rotated = _prepare(x2d, self.group_size, nat.PREP_ROTATE)[0]
+            out = hip_w4a16_matmul(rotated, w, self.scales, self.bias, output_dtype=x.dtype,
+                                   out_features=self.out_features)
+        return out.reshape(*lead, self.out_features)
+
+    def forward_modulated(self, x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
+                          eps: float = 1e-6) -> torch.Tensor:
+        """self((1 + scale) * layer_norm(x) + shift) with the normalization and modulation
+        fused into the activation preparation (see hip_fused_modulated_prepare)."""
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"ConvRotLinear expected K={self.in_features}, got {x.shape[-1]}")
+        lead = x.shape[:-1]
+        x2d = x.reshape(-1, self.in_features)
+        w = self._device_weight()
+        if self.a4:
+            qact, xscales = _prepare_modulated(x2d, shift, scale, self.group_size, nat.PREP_INT8, eps)
+            out = _w4a4(qact, nat.ACT_INT8, self.in_features, w, xscales, self.scales, self.bias, x.dtype,
+                        self.out_features)
+        else:
+            rotated = _prepare_modulated(x2d, shift, scale, self.group_size, nat.PREP_ROTATE, eps)[0]
             out = hip_w4a16_matmul(rotated, w, self.scales, self.bias, output_dtype=x.dtype,
                                    out_features=self.out_features)
         return out.reshape(*lead, self.out_features)

@@ -105,6 +105,40 @@ int convrot_prepare(const void* x, int dtype, int64_t rows, int64_t features, in
                        "convrot_prepare");
 }
 
+int convrot_prepare_modulated(const void* x, int dtype, int64_t rows, int64_t features, int group_size, int mode,
+                              const void* shift, const void* scale, int64_t rows_per_vector, float eps, void* out,
+                              float* scales, void* stream) {
+  if (mode & CONVROT_PREP_NO_ROTATE)
+    return fail(CONVROT_ERR_INVALID, "the modulated producer always rotates (no CONVROT_PREP_NO_ROTATE)");
+  if (mode != CONVROT_PREP_PACKED && mode != CONVROT_PREP_INT8 && mode != CONVROT_PREP_ROTATE)
+    return fail(CONVROT_ERR_INVALID, "unknown ConvRot preparation mode %d", mode);
+  if (!valid_dtype(dtype)) return fail(CONVROT_ERR_INVALID, "unsupported activation dtype code %d", dtype);
+  if (rows < 0 || features <= 0) return fail(CONVROT_ERR_INVALID, "invalid shape (%lld, %lld)", (long long)rows, (long long)features);
+  if (rows_per_vector <= 0 || rows_per_vector > 0x7fffffff)
+    return fail(CONVROT_ERR_INVALID, "rows_per_vector must be in [1, 2^31-1], got %lld", (long long)rows_per_vector);
+  if (!(eps >= 0.0f) || eps > 1e30f) return fail(CONVROT_ERR_INVALID, "eps must be finite and non-negative");
+  const int s = log4_group(group_size);
+  if (s < 0) return fail(CONVROT_ERR_INVALID, "Regular Hadamard size must be a power of 4, got %d", group_size);
+  if (s > 5) return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot supports groups [4, 16, 64, 256, 1024], got %d", group_size);
+  if (features % group_size)
+    return fail(CONVROT_ERR_INVALID, "features %lld not divisible by ConvRot group size %d", (long long)features, group_size);
+  if (features % 16)
+    return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot preparation requires features divisible by 16, got %lld",
+                (long long)features);
+  if (features > kMaxFeatures)
+    return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot preparation supports at most %lld features, got %lld",
+                (long long)kMaxFeatures, (long long)features);
+  if (rows > 0x7fffffff) return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot preparation supports at most 2^31-1 rows");
+  if (rows == 0) return ok();
+  if (!x || !out || !shift || !scale || (mode != CONVROT_PREP_ROTATE && !scales))
+    return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (!aligned(x, 16) || !aligned(out, 16) || !aligned(shift, 16) || !aligned(scale, 16))
+    return fail(CONVROT_ERR_INVALID, "x, out, shift and scale must be 16-byte aligned");
+  return launch_status(convrot::launch_prep_modulated(x, dtype, rows, features, s, mode, shift, scale,
+                                                      rows_per_vector, eps, out, scales, (hipStream_t)stream),
+                       "convrot_prepare_modulated");
+}
+
 int convrot_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
                       const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K, void* out,
                       int out_dtype, void* stream) {

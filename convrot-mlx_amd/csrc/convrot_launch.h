@@ -15,6 +15,12 @@ bool prep_plan(int64_t rows, int64_t K, int* ni_out, int* waves_out);
 hipError_t launch_prep(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode, void* out,
                        float* scales, hipStream_t stream);
 
+// The fused modulated producer (LayerNorm + adaLN modulation, then the
+// preparation of launch_prep).
+hipError_t launch_prep_modulated(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode,
+                                 const void* shift, const void* scale, int64_t rows_per_vector, float eps,
+                                 void* out, float* scales, hipStream_t stream);
+
 hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
                             const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
                             void* out, int out_dtype, hipStream_t stream);

@@ -33,6 +33,7 @@ namespace convrot {
 namespace {
 
 constexpr int kMaxWaves = 16;
+constexpr int kMaxBlocks = 64;  // 1024-feature blocks of the longest row (65536 features)
 constexpr int kRegionFloats = 1280;  // per wave: 1024 features + 1/4 padding
 
 // One radix-4 butterfly with a dtype rounding after every add (core.py:89-91):
@@ -216,11 +217,32 @@ __device__ __forceinline__ uint32_t gather_nibbles(uint32_t b0, uint32_t b1, uin
   return __builtin_amdgcn_perm(0u, pairs, 0x0c0c0200u);
 }
 
-template <int DT, int S, int NI, int MODE>
+// Sum of a float64 over the wave (butterfly: every lane ends with the total,
+// added in the same order in every lane).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+// PRE = true: the fused modulated producer.  Each row is first replaced by
+//   y = rb(rb(rb(1 + scale) * rb((x - mean) * rstd)) + shift)
+// (LayerNorm without affine parameters, then the adaLN modulation with a
+// dtype rounding after every op), with the shift / scale row
+// v = row / rows_per_vector.  Then the ConvRot preparation runs on y as it
+// would on x.  The moments are float64 sums in a fixed order that does not
+// depend on the launch plan: lane l of 1024-feature block b adds features
+// 16l .. 16l+15 in order, the 64 lanes are combined by the xor butterfly of
+// wave_sum_f64, and the block sums are added in block order.
+template <int DT, int S, int NI, int MODE, bool PRE>
 __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, void* __restrict__ out,
-                                                     float* __restrict__ scales, int K) {
+                                                     float* __restrict__ scales, int K,
+                                                     const void* __restrict__ shift,
+                                                     const void* __restrict__ scalev, int rows_per_vector,
+                                                     float eps) {
   extern __shared__ float lds[];
   __shared__ float wave_max[kMaxWaves];
+  __shared__ double block_moments[PRE ? kMaxBlocks : 1][2];
 
   constexpr int G = (S == 0) ? 1 : (1 << (2 * S));
   constexpr int LG = (S >= 3) ? (G / 16) : 1;        // lanes per group
@@ -242,12 +264,69 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
   float keep[NI][16];
   float amax = 0.0f;
 
+  if constexpr (PRE) {
+    const int real_blocks = (chunks + 63) >> 6;
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const int block = wave * NI + it;
+      load16<DT>(xrow, (uint32_t)(block * 64 + lane) * (16u * kEsize), keep[it]);  // past the row end: zeros
+      double b1 = 0.0, b2 = 0.0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const double d = (double)keep[it][j];
+        b1 += d;
+        b2 += d * d;
+      }
+      b1 = wave_sum_f64(b1);
+      b2 = wave_sum_f64(b2);
+      if (lane == 0 && block < real_blocks) {
+        block_moments[block][0] = b1;
+        block_moments[block][1] = b2;
+      }
+    }
+    __syncthreads();
+    double s1 = 0.0, s2 = 0.0;
+    for (int b = 0; b < real_blocks; ++b) {
+      s1 += block_moments[b][0];
+      s2 += block_moments[b][1];
+    }
+    const double m64 = s1 / (double)K;
+    double var = s2 / (double)K - m64 * m64;
+    var = var > 0.0 ? var : 0.0;
+    const float mean = (float)m64;
+    const float rstd = (float)(1.0 / sqrt(var + (double)eps));
+    const int64_t vrow = row / rows_per_vector;
+    const __amdgpu_buffer_rsrc_t shrow = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const char*)shift + vrow * K * kEsize), (short)0, K * kEsize, 0x00020000);
+    const __amdgpu_buffer_rsrc_t scrow = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const char*)scalev + vrow * K * kEsize), (short)0, K * kEsize, 0x00020000);
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const int chunk = (wave * NI + it) * 64 + lane;
+      if (chunk >= chunks) continue;  // padding stays zero (whole groups lie past K)
+      float sh[16], sc[16];
+      load16<DT>(shrow, (uint32_t)chunk * (16u * kEsize), sh);
+      load16<DT>(scrow, (uint32_t)chunk * (16u * kEsize), sc);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        // The float32 product is rounded before the dtype rounding, as in the
+        // eager graph: left to itself the compiler folds multiply-and-narrow
+        // into one v_fma_mix (a single rounding of the exact product to f16),
+        // which differs where the float32 product lands on an f16 midpoint.
+        float prod = (keep[it][j] - mean) * rstd;
+        asm volatile("" : "+v"(prod));
+        const float ln = rnd<DT>(prod);
+        keep[it][j] = rnd<DT>(rnd<DT>(rnd<DT>(1.0f + sc[j]) * ln) + sh[j]);
+      }
+    }
+  }
+
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const int block = wave * NI + it;
     const int chunk = block * 64 + lane;
     float (&v)[16] = keep[it];
-    load16<DT>(xrow, (uint32_t)chunk * (16u * kEsize), v);  // chunks past the row end read zeros
+    if constexpr (!PRE) load16<DT>(xrow, (uint32_t)chunk * (16u * kEsize), v);  // chunks past the row end read zeros
     rotate16<DT, S>(v, region, p);
     if constexpr (!kImplicitNorm && S > 0 && MODE != CONVROT_PREP_ROTATE) {
 #pragma unroll
@@ -316,45 +395,59 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
   }
 }
 
+// Optional input transform of a launch (the fused modulated producer).
+struct Modulation {
+  const void* shift;  // nullptr: plain preparation
+  const void* scale;
+  int rows_per_vector;
+  float eps;
+};
+
 template <int DT, int S, int NI, int MODE>
 hipError_t launch_prep_t(const void* x, void* out, float* scales, int64_t rows, int K, int waves,
-                         hipStream_t stream) {
+                         const Modulation& mod, hipStream_t stream) {
   const size_t lds_bytes = (S >= 3) ? (size_t)waves * kRegionFloats * sizeof(float) : 0;
-  hipLaunchKernelGGL((prep_kernel<DT, S, NI, MODE>), dim3((unsigned)rows), dim3(64 * waves), lds_bytes,
-                     stream, x, out, scales, K);
+  if (mod.shift)
+    hipLaunchKernelGGL((prep_kernel<DT, S, NI, MODE, true>), dim3((unsigned)rows), dim3(64 * waves), lds_bytes,
+                       stream, x, out, scales, K, mod.shift, mod.scale, mod.rows_per_vector, mod.eps);
+  else
+    hipLaunchKernelGGL((prep_kernel<DT, S, NI, MODE, false>), dim3((unsigned)rows), dim3(64 * waves), lds_bytes,
+                       stream, x, out, scales, K, nullptr, nullptr, 1, 0.0f);
   return hipGetLastError();
 }
 
 template <int DT, int S, int NI>
 hipError_t launch_prep_mode(int mode, const void* x, void* out, float* scales, int64_t rows, int K,
-                            int waves, hipStream_t stream) {
+                            int waves, const Modulation& mod, hipStream_t stream) {
   switch (mode) {
-    case CONVROT_PREP_PACKED: return launch_prep_t<DT, S, NI, CONVROT_PREP_PACKED>(x, out, scales, rows, K, waves, stream);
-    case CONVROT_PREP_INT8: return launch_prep_t<DT, S, NI, CONVROT_PREP_INT8>(x, out, scales, rows, K, waves, stream);
-    default: return launch_prep_t<DT, S, NI, CONVROT_PREP_ROTATE>(x, out, scales, rows, K, waves, stream);
+    case CONVROT_PREP_PACKED:
+      return launch_prep_t<DT, S, NI, CONVROT_PREP_PACKED>(x, out, scales, rows, K, waves, mod, stream);
+    case CONVROT_PREP_INT8:
+      return launch_prep_t<DT, S, NI, CONVROT_PREP_INT8>(x, out, scales, rows, K, waves, mod, stream);
+    default: return launch_prep_t<DT, S, NI, CONVROT_PREP_ROTATE>(x, out, scales, rows, K, waves, mod, stream);
   }
 }
 
 template <int DT, int S>
 hipError_t launch_prep_ni(int ni, int mode, const void* x, void* out, float* scales, int64_t rows, int K,
-                          int waves, hipStream_t stream) {
+                          int waves, const Modulation& mod, hipStream_t stream) {
   switch (ni) {
-    case 1: return launch_prep_mode<DT, S, 1>(mode, x, out, scales, rows, K, waves, stream);
-    case 3: return launch_prep_mode<DT, S, 3>(mode, x, out, scales, rows, K, waves, stream);
-    default: return launch_prep_mode<DT, S, 4>(mode, x, out, scales, rows, K, waves, stream);
+    case 1: return launch_prep_mode<DT, S, 1>(mode, x, out, scales, rows, K, waves, mod, stream);
+    case 3: return launch_prep_mode<DT, S, 3>(mode, x, out, scales, rows, K, waves, mod, stream);
+    default: return launch_prep_mode<DT, S, 4>(mode, x, out, scales, rows, K, waves, mod, stream);
   }
 }
 
 template <int DT>
 hipError_t launch_prep_s(int s, int ni, int mode, const void* x, void* out, float* scales, int64_t rows,
-                         int K, int waves, hipStream_t stream) {
+                         int K, int waves, const Modulation& mod, hipStream_t stream) {
   switch (s) {
-    case 0: return launch_prep_ni<DT, 0>(ni, mode, x, out, scales, rows, K, waves, stream);
-    case 1: return launch_prep_ni<DT, 1>(ni, mode, x, out, scales, rows, K, waves, stream);
-    case 2: return launch_prep_ni<DT, 2>(ni, mode, x, out, scales, rows, K, waves, stream);
-    case 3: return launch_prep_ni<DT, 3>(ni, mode, x, out, scales, rows, K, waves, stream);
-    case 4: return launch_prep_ni<DT, 4>(ni, mode, x, out, scales, rows, K, waves, stream);
-    default: return launch_prep_ni<DT, 5>(ni, mode, x, out, scales, rows, K, waves, stream);
+    case 0: return launch_prep_ni<DT, 0>(ni, mode, x, out, scales, rows, K, waves, mod, stream);
+    case 1: return launch_prep_ni<DT, 1>(ni, mode, x, out, scales, rows, K, waves, mod, stream);
+    case 2: return launch_prep_ni<DT, 2>(ni, mode, x, out, scales, rows, K, waves, mod, stream);
+    case 3: return launch_prep_ni<DT, 3>(ni, mode, x, out, scales, rows, K, waves, mod, stream);
+    case 4: return launch_prep_ni<DT, 4>(ni, mode, x, out, scales, rows, K, waves, mod, stream);
+    default: return launch_prep_ni<DT, 5>(ni, mode, x, out, scales, rows, K, waves, mod, stream);
   }
 }
 
@@ -402,16 +495,33 @@ bool prep_plan(int64_t rows, int64_t K, int* ni_out, int* waves_out) {
   return true;
 }
 
-hipError_t launch_prep(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode, void* out,
-                       float* scales, hipStream_t stream) {
+namespace {
+
+hipError_t launch_prep_any(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode, void* out,
+                           float* scales, const Modulation& mod, hipStream_t stream) {
   int ni = 0, waves = 0;
   if (!prep_plan(rows, K, &ni, &waves)) return hipErrorInvalidValue;
   if (rows == 0) return hipSuccess;
   switch (dtype) {
-    case kF32: return launch_prep_s<kF32>(log4g, ni, mode, x, out, scales, rows, (int)K, waves, stream);
-    case kF16: return launch_prep_s<kF16>(log4g, ni, mode, x, out, scales, rows, (int)K, waves, stream);
-    default: return launch_prep_s<kBF16>(log4g, ni, mode, x, out, scales, rows, (int)K, waves, stream);
+    case kF32: return launch_prep_s<kF32>(log4g, ni, mode, x, out, scales, rows, (int)K, waves, mod, stream);
+    case kF16: return launch_prep_s<kF16>(log4g, ni, mode, x, out, scales, rows, (int)K, waves, mod, stream);
+    default: return launch_prep_s<kBF16>(log4g, ni, mode, x, out, scales, rows, (int)K, waves, mod, stream);
   }
+}
+
+}  // namespace
+
+hipError_t launch_prep(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode, void* out,
+                       float* scales, hipStream_t stream) {
+  return launch_prep_any(x, dtype, rows, K, log4g, mode, out, scales, Modulation{nullptr, nullptr, 1, 0.0f},
+                         stream);
+}
+
+hipError_t launch_prep_modulated(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode,
+                                 const void* shift, const void* scale, int64_t rows_per_vector, float eps,
+                                 void* out, float* scales, hipStream_t stream) {
+  return launch_prep_any(x, dtype, rows, K, log4g, mode, out, scales,
+                         Modulation{shift, scale, (int)rows_per_vector, eps}, stream);
 }
 
 }  // namespace convrot

@@ -146,6 +146,22 @@ class Modulation(nn.Module):
         return first, second  # (shift, scale, gate)
 
 
+def modulated(linear: nn.Module, x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, fused: bool):
+    """linear((1 + scale) * layer_norm(x) + shift).  With `fused` and a ConvRotLinear the
+    normalization and modulation run inside its activation preparation (one kernel);
+    otherwise as torch ops."""
+    if fused and hasattr(linear, "forward_modulated"):
+        return linear.forward_modulated(x, shift, scale, eps=1e-6)
+    return linear((1 + scale) * F.layer_norm(x, (x.shape[-1],), eps=1e-6) + shift)
+
+
+def set_fused_modulation(model: nn.Module, on: bool) -> None:
+    """Route every adaLN-modulated Linear input through modulated(..., fused=on)."""
+    for m in model.modules():
+        if hasattr(m, "fused_modulation"):
+            m.fused_modulation = on
+
+
 def _split_heads(qkv: torch.Tensor, heads: int):
     b, l, _ = qkv.shape
     q, k, v = qkv.reshape(b, l, 3, heads, -1).permute(2, 0, 3, 1, 4).unbind(0)
@@ -157,6 +173,7 @@ class DoubleStreamBlock(nn.Module):
         super().__init__()
         mlp_hidden = int(hidden * mlp_ratio)
         self.heads = heads
+        self.fused_modulation = False
         for side in ("img", "txt"):
             setattr(self, f"{side}_mod", Modulation(hidden, double=True))
             setattr(self, f"{side}_qkv", nn.Linear(hidden, 3 * hidden, bias=qkv_bias))
@@ -165,22 +182,20 @@ class DoubleStreamBlock(nn.Module):
             setattr(self, f"{side}_mlp", nn.Sequential(nn.Linear(hidden, mlp_hidden), nn.GELU(approximate="tanh"),
                                                        nn.Linear(mlp_hidden, hidden)))
 
-    def _ln(self, x):
-        return F.layer_norm(x, (x.shape[-1],), eps=1e-6)
-
     def forward(self, img, txt, vec, pe):
         (i_shift1, i_scale1, i_gate1), (i_shift2, i_scale2, i_gate2) = self.img_mod(vec)
         (t_shift1, t_scale1, t_gate1), (t_shift2, t_scale2, t_gate2) = self.txt_mod(vec)
-        iq, ik, iv = _split_heads(self.img_qkv((1 + i_scale1) * self._ln(img) + i_shift1), self.heads)
-        tq, tk, tv = _split_heads(self.txt_qkv((1 + t_scale1) * self._ln(txt) + t_shift1), self.heads)
+        fu = self.fused_modulation
+        iq, ik, iv = _split_heads(modulated(self.img_qkv, img, i_shift1, i_scale1, fu), self.heads)
+        tq, tk, tv = _split_heads(modulated(self.txt_qkv, txt, t_shift1, t_scale1, fu), self.heads)
         iq, ik = self.img_qknorm(iq, ik)
         tq, tk = self.txt_qknorm(tq, tk)
         attn = attention(torch.cat([tq, iq], 2), torch.cat([tk, ik], 2), torch.cat([tv, iv], 2), pe)
         t_attn, i_attn = attn[:, : txt.shape[1]], attn[:, txt.shape[1]:]
         img = img + i_gate1 * self.img_proj(i_attn)
-        img = img + i_gate2 * self.img_mlp((1 + i_scale2) * self._ln(img) + i_shift2)
+        img = img + i_gate2 * self.img_mlp[2](self.img_mlp[1](modulated(self.img_mlp[0], img, i_shift2, i_scale2, fu)))
         txt = txt + t_gate1 * self.txt_proj(t_attn)
-        txt = txt + t_gate2 * self.txt_mlp((1 + t_scale2) * self._ln(txt) + t_shift2)
+        txt = txt + t_gate2 * self.txt_mlp[2](self.txt_mlp[1](modulated(self.txt_mlp[0], txt, t_shift2, t_scale2, fu)))
         return img, txt
 
 
@@ -193,10 +208,11 @@ class SingleStreamBlock(nn.Module):
         self.linear2 = nn.Linear(hidden + self.mlp_hidden, hidden)
         self.norm = QKNorm(hidden // heads)
         self.modulation = Modulation(hidden, double=False)
+        self.fused_modulation = False
 
     def forward(self, x, vec, pe):
         (shift, scale, gate), _ = self.modulation(vec)
-        h = self.linear1((1 + scale) * F.layer_norm(x, (x.shape[-1],), eps=1e-6) + shift)
+        h = modulated(self.linear1, x, shift, scale, self.fused_modulation)
         qkv, mlp = torch.split(h, [3 * self.hidden, self.mlp_hidden], dim=-1)
         q, k, v = _split_heads(qkv, self.heads)
         q, k = self.norm(q, k)
@@ -221,6 +237,7 @@ class Flux(nn.Module):
             [SingleStreamBlock(h, p.num_heads, p.mlp_ratio) for _ in range(p.depth_single_blocks)])
         self.final_adaln = nn.Linear(h, 2 * h)
         self.final_linear = nn.Linear(h, p.in_channels)
+        self.fused_modulation = False
 
     def forward(self, img, img_ids, txt, txt_ids, timesteps, y, guidance=None):
         img = self.img_in(img)
@@ -237,7 +254,7 @@ class Flux(nn.Module):
             x = block(x, vec, pe)
         img = x[:, txt.shape[1]:]
         shift, scale = self.final_adaln(F.silu(vec))[:, None, :].chunk(2, dim=-1)
-        return self.final_linear((1 + scale) * F.layer_norm(img, (img.shape[-1],), eps=1e-6) + shift)
+        return modulated(self.final_linear, img, shift, scale, self.fused_modulation)
 
 
 def make_inputs(p: FluxParams, img_tokens: int, txt_tokens: int, device, seed: int = 5):
@@ -331,9 +348,18 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
     torch.cuda.empty_cache()
     quant, quant_ms, quant_graph_ms = time_step(model, inputs, steps)
     quant = quant.float()
-    diff = quant - dense
-    rel = (diff.norm() / dense.norm()).item()
-    cos = F.cosine_similarity(quant.flatten(), dense.flatten(), dim=0).item()
+    set_fused_modulation(model, True)
+    fused, fused_ms, fused_graph_ms = time_step(model, inputs, steps)
+    fused = fused.float()
+
+    def dev_stats(out):
+        diff = out - dense
+        return (round((diff.norm() / dense.norm()).item(), 4),
+                round(F.cosine_similarity(out.flatten(), dense.flatten(), dim=0).item(), 5),
+                round(diff.abs().max().item(), 4))
+
+    rel, cos, mad = dev_stats(quant)
+    frel, fcos, _ = dev_stats(fused)
     return {
         "what": "random-init FLUX.1-dev DiT, one denoising step, batch 1, "
                 f"{img_tokens} image + {txt_tokens} text tokens, bf16",
@@ -342,8 +368,14 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
         "speedup": round(dense_ms / quant_ms, 3),
         "dense_bf16_graph_ms": round(dense_graph_ms, 2), "convrot_w4a4_graph_ms": round(quant_graph_ms, 2),
         "graph_speedup": round(dense_graph_ms / quant_graph_ms, 3), "convert_s": round(convert_s, 3),
-        "rel_l2_vs_dense": round(rel, 4), "cosine_vs_dense": round(cos, 5),
-        "max_abs_diff": round(diff.abs().max().item(), 4),
+        "rel_l2_vs_dense": rel, "cosine_vs_dense": cos, "max_abs_diff": mad,
+        "fused_modulation": {
+            "what": "adaLN LayerNorm + modulation fused into the ConvRot activation preparation (115 sites: 4 per double block, 1 per single block, the final layer)",
+            "eager_ms": round(fused_ms, 2), "graph_ms": round(fused_graph_ms, 2),
+            "graph_speedup_vs_dense": round(dense_graph_ms / fused_graph_ms, 3),
+            "rel_l2_vs_dense": frel, "cosine_vs_dense": fcos,
+            "rel_l2_vs_unfused": round(((fused - quant).norm() / quant.norm()).item(), 5),
+        },
     }
 
 
@@ -355,8 +387,9 @@ def profile_variant(variant: str, steps: int, group_size: int = 64) -> dict:
     dev = torch.device("cuda:0")
     model = build(p, dev)
     inputs = make_inputs(p, 1024, 512, dev)
-    if variant == "convrot":
+    if variant in ("convrot", "fused"):
         replace_convrot_linears(model, backend="hip-w4a4", group_size=group_size)
+        set_fused_modulation(model, variant == "fused")
     with torch.no_grad():
         model(**inputs)
         torch.cuda.synchronize()
@@ -369,8 +402,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--group-size", type=int, default=64)
-    ap.add_argument("--variant", choices=["both", "dense", "convrot"], default="both",
-                    help="'dense' or 'convrot' runs eager steps of that model only, for profiling")
+    ap.add_argument("--variant", choices=["both", "dense", "convrot", "fused"], default="both",
+                    help="'dense', 'convrot' or 'fused' (convrot with fused modulation) runs eager steps of "
+                         "that model only, for profiling")
     args = ap.parse_args()
     if args.variant == "both":
         print(json.dumps(config5_figure(group_size=args.group_size, steps=args.steps)), flush=True)

@@ -21,7 +21,7 @@ import sys
 
 def category(name: str) -> str:
     low = name.lower()
-    if "w4a4_gemm" in name:
+    if "w4a4_gemm" in name or "w4a4_smallm" in name:
         return "convrot_gemm"
     if "prep_kernel" in name:
         return "convrot_prep"

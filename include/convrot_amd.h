@@ -76,6 +76,26 @@ int convrot_prepare(const void* x, int dtype, int64_t rows, int64_t features,
                     int group_size, int mode, void* out, float* scales, void* stream);
 
 /*
+ * Fused modulated producer: convrot_prepare applied to
+ *   y = rb(rb(rb(1 + scale[v]) * rb((x - mean) * rstd)) + shift[v]),
+ *   v = row / rows_per_vector,
+ * i.e. a LayerNorm without affine parameters (mean and variance of the row
+ * from float64 sums; rstd = 1 / sqrt(var + eps)) followed by the adaLN
+ * modulation `(1 + scale) * ln + shift` of a diffusion transformer, each op
+ * rounded to the dtype, computed in the same pass as the rotation and
+ * quantization (one read of x instead of four passes).  No counterpart in the
+ * reference, which runs these as separate ops before ConvRotLinear
+ * (/root/reference/examples/flux1_dev/adapter.py:45-70 swaps only the Linears);
+ * its design notes name fusing the activation-preparation passes as the
+ * remaining optimization target (docs/design.md:54-64).
+ * shift, scale: dtype [ceil(rows / rows_per_vector), features]; other
+ * arguments as convrot_prepare (group rotation required: no NO_ROTATE).
+ */
+int convrot_prepare_modulated(const void* x, int dtype, int64_t rows, int64_t features, int group_size, int mode,
+                              const void* shift, const void* scale, int64_t rows_per_vector, float eps, void* out,
+                              float* scales, void* stream);
+
+/*
  * W4A4 GEMM with fused epilogue:
  *   out[m, n] = out_dtype(((float(sum_k a[m,k] * w[n,k]) * xscales[m]) * wscales[n]) + bias[n])
  * (left to right, no contraction; integer dot exact in int32).

@@ -273,3 +273,75 @@ void cr_oracle_f32_to_dtype(const float* x, int64_t n, int dt, void* out) {
 void cr_oracle_dtype_to_f32(const void* x, int64_t n, int dt, float* out) {
     for (int64_t i = 0; i < n; ++i) out[i] = load_elem(dt, x, i);
 }
+
+/* ------------------------------------------------------ modulated producer */
+
+/*
+ * The fused producer's input transform (no reference counterpart: it is the
+ * adaLN pattern `(1 + scale) * layer_norm(x) + shift` of a diffusion
+ * transformer, evaluated as a bf16/f16 eager graph would):
+ *   mean  = (float)(s1 / K)
+ *   rstd  = (float)(1 / sqrt(max(s2 / K - (s1 / K)^2, 0) + eps))   (float64)
+ *   ln    = rb((x - mean) * rstd)                                  (float32 ops)
+ *   y     = rb(rb(rb(1 + scale) * ln) + shift)
+ * with shift / scale row v = row / rows_per_vector.  s1 = sum x and
+ * s2 = sum x*x are float64 sums in this fixed order: for each 1024-feature
+ * block b, lane l (0..63) adds features b*1024 + 16l .. +15 in order
+ * (features past K count as 0), the 64 lane sums are combined by the xor
+ * butterfly  s[l] <- s[l] + s[l ^ m]  for m = 32, 16, 8, 4, 2, 1 (every lane
+ * then holds the block sum), and the block sums are added in block order.
+ */
+static void block_moments(int dt, const void* x, int64_t r, int64_t K, int64_t b, double* b1, double* b2) {
+    double s[64], q[64], t[64], u[64];
+    for (int l = 0; l < 64; ++l) {
+        double a1 = 0.0, a2 = 0.0;
+        for (int j = 0; j < 16; ++j) {
+            int64_t k = b * 1024 + 16 * l + j;
+            double d = k < K ? (double)load_elem(dt, x, r * K + k) : 0.0;
+            a1 += d;
+            a2 += d * d;
+        }
+        s[l] = a1;
+        q[l] = a2;
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        for (int l = 0; l < 64; ++l) {
+            t[l] = s[l] + s[l ^ m];
+            u[l] = q[l] + q[l ^ m];
+        }
+        for (int l = 0; l < 64; ++l) {
+            s[l] = t[l];
+            q[l] = u[l];
+        }
+    }
+    *b1 = s[0];
+    *b2 = q[0];
+}
+
+int cr_oracle_modulate(const void* x, int dt, int64_t rows, int64_t K, const void* shift, const void* scale,
+                       int64_t rows_per_vector, float eps, void* out) {
+    if (rows_per_vector <= 0) return -1;
+    const int64_t blocks = (K + 1023) / 1024;
+    for (int64_t r = 0; r < rows; ++r) {
+        double s1 = 0.0, s2 = 0.0;
+        for (int64_t b = 0; b < blocks; ++b) {
+            double b1, b2;
+            block_moments(dt, x, r, K, b, &b1, &b2);
+            s1 += b1;
+            s2 += b2;
+        }
+        double m64 = s1 / (double)K;
+        double var = s2 / (double)K - m64 * m64;
+        if (var < 0.0) var = 0.0;
+        float mean = (float)m64;
+        float rstd = (float)(1.0 / sqrt(var + (double)eps));
+        int64_t vrow = r / rows_per_vector;
+        for (int64_t k = 0; k < K; ++k) {
+            float ln = rb(dt, (load_elem(dt, x, r * K + k) - mean) * rstd);
+            float one_plus = rb(dt, 1.0f + load_elem(dt, scale, vrow * K + k));
+            float y = rb(dt, rb(dt, one_plus * ln) + load_elem(dt, shift, vrow * K + k));
+            store_elem(dt, out, r * K + k, y);
+        }
+    }
+    return 0;
+}

@@ -56,6 +56,7 @@ def lib() -> ctypes.CDLL:
         L.cr_oracle_w4a4_matmul.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, vp, vp]
         L.cr_oracle_w4a16_matmul.argtypes = [vp, i32, vp, vp, vp, i64, i64, i64, i32, vp, vp, vp]
         L.cr_oracle_f32_to_dtype.argtypes = [vp, i64, i32, vp]
+        L.cr_oracle_modulate.argtypes = [vp, i32, i64, i64, vp, vp, i64, ctypes.c_float, vp]
         L.cr_oracle_dtype_to_f32.argtypes = [vp, i64, i32, vp]
         L.cr_f32_to_bf16.argtypes = [ctypes.c_float]
         L.cr_f32_to_bf16.restype = ctypes.c_uint16
@@ -175,6 +176,23 @@ def quantize_convrot_weight(weight: np.ndarray, dtype: str, group_size: int = 25
             f"in_features {weight.shape[-1]} not divisible by ConvRot group size {group_size}"
         )
     return prepare_convrot_activation(weight, dtype, group_size)
+
+
+def modulate(x: np.ndarray, dtype: str, shift: np.ndarray, scale: np.ndarray, rows_per_vector: int,
+             eps: float = 1e-6) -> np.ndarray:
+    """Input transform of the fused modulated producer (no reference counterpart; the
+    adaLN pattern `(1 + scale) * layer_norm(x) + shift`), C restatement:
+    LayerNorm moments as float64 sums in the order fixed in convrot_oracle.c, then
+    per-op dtype rounding."""
+    x = np.ascontiguousarray(x)
+    shift = np.ascontiguousarray(shift)
+    scale = np.ascontiguousarray(scale)
+    rows, K = x.shape
+    out = np.empty_like(x)
+    rc = lib().cr_oracle_modulate(_ptr(x), DTYPE_CODES[dtype], rows, K, _ptr(shift), _ptr(scale),
+                                  rows_per_vector, eps, _ptr(out))
+    assert rc == 0
+    return out
 
 
 def w4a4_matmul_codes(a_codes, w_codes, xscales, wscales, bias, out_dtype: str, want_dots: bool = False):

@@ -87,3 +87,26 @@ def test_converted_model_tracks_dense(dev, backend, max_rel):
     cos = F.cosine_similarity(got.flatten(), ref.flatten(), dim=0).item()
     print(f"{backend}: rel_l2={rel:.4f} cosine={cos:.5f}")
     assert rel < max_rel and cos > 1 - max_rel ** 2
+
+
+def test_fused_modulation_tracks_unfused(dev):
+    """The converted tiny DiT with the adaLN LayerNorm + modulation fused into the ConvRot
+    preparation stays next to the same model with torch's LayerNorm and modulation ops: the
+    two differ only where torch's float32 LayerNorm and the fused float64-moment one round
+    a normalized value to different bf16 neighbours."""
+    from convrot_mlx_amd import replace_convrot_linears
+    from examples.flux1_dev.dit import set_fused_modulation
+
+    p = _tiny()
+    model = build(p, dev, seed=7)
+    inputs = make_inputs(p, img_tokens=64, txt_tokens=24, device=dev, seed=8)
+    ref = _run(model, inputs).float()
+    replace_convrot_linears(model, group_size=G)
+    unfused = _run(model, inputs).float()
+    set_fused_modulation(model, True)
+    fused = _run(model, inputs).float()
+    assert torch.equal(fused, _run(model, inputs).float())
+    rel = ((fused - unfused).norm() / unfused.norm()).item()
+    rel_dense = ((fused - ref).norm() / ref.norm()).item()
+    print(f"fused vs unfused rel_l2={rel:.5f}; fused vs dense {rel_dense:.4f}")
+    assert rel < 0.05 and rel_dense < 0.35
