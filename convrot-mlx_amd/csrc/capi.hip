@@ -56,6 +56,10 @@ int log4_group(int g) {
 }
 
 constexpr int64_t kMaxFeatures = 65536;
+// The GEMM kernels address the packed weights ([ceil(K/128)][ceil(N/16)][1 KB])
+// through buffer resources with 32-bit signed offsets: below 2 GiB.
+constexpr int64_t kMaxWeightBytes = int64_t(1) << 31;
+int64_t packed_weight_bytes(int64_t N, int64_t K) { return ((K + 127) / 128) * ((N + 15) / 16) * 1024; }
 
 }  // namespace
 
@@ -150,6 +154,9 @@ int convrot_w4a4_gemm(const void* act, int act_format, const float* xscales, con
   if (K > kMaxFeatures)
     return fail(CONVROT_ERR_UNSUPPORTED, "W4A4 GEMM supports K up to %lld, got %lld", (long long)kMaxFeatures, (long long)K);
   if (M > 0x7fffffff || N > 0x7fffffff) return fail(CONVROT_ERR_UNSUPPORTED, "GEMM dimension too large");
+  if (packed_weight_bytes(N, K) >= kMaxWeightBytes)
+    return fail(CONVROT_ERR_UNSUPPORTED, "W4A4 GEMM packed weights are limited to 2 GiB (N=%lld K=%lld)", (long long)N,
+                (long long)K);
   if (M == 0 || N == 0) return ok();
   if (!act || !xscales || !qweight || !wscales || !out) return fail(CONVROT_ERR_INVALID, "null pointer argument");
   if (!aligned(act, 16) || !aligned(qweight, 16) || !aligned(out, 16))
@@ -169,6 +176,9 @@ int convrot_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight, c
   if (K > kMaxFeatures)
     return fail(CONVROT_ERR_UNSUPPORTED, "W4A16 GEMM supports K up to %lld, got %lld", (long long)kMaxFeatures, (long long)K);
   if (M > 0x7fffffff || N > 0x7fffffff) return fail(CONVROT_ERR_UNSUPPORTED, "GEMM dimension too large");
+  if (packed_weight_bytes(N, K) >= kMaxWeightBytes)
+    return fail(CONVROT_ERR_UNSUPPORTED, "W4A16 GEMM packed weights are limited to 2 GiB (N=%lld K=%lld)", (long long)N,
+                (long long)K);
   if (M == 0 || N == 0) return ok();
   if (!act || !qweight || !wscales || !out) return fail(CONVROT_ERR_INVALID, "null pointer argument");
   if (!aligned(act, 16) || !aligned(qweight, 16) || !aligned(out, 16))

@@ -94,4 +94,33 @@ __device__ __forceinline__ void nibbles_x16(uint32_t w, uint32_t& lo, uint32_t& 
   hi = w & 0xf0f0f0f0u;
 }
 
+// ---- direct-to-LDS loads (the DMA GEMM pipelines)
+
+typedef int i32x4_sgpr __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (stride 0): accesses at or beyond `bytes` read as zero.
+// Built from wave-uniform values so it lives in SGPRs.
+__device__ __forceinline__ i32x4_sgpr buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  return (i32x4_sgpr){__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                      __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)),
+                      __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+
+// One wave-wide 16-byte-per-lane load from a buffer straight into LDS at
+// lds_addr + 16 * lane (buffer_load_dwordx4 ... lds, address in M0).  Issued
+// through asm so the compiler does not add conservative vmcnt waits before
+// LDS reads; the kernel orders these loads with explicit waits + barriers.
+__device__ __forceinline__ void dma16(i32x4_sgpr rsrc, uint32_t voffset, uint32_t lds_addr) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc), "{m0}"(lds_addr) : "memory");
+}
+
+// s_waitcnt on vmcnt only (expcnt and lgkmcnt left at "no wait").
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+  asm volatile("" ::: "memory");
+}
+
 }  // namespace convrot

@@ -31,6 +31,9 @@ hipError_t launch_w4a4_smallm(const int8_t* act, const float* xscales, const uin
                               const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K, void* out,
                               int out_dtype, hipStream_t stream);
 
+// Compute units of the current device (cached per device).
+int device_cus();
+
 hipError_t launch_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales,
                              const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
                              hipStream_t stream);

@@ -172,6 +172,282 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
   }
 }
 
+// ---- many token rows: tiled kernel on direct-to-LDS loads
+//
+// A workgroup of 8 waves owns a BM (tokens) x BN (output features) tile,
+// BM, BN in {128, 256}; wave w computes rows (w / 4) * BM/2 .. and features
+// (w % 4) * BN/4 .. as FM x FN float32 fragments of 16 x 16.  K advances in
+// 128-feature blocks through two LDS stages, each filled by one-KB
+// buffer_load ... lds pieces (no register staging):
+//   activations: BM rows x 256 bytes; piece j = rows 4j .. 4j+3, lane L
+//     writes row 4j + L/16, slot L%16, which receives the row's 16-byte chunk
+//     (L%16) ^ (row & 15): 16 lanes reading one chunk of 16 consecutive rows
+//     then hit 16 different bank groups;
+//   weights: BN/16 CDNA4 blocks (16 features x 128 k each) read as stored.
+// Block i+1 is loaded while block i is multiplied.  Per k-step of 32 the
+// wave expands its FN weight fragments (8 codes per lane) to 16x-scaled
+// 16-bit floats once and uses each for FM MFMAs.  Rows >= M and reads past
+// the weights return zeros (buffer range check); the ragged end of K is
+// zeroed at the fragment (K % 8 == 0, so fragments are whole or empty).
+constexpr int kTileWaves = 8;
+
+template <int BM, int BN>
+struct TiledShape {
+  static constexpr int FM = BM / 32, FN = BN / 64;           // 16x16 fragments per wave
+  static constexpr int APieces = BM / 4, BPieces = BN / 16;  // one-KB pieces per stage
+  static constexpr int APW = APieces / kTileWaves, BPW = BPieces / kTileWaves;
+  static constexpr int StageBytes = (APieces + BPieces) * 1024;
+  static constexpr int RS = BN / 2 + 16;  // output staging row: BN/4 16-bit values + 16 bytes
+  static_assert(APW * kTileWaves == APieces && BPW * kTileWaves == BPieces, "pieces split over waves");
+  static_assert(kTileWaves * (BM / 2) * RS <= 2 * StageBytes, "output staging fits the ring");
+};
+
+template <int ADT, int ODT, int BM, int BN>
+__global__ __launch_bounds__(kTileWaves * 64) __attribute__((amdgpu_waves_per_eu(BM * BN <= 128 * 128 ? 4 : 2)))
+void w4a16_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ wq,
+                        const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out,
+                        int M, int N, int K, int nblocks, int kblocks, int tiles_m, int tiles_n) {
+  using S = TiledShape<BM, BN>;
+  constexpr int FM = S::FM, FN = S::FN;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * S::StageBytes];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / 4, wn = wave % 4;
+  const int q = lane >> 4, r = lane & 15;
+
+  // Tile order: consecutive workgroups of one XCD take adjacent tiles, four
+  // tile rows at a time (they share activation rows and weight columns in L2).
+  const int tiles = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  const int per_xcd = tiles / 8;
+  if (t < per_xcd * 8) t = (t % 8) * per_xcd + t / 8;
+  const int gm = t / (4 * tiles_n), first = gm * 4, rows_g = min(4, tiles_m - first);
+  const int in_g = t - gm * 4 * tiles_n;
+  const int m0 = (first + in_g % rows_g) * BM, n0 = (in_g / rows_g) * BN;
+
+  const int rows_valid = min(BM, M - m0);
+  const i32x4_sgpr ra = buffer_rsrc(act + (int64_t)m0 * K, (uint32_t)rows_valid * (uint32_t)K * 2u);
+  const i32x4_sgpr rw = buffer_rsrc(wq + (int64_t)(n0 / 16) * 1024,
+                                    (uint32_t)(((int64_t)kblocks * nblocks - n0 / 16) * 1024));
+  const uint32_t smem_addr = (uint32_t)(uintptr_t)smem;
+  // this lane's activation piece offsets: row 4j + L/16 of a piece, and
+  // (4j + L/16) & 15 = 4 (j & 3) + L/16
+  uint32_t va[4];
+#pragma unroll
+  for (int j4 = 0; j4 < 4; ++j4) {
+    const int row = 4 * j4 + (lane >> 4);
+    va[j4] = (uint32_t)(row * K * 2 + 16 * ((lane & 15) ^ row));
+  }
+  auto issue = [&](int kb, int stage) {
+    const uint32_t base = smem_addr + (uint32_t)(stage * S::StageBytes);
+#pragma unroll
+    for (int i = 0; i < S::APW; ++i) {
+      const uint32_t j = (uint32_t)(wave * S::APW + i);
+      uint32_t so = (j & ~3u) * 4u * (uint32_t)K * 2u + (uint32_t)kb * 256u;  // rows 4j.., block kb
+      asm volatile("" : "+s"(so));
+      dma16(ra, va[j & 3] + so, base + j * 1024u);
+    }
+#pragma unroll
+    for (int i = 0; i < S::BPW; ++i) {
+      const uint32_t j = (uint32_t)(wave * S::BPW + i);
+      uint32_t so = j * 1024u + (uint32_t)kb * (uint32_t)nblocks * 1024u;
+      asm volatile("" : "+s"(so));
+      dma16(rw, (uint32_t)lane * 16u + so, base + (uint32_t)(S::APieces + j) * 1024u);
+    }
+  };
+
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int a = 0; a < FN; ++a)
+#pragma unroll
+    for (int b = 0; b < FM; ++b) acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  const bool ragged = (K & 127) != 0;
+  issue(0, 0);
+  for (int i = 0; i < kblocks; ++i) {
+    wait_vmcnt<0>();
+    __syncthreads();  // block i visible; every wave is done with stage (i + 1) % 2
+    if (i + 1 < kblocks) issue(i + 1, (i + 1) & 1);
+    const uint8_t* st = smem + (i & 1) * S::StageBytes;
+    uint4 wd[FN];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+      wd[fn] = *(const uint4*)(st + (S::APieces + wn * FN + fn) * 1024 + lane * 16);
+    const bool last = ragged && i + 1 == kblocks;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      i32x4 aop[FM];
+      const int chunk = 4 * q + c;  // features 32q + 8c .. +7 of the block
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int row = wm * (BM / 2) + fm * 16 + r;
+        aop[fm] = *(const i32x4*)(st + row * 256 + 16 * (chunk ^ r));
+      }
+      if (last && i * 128 + 8 * chunk >= K) {
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) aop[fm] = (i32x4){0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const uint32_t wdc = c == 0 ? wd[fn].x : c == 1 ? wd[fn].y : c == 2 ? wd[fn].z : wd[fn].w;
+        const i32x4 bop = expand8<ADT>(wdc);
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) acc[fn][fm] = mfma16<ADT>(bop, aop[fm], acc[fn][fm]);
+      }
+    }
+  }
+  __syncthreads();  // ring -> output staging
+
+  // ---- epilogue (core.py:1151-1152): (dots * ws) + bias, rounded once; codes were scaled by 16
+  const int mw = m0 + wm * (BM / 2), nw = n0 + wn * (BN / 4);
+  if constexpr (ODT == kF32) {
+    const bool vec_ok = (N & 3) == 0;
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int n = nw + fn * 16 + 4 * q;
+      if (n >= N) continue;
+      float wsv[4], bv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int nn = n + j < N ? n + j : N - 1;
+        wsv[j] = wscales[nn] * 0.0625f;
+        bv[j] = bias ? bias[nn] : 0.0f;
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int m = mw + fm * 16 + r;
+        if (m >= M) continue;
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = acc[fn][fm][j] * wsv[j] + bv[j];
+        const int64_t idx = (int64_t)m * N + n;
+        if (vec_ok) {
+          store_out4<ODT>(out, idx, o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (n + j < N) store_out<ODT>(out, idx + j, o[j]);
+        }
+      }
+    }
+  } else {
+    // 16-bit outputs go through the wave's LDS region (BM/2 rows of RS bytes)
+    // and leave as 16-byte stores of whole row segments.
+    uint8_t* region = smem + wave * (BM / 2) * S::RS;
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int nl = fn * 16 + 4 * q;
+      float wsv[4], bv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int nn = min(nw + nl + j, N - 1);
+        wsv[j] = wscales[nn] * 0.0625f;
+        bv[j] = bias ? bias[nn] : 0.0f;
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = acc[fn][fm][j] * wsv[j] + bv[j];
+        const uint2 w2 = ODT == kBF16 ? make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]))
+                                      : make_uint2(pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3]));
+        *(uint2*)(region + (fm * 16 + r) * S::RS + nl * 2) = w2;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    constexpr int CPR = BN / 32;         // 16-byte chunks per staged row
+    constexpr int RPI = 64 / CPR;        // rows per instruction
+    const int cr = lane / CPR, cc = lane % CPR;
+    const bool vec_ok = (N & 7) == 0;
+#pragma unroll
+    for (int r0 = 0; r0 < BM / 2; r0 += RPI) {
+      const int rl = r0 + cr;
+      const int m = mw + rl, n = nw + cc * 8;
+      if (m >= M || n >= N) continue;
+      const uint4 v = *(const uint4*)(region + rl * S::RS + cc * 16);
+      uint16_t* dst = (uint16_t*)out + (int64_t)m * N + n;
+      if (vec_ok && n + 8 <= N) {
+        *(uint4*)dst = v;
+      } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (n + j < N) dst[j] = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+      }
+    }
+  }
+}
+
+template <int ADT, int ODT, int BM, int BN>
+hipError_t launch_tiled_t(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
+                          int64_t N, int64_t K, void* out, hipStream_t stream) {
+  const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
+  const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
+  hipLaunchKernelGGL((w4a16_tiled_kernel<ADT, ODT, BM, BN>), dim3((unsigned)(tm * tn)), dim3(kTileWaves * 64), 0,
+                     stream, (const uint16_t*)act, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, tm,
+                     tn);
+  return hipGetLastError();
+}
+
+// Tile choice: the candidate with the least modelled time.  Each CU works
+// through ceil(tiles / CUs) tiles of BM * BN * kblocks MFMA work at the tile's
+// rate, holding per_cu of them at once, plus a fixed cost (pipeline fill and
+// epilogue) per resident batch.  Rates and the fixed cost (in units of one
+// 128-feature block of a 256 x 256 tile, ~4 us) are fitted to MI355X timings
+// of M = 512 .. 4096, K = 3072 .. 15360, N = 3072 .. 21504: a 128 x 128 tile
+// (two per CU) sustains the 256 x 256 tile's throughput and wins whenever the
+// 256 x 256 grid leaves CUs idle or has a partial last round.
+// CONVROT_W4A16_TILE=256x256|256x128|128x256|128x128 forces one.
+struct TiledCand {
+  int bm, bn, per_cu;
+  double rate;
+};
+constexpr TiledCand kTiledCands[] = {
+    {256, 256, 1, 1.00},
+    {256, 128, 1, 0.85},
+    {128, 256, 1, 0.75},
+    {128, 128, 2, 1.00},
+};
+constexpr double kTiledFixed = 1.5;
+constexpr double kTiledUsPerUnit = 4.0;
+
+struct TiledPlan {
+  int pick;   // index into kTiledCands
+  double us;  // modelled launch time
+};
+
+TiledPlan tiled_plan(int64_t M, int64_t N, int64_t K) {
+  const int64_t cus = device_cus();
+  const int64_t kb = (K + 127) / 128;
+  int bm = 0, bn = 0;
+  if (const char* env = getenv("CONVROT_W4A16_TILE")) sscanf(env, "%dx%d", &bm, &bn);
+  TiledPlan best{3, 1e300};
+  for (int i = 0; i < (int)(sizeof(kTiledCands) / sizeof(kTiledCands[0])); ++i) {
+    const TiledCand& c = kTiledCands[i];
+    if (bm && (c.bm != bm || c.bn != bn)) continue;
+    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    const int64_t per_cu = (tiles + cus - 1) / cus;
+    const double units = (double)per_cu * ((double)c.bm * c.bn / 65536.0 * (double)kb) / c.rate +
+                         kTiledFixed * (double)((per_cu + c.per_cu - 1) / c.per_cu);
+    if (units * kTiledUsPerUnit < best.us) best = {i, units * kTiledUsPerUnit};
+  }
+  return best;
+}
+
+template <int ADT, int ODT>
+hipError_t launch_tiled(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
+                        int64_t N, int64_t K, void* out, hipStream_t stream) {
+  const int pick = tiled_plan(M, N, K).pick;
+  switch (pick) {
+    case 0: return launch_tiled_t<ADT, ODT, 256, 256>(act, wq, ws, bias, M, N, K, out, stream);
+    case 1: return launch_tiled_t<ADT, ODT, 256, 128>(act, wq, ws, bias, M, N, K, out, stream);
+    case 2: return launch_tiled_t<ADT, ODT, 128, 256>(act, wq, ws, bias, M, N, K, out, stream);
+    default: return launch_tiled_t<ADT, ODT, 128, 128>(act, wq, ws, bias, M, N, K, out, stream);
+  }
+}
+
 template <int ADT, int ODT, int FM, int NB, int SPLIT, int KPW>
 hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M, int64_t N,
                     int64_t K, void* out, hipStream_t stream) {
@@ -187,19 +463,27 @@ hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const f
 // 12288->3072):
 //   A (1,2,8,3)  many weight tiles, or 16 < M <= 32 (two token tiles)
 //   B (1,1,16,4) few weight tiles and long K, M <= 16
-//   F (4,2,4,2)  M > 32
+//   F (4,2,4,2)  M > 32 unless the tiled kernel is modelled faster
+//   T            the tiled kernel (256 / 128 edges), M >= kTiledMinM
 // At M = 1 both stream the 18.9 MB weight matrix in ~8 us (~2.3 TB/s), where
 // a plain 19 MB device copy takes ~10 us; the rest is weight expansion
-// (~2 VALU ops per code) and the launch/tail.  CONVROT_W4A16_CFG=A|B|F
+// (~2 VALU ops per code) and the launch/tail.  CONVROT_W4A16_CFG=A|B|F|T
 // overrides (tuning sweeps).
+constexpr int64_t kTiledMinM = 64;
 template <int ADT, int ODT>
 hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
                         int64_t N, int64_t K, void* out, hipStream_t stream) {
   const int64_t nblocks = (N + 15) / 16;
   char cfg = M > 32 ? 'F' : (M <= 16 && nblocks < 512 ? 'B' : 'A');
+  // From kTiledMinM rows on, the tiled kernel takes over where its modelled
+  // time beats split F's: F sustains ~280 TFLOP/s over a ~5 us floor, the
+  // tiled kernel needs enough tiles to fill the CUs (M = 128: N = 12288 runs
+  // 28 us tiled against 41 us in F, N = 3072 has 24 tiles and stays in F).
+  if (M >= kTiledMinM && tiled_plan(M, N, K).us < 2.0 * (double)M * (double)N * (double)K / 280e6 + 5.0) cfg = 'T';
   if (const char* env = getenv("CONVROT_W4A16_CFG"))
-    if (env[0] == 'A' || env[0] == 'B' || env[0] == 'F') cfg = env[0];
+    if (env[0] == 'A' || env[0] == 'B' || env[0] == 'F' || env[0] == 'T') cfg = env[0];
   switch (cfg) {
+    case 'T': return launch_tiled<ADT, ODT>(act, wq, ws, bias, M, N, K, out, stream);
     case 'A': return launch_t<ADT, ODT, 1, 2, 8, 3>(act, wq, ws, bias, M, N, K, out, stream);
     case 'B': return launch_t<ADT, ODT, 1, 1, 16, 4>(act, wq, ws, bias, M, N, K, out, stream);
     default: return launch_t<ADT, ODT, 4, 2, 4, 2>(act, wq, ws, bias, M, N, K, out, stream);

@@ -100,6 +100,13 @@ def test_gemm_validation(lib):
     assert lib.convrot_w4a16_gemm(None, 0, None, None, None, 4, 8, 64, None, BF16, None) == 1
     assert _err(lib) == "MPP W4A16 requires float16 or bfloat16 activation, got float32"
     assert lib.convrot_w4a16_gemm(None, BF16, None, None, None, 4, 8, 65600, None, BF16, None) == 2
+    # packed weights of 2 GiB or more: the kernels' buffer offsets are 32-bit signed
+    big_n = (1 << 31) // ((65536 // 128) * 1024) * 16  # ceil(K/128) * ceil(N/16) KB == 2 GiB
+    assert lib.convrot_w4a16_gemm(None, BF16, None, None, None, 4, big_n, 65536, None, BF16, None) == 2
+    assert _err(lib) == f"W4A16 GEMM packed weights are limited to 2 GiB (N={big_n} K=65536)"
+    assert lib.convrot_w4a4_gemm(None, 1, None, None, None, None, 4, big_n, 65536, None, BF16, None) == 2
+    assert lib.convrot_w4a4_gemm(None, 1, None, None, None, None, 4, big_n - 16, 65536, None, BF16, None) == 1
+    assert _err(lib) == "null pointer argument"
 
 
 def test_repack_validation(lib):

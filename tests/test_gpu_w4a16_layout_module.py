@@ -67,7 +67,7 @@ def test_w4a16_config4(orc, dev, M, K, N):
     _w4a16_check(orc, dev, act, "bfloat16", w, ws, b, "bfloat16")
 
 
-@pytest.mark.parametrize("cfg", ["A", "B", "F"])
+@pytest.mark.parametrize("cfg", ["A", "B", "F", "T"])
 @pytest.mark.parametrize("M,K,N", [(17, 96, 46), (37, 2688, 530), (1, 4000, 33), (5, 12288, 3072)])
 def test_w4a16_every_split(orc, dev, monkeypatch, cfg, M, K, N):
     """Each W4A16 work split (forced through CONVROT_W4A16_CFG) on ragged M/N and on K that is
@@ -79,6 +79,36 @@ def test_w4a16_every_split(orc, dev, monkeypatch, cfg, M, K, N):
     b = rng.normal(0, 0.02, size=(N,)).astype(np.float32)
     act = normal_input(M + K + N, (M, K), "bfloat16", orc)
     _w4a16_check(orc, dev, act, "bfloat16", w, ws, b, "bfloat16")
+
+
+def _w4a16_tiled_case(orc, dev, act_dtype, out_dtype, M, K, N):
+    rng = np.random.default_rng(M * 17 + K * 3 + N)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.01, size=(N,)).astype(np.float32)
+    b = rng.normal(0, 0.02, size=(N,)).astype(np.float32)
+    act = outlier_input(M + K + N, (M, K), act_dtype, orc)
+    _w4a16_check(orc, dev, act, act_dtype, w, ws, b, out_dtype)
+
+
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128"])
+@pytest.mark.parametrize("M,K,N", [(256, 128, 256), (300, 2688, 530), (1100, 4000, 2100), (129, 96, 8)])
+def test_w4a16_tiled(orc, dev, monkeypatch, tile, M, K, N):
+    """Every tile of the tiled kernel (M >= 128, forced through CONVROT_W4A16_TILE): partial
+    tiles in M and N, K ending inside a 128-feature block, more tiles than the eight-way XCD
+    interleave covers, and an incomplete group of four tile rows."""
+    monkeypatch.setenv("CONVROT_W4A16_CFG", "T")
+    monkeypatch.setenv("CONVROT_W4A16_TILE", tile)
+    _w4a16_tiled_case(orc, dev, "bfloat16", "bfloat16", M, K, N)
+
+
+@pytest.mark.parametrize("tile", ["256x256", "128x128"])
+@pytest.mark.parametrize("act_dtype,out_dtype", [("bfloat16", "float32"), ("float16", "float16"),
+                                                  ("float16", "bfloat16"), ("float16", "float32")])
+def test_w4a16_tiled_dtypes(orc, dev, monkeypatch, tile, act_dtype, out_dtype):
+    """Activation and output dtypes of the tiled kernel on a ragged shape."""
+    monkeypatch.setenv("CONVROT_W4A16_CFG", "T")
+    monkeypatch.setenv("CONVROT_W4A16_TILE", tile)
+    _w4a16_tiled_case(orc, dev, act_dtype, out_dtype, 300, 2688, 530)
 
 
 # ---------------------------------------------------------------- layouts
