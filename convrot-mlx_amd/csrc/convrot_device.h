@@ -115,6 +115,13 @@ __device__ __forceinline__ void dma16(i32x4_sgpr rsrc, uint32_t voffset, uint32_
   asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc), "{m0}"(lds_addr) : "memory");
 }
 
+// The same with 4 bytes per lane (buffer_load_dword ... lds): LDS at
+// lds_addr + 4 * lane.  Each dword is range-checked on its own, so a ragged
+// end reads zeros exactly from the first dword past `bytes`.
+__device__ __forceinline__ void dma4(i32x4_sgpr rsrc, uint32_t voffset, uint32_t lds_addr) {
+  asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc), "{m0}"(lds_addr) : "memory");
+}
+
 // s_waitcnt on vmcnt only (expcnt and lgkmcnt left at "no wait").
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

@@ -214,17 +214,22 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_kernel(
 // bytes) and written back as 16-byte stores covering whole row segments; the
 // MFMA accumulator layout (4 consecutive n of one m per lane) would otherwise
 // produce 32-byte write fragments.  float32 outputs store 4 values per lane.
-template <int ODT, int TM, int TN, int SHIFT>
+//
+// Operands: xs[m], ws[n] and bias[n] come from global memory, or (LDS_OPS)
+// from the tile's LDS copies xs[m - m0], ws[n - n0], bias[n - n0] (rows and
+// columns past M / N hold zeros there and are never stored).
+template <int ODT, int TM, int TN, int SHIFT, bool LDS_OPS = false>
 __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], uint8_t* region, int lane,
                                          int mw, int nw, int M, int N, const float* __restrict__ xscales,
                                          const float* __restrict__ wscales, const float* __restrict__ bias,
-                                         void* __restrict__ out) {
+                                         void* __restrict__ out, int m0 = 0, int n0 = 0) {
   constexpr int FM = TM / 16, FN = TN / 16;
   float xs[FM];
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
     const int m = mw + fm * 16 + (lane & 15);
-    xs[fm] = xscales[m < M ? m : M - 1];
+    if constexpr (LDS_OPS) xs[fm] = xscales[m - m0];
+    else xs[fm] = xscales[m < M ? m : M - 1];
   }
   if constexpr (ODT == kF32) {
     const bool vec_ok = (N & 3) == 0;
@@ -233,11 +238,18 @@ __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], u
       const int n = nw + fn * 16 + 4 * (lane >> 4);
       if (n >= N) continue;
       float wsv[4], bv[4];
+      if constexpr (LDS_OPS) {
+        const float4 w4 = *(const float4*)(wscales + (n - n0));
+        const float4 b4 = *(const float4*)(bias + (n - n0));
+        wsv[0] = w4.x, wsv[1] = w4.y, wsv[2] = w4.z, wsv[3] = w4.w;
+        bv[0] = b4.x, bv[1] = b4.y, bv[2] = b4.z, bv[3] = b4.w;
+      } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int nn = n + r < N ? n + r : N - 1;
-        wsv[r] = wscales[nn];
-        bv[r] = bias ? bias[nn] : 0.0f;
+        for (int r = 0; r < 4; ++r) {
+          const int nn = n + r < N ? n + r : N - 1;
+          wsv[r] = wscales[nn];
+          bv[r] = bias ? bias[nn] : 0.0f;
+        }
       }
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
@@ -262,11 +274,18 @@ __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], u
     for (int fn = 0; fn < FN; ++fn) {
       const int nl = fn * 16 + 4 * (lane >> 4);
       float wsv[4], bv[4];
+      if constexpr (LDS_OPS) {
+        const float4 w4 = *(const float4*)(wscales + (nw + nl - n0));
+        const float4 b4 = *(const float4*)(bias + (nw + nl - n0));
+        wsv[0] = w4.x, wsv[1] = w4.y, wsv[2] = w4.z, wsv[3] = w4.w;
+        bv[0] = b4.x, bv[1] = b4.y, bv[2] = b4.z, bv[3] = b4.w;
+      } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int nn = min(nw + nl + r, N - 1);
-        wsv[r] = wscales[nn];
-        bv[r] = bias ? bias[nn] : 0.0f;
+        for (int r = 0; r < 4; ++r) {
+          const int nn = min(nw + nl + r, N - 1);
+          wsv[r] = wscales[nn];
+          bv[r] = bias ? bias[nn] : 0.0f;
+        }
       }
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
@@ -341,14 +360,20 @@ struct DmaEngine {
   static constexpr int A_FRAGS = (BM / 16) * 2, B_FRAGS = BN / 16;
   static constexpr int LOADS = A_FRAGS + B_FRAGS;
   static constexpr int STAGE_BYTES = LOADS * 1024;
-  static constexpr int SMEM_BYTES = STAGES * STAGE_BYTES;
+  // Epilogue operands of the tile, loaded into LDS with the first k-blocks:
+  // xs[m0 .. m0+255], ws[n0 .. n0+255], bias[n0 .. n0+255] (1 KB each).
+  static constexpr int EPI_OFF = STAGES * STAGE_BYTES;
+  static constexpr int EPI_BYTES = 3 * 1024;
+  static constexpr int EPI_DMAS = 3 * 4;  // 256-byte dword DMAs
+  static constexpr int SMEM_BYTES = EPI_OFF + EPI_BYTES;
   static constexpr int LPW = LOADS / NW;  // DMA instructions per wave per k-block
   static constexpr int APW = A_FRAGS / NW, BPW = B_FRAGS / NW;  // of which activation / weight
   static constexpr int SHIFT = 4;         // weights unpacked x16: acc = 16 * dot
   static constexpr int STAGING = TM * (TN * 2 + 16);  // epilogue LDS bytes per wave
   static_assert(LOADS % NW == 0, "fragment loads must split evenly over waves");
   static_assert(A_FRAGS % NW == 0 && B_FRAGS % NW == 0 && APW % 2 == 0, "each wave loads APW (even) + BPW pieces");
-  static_assert(NW * STAGING <= SMEM_BYTES, "epilogue staging exceeds LDS");
+  static_assert(NW * STAGING <= EPI_OFF, "epilogue staging exceeds the ring");
+  static_assert(BM <= 256 && BN <= 256, "one KB of LDS per epilogue operand");
   static_assert(STAGES >= 3 && (STAGES - 1) * LPW <= 63, "ring depth: vmcnt counts at most 63 DMAs");
 
   // Fragments of one k-block held in registers: packed weights (both k-steps)
@@ -380,6 +405,26 @@ struct DmaEngine {
   }
 
   __device__ __forceinline__ uint8_t* staging() const { return smem + wave * STAGING; }
+  __device__ __forceinline__ const float* epi_xs() const { return (const float*)(smem + EPI_OFF); }
+  __device__ __forceinline__ const float* epi_ws() const { return (const float*)(smem + EPI_OFF + 1024); }
+  __device__ __forceinline__ const float* epi_bias() const { return (const float*)(smem + EPI_OFF + 2048); }
+
+  // Load the tile's epilogue operands into LDS: 12 dword DMAs of 256 bytes,
+  // DMA d by wave d % NW.  Entries past M or N, and all of a missing
+  // bias, read as zero.  Issued before the run's prologue: vmcnt retires in
+  // issue order, so the run's first DMA wait also retires these, and the
+  // barrier after the run publishes them to every wave.  The area must not be
+  // read by a previous epilogue when they are issued.
+  __device__ __forceinline__ void issue_epi(const float* xscales, const float* wscales, const float* bias, int M,
+                                            int N, int m0, int n0) {
+    for (int d = wave; d < EPI_DMAS; d += NW) {  // array d / 4, quarter d % 4
+      const int arr = d >> 2;
+      const float* base = arr == 0 ? xscales + m0 : arr == 1 ? wscales + n0 : (bias ? bias + n0 : wscales);
+      const int count = arr == 0 ? M - m0 : (arr == 1 || bias) ? N - n0 : 0;
+      const i32x4_sgpr r = buffer_rsrc(base, (uint32_t)count * 4u);
+      dma4(r, (uint32_t)((d & 3) * 256 + lane * 4), smem_addr + (uint32_t)(EPI_OFF + arr * 1024 + (d & 3) * 256));
+    }
+  }
 
   // Point the loads at the output tile whose top-left corner is (m0, n0).
   __device__ __forceinline__ void set_tile(const int8_t* act, const uint8_t* wq, int M, int K, int nblocks,
@@ -573,6 +618,7 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
   tile_origin(logical, tiles_m, tiles_n, BM, BN, m0, n0);
 
   e.set_tile(act, wq, M, K, nblocks, kblocks, m0, n0);
+  e.issue_epi(xscales, wscales, bias, M, N, m0, n0);
   i32x4 acc[E::FN][E::FM];
 #pragma unroll
   for (int a = 0; a < E::FN; ++a)
@@ -580,8 +626,8 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
     for (int b = 0; b < E::FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
   e.run(0, kblocks, acc);
   __syncthreads();  // all waves done with the LDS ring before it is reused for output staging
-  epilogue<ODT, E::TM, E::TN, E::SHIFT>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M, N,
-                                        xscales, wscales, bias, out);
+  epilogue<ODT, E::TM, E::TN, E::SHIFT, true>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M,
+                                              N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, m0, n0);
 }
 
 // ---- stream-K
@@ -773,6 +819,7 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
     tile_origin(tb + t, tiles_m, tiles_n, BM, BN, m0, n0);
     if (!prefetched) {
       e.set_tile(act, wq, M, K, nblocks, kblocks, m0, n0);
+      e.issue_epi(xscales, wscales, bias, M, N, m0, n0);
       e.prologue(k0, k1 - k0);
     }
 #pragma unroll
@@ -799,6 +846,7 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
         int nm0, nn0;
         tile_origin(tb + nt, tiles_m, tiles_n, BM, BN, nm0, nn0);
         e.set_tile(act, wq, M, K, nblocks, kblocks, nm0, nn0);
+        e.issue_epi(xscales, wscales, bias, M, N, nm0, nn0);
         e.prologue(nk0, nk1 - nk0);
         prefetched = true;
         pending = flag;
@@ -818,8 +866,8 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
           sk_add_partial<FN, FM>(partials + (int64_t)(group * P + q) * (BM * BN * 4) + wave_off, e.lane, acc);
       }
       __syncthreads();  // ring -> epilogue staging
-      epilogue<ODT, E::TM, E::TN, E::SHIFT>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M, N,
-                                            xscales, wscales, bias, out);
+      epilogue<ODT, E::TM, E::TN, E::SHIFT, true>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN,
+                                                  M, N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, m0, n0);
       __syncthreads();  // staging -> next item's DMA
     }
     t = nt;

@@ -166,6 +166,32 @@ def test_stream_k(orc, dev, monkeypatch, tile, seed, M, K, N, sk_min):
         _assert_exact(from_dev(out)[rows], expected, f"tile {tile} call {call}")
 
 
+@pytest.mark.parametrize("sk", [False, True], ids=["dp", "sk"])
+@pytest.mark.parametrize("tile", ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2"])
+@pytest.mark.parametrize("out_dtype", ["float32", "float16"])
+def test_epilogue_operands_without_bias(orc, dev, monkeypatch, tile, sk, out_dtype):
+    """The DMA kernels stage xs / ws / bias of each tile in LDS: ragged M and N that are not
+    multiples of 4 (the staged copies end mid-vector) and a missing bias (read as zeros)."""
+    api = _api()
+    monkeypatch.setenv("CONVROT_GEMM_TILE", tile)
+    monkeypatch.setenv("CONVROT_GEMM_SK", "1" if sk else "0")
+    monkeypatch.setenv("CONVROT_GEMM_SK_MIN", "1")
+    monkeypatch.delenv("CONVROT_GEMM_NO_DMA", raising=False)
+    M, K, N = 301, 384, 531
+    rng = np.random.default_rng(61)
+    a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    dt = {"float16": torch.float16, "float32": torch.float32}[out_dtype]
+    out = api.hip_w4a4_int8_matmul(torch.from_numpy(a).to(dev), _dev_u8(orc.codes_to_cdna4(w), dev),
+                                   torch.from_numpy(xs).to(dev), torch.from_numpy(ws).to(dev), None,
+                                   output_dtype=dt, out_features=N)
+    torch.cuda.synchronize()
+    expected = orc.w4a4_matmul_codes(a, w, xs, ws, np.zeros(N, np.float32), out_dtype)
+    _assert_exact(from_dev(out), expected, f"tile {tile} sk={sk} {out_dtype}")
+
+
 def test_kn_layout_entry_matches(orc, dev):
     """mpp_w4a4_matmul with the reference's K x packed-N weight (repacked on device)."""
     api = _api()
