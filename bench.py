@@ -58,7 +58,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--sets", type=int, default=3, help="buffer sets cycled to defeat the Infinity Cache")
-    ap.add_argument("--cpu-rows", type=int, default=96, help="rows per linear in the CPU-baseline sample")
+    ap.add_argument("--cpu-rows", type=int, default=288, help="rows per linear in the CPU-baseline sample (~11 s)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the dense control and the config-3/4/5 figures")
