@@ -371,7 +371,7 @@ struct DmaEngine {
   static constexpr int SHIFT = 4;         // weights unpacked x16: acc = 16 * dot
   static constexpr int STAGING = TM * (TN * 2 + 16);  // epilogue LDS bytes per wave
   static_assert(LOADS % NW == 0, "fragment loads must split evenly over waves");
-  static_assert(A_FRAGS % NW == 0 && B_FRAGS % NW == 0 && APW % 2 == 0, "each wave loads APW (even) + BPW pieces");
+  static_assert(A_FRAGS % NW == 0 && B_FRAGS % NW == 0, "each wave loads APW + BPW pieces");
   static_assert(NW * STAGING <= EPI_OFF, "epilogue staging exceeds the ring");
   static_assert(BM <= 256 && BN <= 256, "one KB of LDS per epilogue operand");
   static_assert(STAGES >= 3 && (STAGES - 1) * LPW <= 63, "ring depth: vmcnt counts at most 63 DMAs");
@@ -387,9 +387,10 @@ struct DmaEngine {
   uint32_t smem_addr;
   int lane, wave, wm, wn;
   // This wave's loads: activation pieces j = wave APW + i (rows 8j .. 8j+7)
-  // and weight blocks j = wave BPW + i.  Per-lane byte offsets: va[j & 1]
-  // for activations (the row swizzle flips with the parity of j, which is
-  // i's since APW is even), vb for weights; the rest of each offset is
+  // and weight blocks j = wave BPW + i.  Per-lane byte offsets: va[i & 1]
+  // for activations (the row swizzle flips with the parity of j; set_tile
+  // swaps the pair where APW and wave are odd, so that i's parity selects
+  // it), vb for weights; the rest of each offset is
   // wave-uniform and added at issue time (it changes with k, so the sums are
   // never hoisted into registers).
   i32x4_sgpr ra, rw;
@@ -439,8 +440,9 @@ struct DmaEngine {
     // swz(row) = (L >> 3) ^ (j & 1).  The row term 8 j K stays in the
     // per-lane offset so rows at or beyond M fail the buffer range check.
     const int rl = lane >> 3, c = lane & 7;
-    va[0] = (uint32_t)(rl * K + 16 * (c ^ rl));
-    va[1] = (uint32_t)(rl * K + 16 * (c ^ rl ^ 1));
+    const int flip = (APW & 1) ? (wave & 1) : 0;  // parity of j = wave APW + i, beyond i's
+    va[0] = (uint32_t)(rl * K + 16 * (c ^ rl ^ flip));
+    va[1] = (uint32_t)(rl * K + 16 * (c ^ rl ^ flip ^ 1));
     vb = (uint32_t)lane * 16u;
     krow = 8u * (uint32_t)K;
     a_kstride = 128u;
@@ -920,16 +922,24 @@ namespace {
 // runs one workgroup per CU; 128x128 fits two per CU).  `sk` marks the tiles
 // the stream-K kernel runs well: the 256x256 one spills registers there and
 // 128x128 pieces are too short.
+//
+// The 192x128 tile moves more L2 bytes per MFMA than the 256x256 one and
+// sustains 0.75 of its rate with every CU busy, but 0.83 when its grid is a
+// single round that leaves CUs idle (1536 tokens: 192 tiles at N = 3072,
+// 21.2 us against 24.2-25.4 us for every other tile).
 struct Cand {
   Tile t;
   int per_cu;
   double eff;
+  double eff_partial;  // eff when the grid is one round of fewer tiles than CUs
   bool sk;
+  bool dma_only;  // no register-staged (packed-activation) variant
 };
-constexpr Cand kCands[4] = {{{256, 256, 2, 4, 3}, 1, 1.0, false},
-                            {{128, 256, 2, 4, 3}, 1, 0.85, true},
-                            {{256, 128, 4, 2, 3}, 1, 0.8, true},
-                            {{128, 128, 2, 2, 3}, 2, 0.8, false}};
+constexpr Cand kCands[5] = {{{256, 256, 2, 4, 3}, 1, 1.0, 1.0, false, false},
+                            {{128, 256, 2, 4, 3}, 1, 0.85, 0.85, true, false},
+                            {{256, 128, 4, 2, 3}, 1, 0.8, 0.8, true, false},
+                            {{128, 128, 2, 2, 3}, 2, 0.8, 0.8, false, false},
+                            {{192, 128, 4, 2, 3}, 1, 0.75, 0.83, false, true}};
 // Fixed cost of the stream-K fix-up (ticket, partial store and reload, the
 // extra pipeline ramp of each piece, the idle tail while owners wait), in
 // units of one 256x256 k-block; fitted to M = 512 .. 4608 FLUX shapes.
@@ -945,7 +955,8 @@ double block_cost(const Cand& c) { return (double)c.t.bm * c.t.bn / 65536.0 / c.
 // steps of 1/per_cu of a tile.
 double dp_time(const Cand& c, int64_t tiles, int64_t kb, int cus) {
   const int64_t steps = (tiles * c.per_cu + cus - 1) / cus;  // ceil(tiles per CU * per_cu)
-  return (double)steps / c.per_cu * (double)kb * block_cost(c);
+  const double partial = tiles < cus ? c.eff / c.eff_partial : 1.0;
+  return (double)steps / c.per_cu * (double)kb * block_cost(c) * partial;
 }
 
 double sk_time(const Cand& c, int64_t tiles, int64_t kb, int cus, int min_iters) {
@@ -987,7 +998,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_sk) {
   for (const Cand& c : kCands) {
     const bool match = forced && c.t.bm == forced->bm && c.t.bn == forced->bn && c.t.wm == forced->wm &&
                        c.t.wn == forced->wn && c.t.stages == forced->stages;
-    if (forced && !match) continue;
+    if ((forced && !match) || (c.dma_only && !allow_sk)) continue;
     const int64_t tiles = ((M + c.t.bm - 1) / c.t.bm) * ((N + c.t.bn - 1) / c.t.bn);
     const double td = dp_time(c, tiles, kb, cus);
     const double ts = sk_time(c, tiles, kb, cus, min_iters);
@@ -1106,6 +1117,7 @@ hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const f
     CONVROT_DMA(256, 128, 4, 2, 3)
     CONVROT_DMA(128, 256, 2, 4, 3)
     CONVROT_DMA(128, 128, 2, 2, 3)
+    CONVROT_DMA(192, 128, 4, 2, 3)
 #undef CONVROT_DMA
   }
 #define CONVROT_TILE(BM_, BN_, WM_, WN_)                    \

@@ -108,8 +108,8 @@ def test_odd_shapes_bf16(orc, dev, seed, M, K, N):
 
 # Tiles the automatic choice picks (BMxBN, waves WMxWN), plus 2x2-wave register-staged
 # variants that are only reached through the override.
-_TILES = ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2", "256x256w2x2", "256x128w2x2",
-          "128x256w2x2", "256x256w4x2"]
+_TILES = ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2", "192x128w4x2", "256x256w2x2",
+          "256x128w2x2", "128x256w2x2", "256x256w4x2"]
 
 
 @pytest.mark.parametrize("no_dma", [False, True], ids=["dma", "regstaged"])
@@ -134,7 +134,7 @@ def test_every_tile_config(orc, dev, monkeypatch, tile, no_dma, seed, M, K, N):
         _assert_exact(got, expected, f"{name} tile {tile}")
 
 
-@pytest.mark.parametrize("tile", ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2"])
+@pytest.mark.parametrize("tile", ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2", "192x128w4x2"])
 @pytest.mark.parametrize(
     "seed,M,K,N,sk_min",
     [(51, 300, 2688, 530, 1),    # tiles split into up to 21 one-k-block pieces
@@ -167,7 +167,7 @@ def test_stream_k(orc, dev, monkeypatch, tile, seed, M, K, N, sk_min):
 
 
 @pytest.mark.parametrize("sk", [False, True], ids=["dp", "sk"])
-@pytest.mark.parametrize("tile", ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2"])
+@pytest.mark.parametrize("tile", ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2", "192x128w4x2"])
 @pytest.mark.parametrize("out_dtype", ["float32", "float16"])
 def test_epilogue_operands_without_bias(orc, dev, monkeypatch, tile, sk, out_dtype):
     """The DMA kernels stage xs / ws / bias of each tile in LDS: ragged M and N that are not
