@@ -20,6 +20,8 @@ Prints ONE JSON line (the driver's contract).  Extra keys:
   cpu_baseline   the CPU oracle (C restatement, 1 thread) on a bounded row sample
   dense_bf16_control  torch bf16 linear (hipBLASLt) on the same shapes
   flux_m4608     config 3's 4608x3072->12288 G=256 complete-path figure
+  flux_m4608_column_shard_8  the same linear at one GPU's share of an 8-way column
+                 split (4608x3072->1536), the per-GPU work of the sharded design
   w4a16_config4  config 4 (W4A16, M in {1, 8, 32}): int4-weight GB/s of the GEMM and
                  the complete path (rotation + GEMM), replayed from a HIP graph
   flux_dit_config5  config 5: one step of a random-init FLUX.1-dev DiT (1536 tokens),
@@ -242,6 +244,8 @@ def main() -> int:
         result["dense_bf16_control"]["convrot_speedup"] = round(
             result["dense_bf16_control"]["ms_per_step"] / ms_per_step, 3)
         result["flux_m4608"] = config3_figure(torch, core, nat, dev)
+        # One GPU's share of an 8-way column split of the same linear (no collective runs).
+        result["flux_m4608_column_shard_8"] = config3_figure(torch, core, nat, dev, N=CONFIG3_MLP["N"] // 8)
         result["w4a16_config4"] = w4a16_figure(torch, core, nat, dev)
         if not args.no_config5:
             from examples.flux1_dev.dit import config5_figure
@@ -280,10 +284,12 @@ def dense_control(torch, layers, M, shapes):
             "pct_bf16_peak": round(100 * flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 2)}
 
 
-def config3_figure(torch, core, nat, dev):
-    """Config 3's MLP-up linear, 4608x3072->12288, G=256: complete path, 3 buffer sets."""
+def config3_figure(torch, core, nat, dev, N=None):
+    """Config 3's MLP-up linear, 4608x3072->12288, G=256: complete path, 3 buffer sets.
+    With N given, the same linear at that output width (one GPU's column shard)."""
     c = CONFIG3_MLP
-    M, K, N, G = c["M"], c["K"], c["N"], c["G"]
+    M, K, G = c["M"], c["K"], c["G"]
+    N = c["N"] if N is None else N
     gen = torch.Generator(device=dev)
     gen.manual_seed(3)
     lib, stream = nat.load(), nat.stream_of(dev)
@@ -315,7 +321,7 @@ def config3_figure(torch, core, nat, dev):
     torch.cuda.synchronize()
     us = (time.perf_counter() - t0) * 1e6 / n
     tops = 2 * M * N * K / (us * 1e-6) / 1e12
-    return {"shape": "4608x3072->12288 G=256", "us_per_linear": round(us, 2), "tops": round(tops, 2),
+    return {"shape": f"{M}x{K}->{N} G={G}", "us_per_linear": round(us, 2), "tops": round(tops, 2),
             "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2)}
 
 

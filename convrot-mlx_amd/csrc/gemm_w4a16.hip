@@ -461,8 +461,11 @@ hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const f
 // Configurations (FM token tiles, NB weight tiles, SPLIT waves, KPW blocks
 // per wave), measured on the config-4 shapes (M = 1, 8, 32; 3072->12288 and
 // 12288->3072):
-//   A (1,2,8,3)  many weight tiles, or 16 < M <= 32 (two token tiles)
-//   B (1,1,16,4) few weight tiles and long K, M <= 16
+//   A (1,2,8,3)  more than 256 weight tiles (N > 4096), or 16 < M <= 32
+//   B (1,1,16,4) at most 256 weight tiles, M <= 16 (at M = 1: 3072->3072
+//                4.3 us vs 4.9, 12288->3072 8.7 vs 12.3; while 3072->6144
+//                takes 5.8 us in A against 8.1 in B, whose 16 waves per tile
+//                outnumber K = 3072's 24 k-blocks)
 //   F (4,2,4,2)  M > 32 unless the tiled kernel is modelled faster
 //   T            the tiled kernel (256 / 128 edges), M >= kTiledMinM
 // At M = 1 both stream the 18.9 MB weight matrix in ~8 us (~2.3 TB/s), where
@@ -474,7 +477,7 @@ template <int ADT, int ODT>
 hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
                         int64_t N, int64_t K, void* out, hipStream_t stream) {
   const int64_t nblocks = (N + 15) / 16;
-  char cfg = M > 32 ? 'F' : (M <= 16 && nblocks < 512 ? 'B' : 'A');
+  char cfg = M > 32 ? 'F' : (M <= 16 && nblocks <= 256 ? 'B' : 'A');
   // From kTiledMinM rows on, the tiled kernel takes over where its modelled
   // time beats split F's: F sustains ~280 TFLOP/s over a ~5 us floor, the
   // tiled kernel needs enough tiles to fill the CUs (M = 128: N = 12288 runs
