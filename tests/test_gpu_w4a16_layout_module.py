@@ -212,6 +212,45 @@ def test_w4a16_layer_group64_k2688(orc, dev, backend):
     assert (np.abs(got - ref) <= tol).all()
 
 
+_MANY_TOKENS = {}
+
+
+def _many_tokens_case(orc, K, N):
+    """Inputs and oracle of the many-token layer test (computed once per session)."""
+    if (K, N) not in _MANY_TOKENS:
+        rng = np.random.default_rng(20260823)
+        dense_w = orc.from_f32((rng.normal(size=(N, K)) * 0.02).astype(np.float32), "bfloat16")
+        dense_b = (rng.normal(size=(N,)) * 0.02).astype(np.float32)
+        values = outlier_input(31, (2, 256, K), "bfloat16", orc)
+        rot = orc.regular_hadamard(values.reshape(-1, K), "bfloat16", 64)
+        w_codes, ws = orc.prepare_codes(dense_w, "bfloat16", 64)
+        ref, _, mag = orc.w4a16_matmul_codes(rot, "bfloat16", w_codes, ws, dense_b, "float32")
+        _MANY_TOKENS[(K, N)] = (dense_w, dense_b, values, ws, ref, mag)
+    return _MANY_TOKENS[(K, N)]
+
+
+@pytest.mark.parametrize("cfg", [None, "T", "F"], ids=["auto", "tiled", "split"])
+def test_w4a16_layer_many_tokens(orc, dev, monkeypatch, cfg):
+    """ConvRotLinear (hip-w4a16) at 512 tokens, 1024 -> 3072, G=64: the automatic dispatch
+    (the tiled kernel at this size) and each kernel forced, against the oracle."""
+    api = _api()
+    if cfg is None:
+        monkeypatch.delenv("CONVROT_W4A16_CFG", raising=False)
+    else:
+        monkeypatch.setenv("CONVROT_W4A16_CFG", cfg)
+    monkeypatch.delenv("CONVROT_W4A16_TILE", raising=False)
+    K, N = 1024, 3072
+    dense_w, dense_b, values, ws, ref, mag = _many_tokens_case(orc, K, N)
+    qweight, wscales = api.quantize_convrot_weight(to_dev(dense_w, "bfloat16", dev), 64)
+    layer = api.ConvRotLinear(K, N, group_size=64, backend="hip-w4a16", device=dev)
+    layer.load_nk_weight(qweight, wscales, torch.from_numpy(dense_b).to(dev))
+    out = layer(to_dev(values, "bfloat16", dev))
+    assert tuple(out.shape) == (2, 256, N) and out.dtype == torch.bfloat16
+    got = orc.to_f32(from_dev(out).reshape(-1, N), "bfloat16")
+    tol = 2.0 ** -22 * K * mag * ws[None, :] + np.abs(ref) * 2.0 ** -8
+    assert (np.abs(got - ref) <= tol).all(), f"max excess {np.max(np.abs(got - ref) - tol)}"
+
+
 def test_w4a4_layer_group64_k2688(orc, dev):
     api = _api()
     rng = np.random.default_rng(2026082306)
