@@ -12,7 +12,7 @@ inputs and weights already resident in HBM.  Three independent buffer sets
 
 `value` comes from K steps launched back to back with no event markers in the
 queue; per-kernel durations come from HIP events around every launch over a
-pass of K steps run between the warm-up and the timed region.
+pass of max(K, 50) steps run between the warm-up and the timed region.
 
 Prints ONE JSON line (the driver's contract).  Extra keys:
   roofline       dominant kernel (the W4A4 GEMM) vs the INT8 MFMA peak
@@ -150,16 +150,18 @@ def main() -> int:
         step(i)
     torch.cuda.synchronize()
 
-    # Per-kernel durations: K steps with HIP events around every prep and GEMM
-    # launch, on the launch stream.  This pass runs before the timed region.
-    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in shapes] for _ in range(args.steps)]
+    # Per-kernel durations: max(K, 50) steps with HIP events around every prep
+    # and GEMM launch, on the launch stream.  This pass runs before the timed
+    # region, so that region also starts on a warm GPU when K and W are small.
+    ev_steps = max(args.steps, 50)
+    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in shapes] for _ in range(ev_steps)]
     torch.cuda.synchronize()
     t2 = time.perf_counter()
-    for i in range(args.steps):
+    for i in range(ev_steps):
         step(i, ev[i])
     torch.cuda.synchronize()
     t3 = time.perf_counter()
-    ms_per_step_events = (t3 - t2) * 1e3 / args.steps
+    ms_per_step_events = (t3 - t2) * 1e3 / ev_steps
 
     # Timed region: K steps back to back.  HIP event markers are kept out of it:
     # each one is a separate queue packet that costs ~4 us of dispatch gap, and 12
@@ -176,12 +178,12 @@ def main() -> int:
 
     prep_ms = np.zeros(len(shapes))
     gemm_ms = np.zeros(len(shapes))
-    for i in range(args.steps):
+    for i in range(ev_steps):
         for j in range(len(shapes)):
             prep_ms[j] += ev[i][j][0].elapsed_time(ev[i][j][1])
             gemm_ms[j] += ev[i][j][1].elapsed_time(ev[i][j][2])
-    prep_ms /= args.steps
-    gemm_ms /= args.steps
+    prep_ms /= ev_steps
+    gemm_ms /= ev_steps
     gemm_ops = np.array([2 * M * K * N for K, N in shapes], dtype=np.float64)
     gemm_tops = gemm_ops.sum() / (gemm_ms.sum() * 1e-3) / 1e12
     prep_bytes = np.array([3 * M * K + 4 * M for K, _ in shapes], dtype=np.float64)  # bf16 in, int8 out, f32 scales
@@ -224,7 +226,7 @@ def main() -> int:
             "traffic": traffic,
             "per_shape_us": [round(t * 1e3, 2) for t in gemm_ms],
             "algorithmic": "2*M*N*K int ops per launch",
-            "timing": "HIP events around each launch, over a pass of K steps run just before the "
+            "timing": f"HIP events around each launch, over a pass of {ev_steps} steps run just before the "
                       f"timed region (that pass: {ms_per_step_events:.4f} ms per step with the event markers)",
         },
         "prep_roofline": {
