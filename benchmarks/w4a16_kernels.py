@@ -35,7 +35,7 @@ from convrot_mlx_amd import core  # noqa: E402
 DEFAULT_SHAPES = ["1536x3072x21504", "1536x15360x3072", "1024x3072x3072", "1024x3072x12288",
                   "1024x12288x3072", "512x3072x3072", "4096x3072x3072", "4096x4096x4096",
                   "256x3072x12288", "128x3072x12288", "128x3072x3072", "64x3072x12288"]
-DEFAULT_VARIANTS = "F,T256x256,T256x128,T128x256,T128x128,auto"
+DEFAULT_VARIANTS = "A,F,T256x256,T256x128,T128x256,T128x128,auto"
 WEIGHT_SETS = 4
 LAUNCHES = 16
 

@@ -461,32 +461,37 @@ hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const f
 // Configurations (FM token tiles, NB weight tiles, SPLIT waves, KPW blocks
 // per wave), measured on the config-4 shapes (M = 1, 8, 32; 3072->12288 and
 // 12288->3072):
-//   A (1,2,8,3)  more than 256 weight tiles (N > 4096), or 16 < M <= 32
+//   A (1,2,8,3)  more than 256 weight tiles (N > 4096), or M > 16 unless the
+//                tiled kernel is modelled faster
 //   B (1,1,16,4) at most 256 weight tiles, M <= 16 (at M = 1: 3072->3072
 //                4.3 us vs 4.9, 12288->3072 8.7 vs 12.3; while 3072->6144
 //                takes 5.8 us in A against 8.1 in B, whose 16 waves per tile
 //                outnumber K = 3072's 24 k-blocks)
-//   F (4,2,4,2)  M > 32 unless the tiled kernel is modelled faster
+//   C (2,2,8,2)  sweeps and tests only (one 32-token tile: slower than two of A)
+//   F (4,2,4,2)  sweeps and tests only (slower than A at every M measured)
 //   T            the tiled kernel (256 / 128 edges), M >= kTiledMinM
 // At M = 1 both stream the 18.9 MB weight matrix in ~8 us (~2.3 TB/s), where
 // a plain 19 MB device copy takes ~10 us; the rest is weight expansion
-// (~2 VALU ops per code) and the launch/tail.  CONVROT_W4A16_CFG=A|B|F|T
+// (~2 VALU ops per code) and the launch/tail.  CONVROT_W4A16_CFG=A|B|C|F|T
 // overrides (tuning sweeps).
 constexpr int64_t kTiledMinM = 64;
 template <int ADT, int ODT>
 hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
                         int64_t N, int64_t K, void* out, hipStream_t stream) {
   const int64_t nblocks = (N + 15) / 16;
-  char cfg = M > 32 ? 'F' : (M <= 16 && nblocks <= 256 ? 'B' : 'A');
+  char cfg = (M <= 16 && nblocks <= 256) ? 'B' : 'A';
   // From kTiledMinM rows on, the tiled kernel takes over where its modelled
-  // time beats split F's: F sustains ~280 TFLOP/s over a ~5 us floor, the
-  // tiled kernel needs enough tiles to fill the CUs (M = 128: N = 12288 runs
-  // 28 us tiled against 41 us in F, N = 3072 has 24 tiles and stays in F).
-  if (M >= kTiledMinM && tiled_plan(M, N, K).us < 2.0 * (double)M * (double)N * (double)K / 280e6 + 5.0) cfg = 'T';
+  // time beats split A's: A runs each 16-token tile at ~246 TFLOP/s over a
+  // ~5 us floor, the tiled kernel needs enough tiles to fill the CUs (M = 128:
+  // 3072 -> 12288 runs 28 us tiled against 45 us in A; 12288 -> 3072 has 24
+  // tiles of long K and stays in A up to M = 256, 78 us against 99 us).
+  const double m16 = (double)((M + 15) / 16 * 16);
+  if (M >= kTiledMinM && tiled_plan(M, N, K).us < 2.0 * m16 * (double)N * (double)K / 246e6 + 5.0) cfg = 'T';
   if (const char* env = getenv("CONVROT_W4A16_CFG"))
-    if (env[0] == 'A' || env[0] == 'B' || env[0] == 'F' || env[0] == 'T') cfg = env[0];
+    if (env[0] == 'A' || env[0] == 'B' || env[0] == 'C' || env[0] == 'F' || env[0] == 'T') cfg = env[0];
   switch (cfg) {
     case 'T': return launch_tiled<ADT, ODT>(act, wq, ws, bias, M, N, K, out, stream);
+    case 'C': return launch_t<ADT, ODT, 2, 2, 8, 2>(act, wq, ws, bias, M, N, K, out, stream);
     case 'A': return launch_t<ADT, ODT, 1, 2, 8, 3>(act, wq, ws, bias, M, N, K, out, stream);
     case 'B': return launch_t<ADT, ODT, 1, 1, 16, 4>(act, wq, ws, bias, M, N, K, out, stream);
     default: return launch_t<ADT, ODT, 4, 2, 4, 2>(act, wq, ws, bias, M, N, K, out, stream);

@@ -67,7 +67,7 @@ def test_w4a16_config4(orc, dev, M, K, N):
     _w4a16_check(orc, dev, act, "bfloat16", w, ws, b, "bfloat16")
 
 
-@pytest.mark.parametrize("cfg", ["A", "B", "F", "T"])
+@pytest.mark.parametrize("cfg", ["A", "B", "C", "F", "T"])
 @pytest.mark.parametrize("M,K,N", [(17, 96, 46), (37, 2688, 530), (1, 4000, 33), (5, 12288, 3072)])
 def test_w4a16_every_split(orc, dev, monkeypatch, cfg, M, K, N):
     """Each W4A16 work split (forced through CONVROT_W4A16_CFG) on ragged M/N and on K that is
