@@ -28,6 +28,7 @@ SIGNATURES = {
     "convrot_prepare": (_i32, [_vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
     "convrot_prepare_modulated": (_i32, [_vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _i64, ctypes.c_float, _vp,
                                          _vp, _vp]),
+    "convrot_prepare_gelu": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
     "convrot_w4a4_gemm": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_w4a16_gemm": (_i32, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_pack_int4": (_i32, [_vp, _i64, _i64, _vp, _vp]),

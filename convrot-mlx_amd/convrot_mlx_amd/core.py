@@ -177,6 +177,78 @@ def hip_fused_modulated_prepare(
     return out if output == "rotate" else (out, scales)
 
 
+def _gelu_operand(t: torch.Tensor) -> torch.Tensor:
+    """A producer operand as rows the kernel can read in place: unit feature stride, a row
+    stride that covers the row, 16-byte aligned rows (else a contiguous copy on the device)."""
+    esize = t.element_size()
+    if (t.stride(-1) != 1 or t.stride(0) < t.shape[1] or t.data_ptr() % 16 or (t.stride(0) * esize) % 16):
+        t = t.contiguous()
+    return t
+
+
+def _prepare_gelu(x: torch.Tensor, head: torch.Tensor | None, group_size: int,
+                  mode: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+    if head is not None and head.shape[-1] == 0:
+        head = None
+    nat.require_device(x, *([head] if head is not None else []))
+    x = _gelu_operand(x)
+    rows, x_features = x.shape
+    head_features = 0
+    if head is not None:
+        if head.shape[0] != rows:
+            raise ValueError(f"GELU producer head has {head.shape[0]} rows, x has {rows}")
+        if head.dtype != x.dtype:
+            raise ValueError(f"GELU producer head dtype {head.dtype} differs from x dtype {x.dtype}")
+        head = _gelu_operand(head)
+        head_features = head.shape[1]
+    features = head_features + x_features
+    if mode == nat.PREP_PACKED:
+        out = torch.empty((rows, features // 2), dtype=torch.uint8, device=x.device)
+    elif mode == nat.PREP_INT8:
+        out = torch.empty((rows, features), dtype=torch.int8, device=x.device)
+    else:
+        out = torch.empty((rows, features), dtype=x.dtype, device=x.device)
+    scales = None if mode == nat.PREP_ROTATE else torch.empty((rows,), dtype=torch.float32, device=x.device)
+    nat.check(
+        nat.load().convrot_prepare_gelu(
+            nat.ptr(head), head_features, head.stride(0) if head is not None else 0, nat.ptr(x), x_features,
+            x.stride(0), nat.dtype_code(x.dtype), rows, group_size, mode, nat.ptr(out), nat.ptr(scales),
+            nat.stream_of(x.device),
+        )
+    )
+    return out, scales
+
+
+def hip_fused_gelu_prepare(
+    x: torch.Tensor,
+    group_size: int = CONVROT_GROUP_SIZE,
+    *,
+    head: torch.Tensor | None = None,
+    output: str = "int8",
+):
+    """Fused producer: ConvRot preparation of `cat([head, gelu(x)], -1)`.
+
+    gelu is the tanh GELU (nn.GELU(approximate="tanh")) as a fixed float32 sequence,
+    rounded once to x's dtype; one kernel applies it, concatenates, rotates and
+    quantizes, reading x and head in place (row-strided views such as a slice of a
+    fused projection's output need no copy).  No counterpart in the reference, which
+    runs the activation and the concatenation as separate ops before ConvRotLinear.
+
+    x: [..., Kx]; head: None or [..., Kh] with the same leading shape and dtype;
+    Kx and Kh divisible by 16, Kh + Kx by group_size.  output as in
+    hip_fused_modulated_prepare.
+    """
+    modes = {"int8": nat.PREP_INT8, "packed": nat.PREP_PACKED, "rotate": nat.PREP_ROTATE}
+    if output not in modes:
+        raise ValueError(f"output must be one of {sorted(modes)}, got {output!r}")
+    x2d = x.reshape(-1, x.shape[-1])
+    h2d = None if head is None else head.reshape(-1, head.shape[-1])
+    features = x2d.shape[1] + (0 if h2d is None else h2d.shape[1])
+    _validate_fused(torch.empty((0, features), device="meta"), group_size, "GELU activation preparation")
+    out, scales = _prepare_gelu(x2d, h2d, group_size, modes[output])
+    return out if output == "rotate" else (out, scales)
+
+
 def hip_fused_prepare_convrot_activation(x: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE):
     """Rotation + absmax + A4 quantize + pack in one pass.
 
@@ -618,6 +690,28 @@ class ConvRotLinear(nn.Module):
                         self.out_features)
         else:
             rotated = _prepare_modulated(x2d, shift, scale, self.group_size, nat.PREP_ROTATE, eps)[0]
+            out = hip_w4a16_matmul(rotated, w, self.scales, self.bias, output_dtype=x.dtype,
+                                   out_features=self.out_features)
+        return out.reshape(*lead, self.out_features)
+
+    def forward_gelu(self, x: torch.Tensor, head: torch.Tensor | None = None) -> torch.Tensor:
+        """self(cat([head, gelu(x)], -1)) (or self(gelu(x))) with the tanh GELU and the
+        concatenation fused into the activation preparation (see hip_fused_gelu_prepare)."""
+        head_features = 0 if head is None else head.shape[-1]
+        if head_features + x.shape[-1] != self.in_features:
+            raise ValueError(f"ConvRotLinear expected K={self.in_features}, got {head_features} + {x.shape[-1]}")
+        if head is not None and head.shape[:-1] != x.shape[:-1]:
+            raise ValueError(f"GELU producer head {tuple(head.shape)} and x {tuple(x.shape)} differ in leading shape")
+        lead = x.shape[:-1]
+        x2d = x.reshape(-1, x.shape[-1])
+        h2d = None if head is None else head.reshape(-1, head_features)
+        w = self._device_weight()
+        if self.a4:
+            qact, xscales = _prepare_gelu(x2d, h2d, self.group_size, nat.PREP_INT8)
+            out = _w4a4(qact, nat.ACT_INT8, self.in_features, w, xscales, self.scales, self.bias, x.dtype,
+                        self.out_features)
+        else:
+            rotated = _prepare_gelu(x2d, h2d, self.group_size, nat.PREP_ROTATE)[0]
             out = hip_w4a16_matmul(rotated, w, self.scales, self.bias, output_dtype=x.dtype,
                                    out_features=self.out_features)
         return out.reshape(*lead, self.out_features)

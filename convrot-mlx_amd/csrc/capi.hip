@@ -143,6 +143,45 @@ int convrot_prepare_modulated(const void* x, int dtype, int64_t rows, int64_t fe
                        "convrot_prepare_modulated");
 }
 
+int convrot_prepare_gelu(const void* head, int64_t head_features, int64_t head_stride, const void* x,
+                         int64_t x_features, int64_t x_stride, int dtype, int64_t rows, int group_size, int mode,
+                         void* out, float* scales, void* stream) {
+  if (mode & CONVROT_PREP_NO_ROTATE)
+    return fail(CONVROT_ERR_INVALID, "the GELU producer always rotates (no CONVROT_PREP_NO_ROTATE)");
+  if (mode != CONVROT_PREP_PACKED && mode != CONVROT_PREP_INT8 && mode != CONVROT_PREP_ROTATE)
+    return fail(CONVROT_ERR_INVALID, "unknown ConvRot preparation mode %d", mode);
+  if (!valid_dtype(dtype)) return fail(CONVROT_ERR_INVALID, "unsupported activation dtype code %d", dtype);
+  if (rows < 0 || head_features < 0 || x_features <= 0)
+    return fail(CONVROT_ERR_INVALID, "invalid GELU producer shape: rows %lld, head %lld, x %lld features",
+                (long long)rows, (long long)head_features, (long long)x_features);
+  if (head_features % 16 || x_features % 16)
+    return fail(CONVROT_ERR_UNSUPPORTED, "the GELU producer requires head and x features divisible by 16, got %lld and %lld",
+                (long long)head_features, (long long)x_features);
+  const int64_t features = head_features + x_features;
+  const int s = log4_group(group_size);
+  if (s < 0) return fail(CONVROT_ERR_INVALID, "Regular Hadamard size must be a power of 4, got %d", group_size);
+  if (s > 5) return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot supports groups [4, 16, 64, 256, 1024], got %d", group_size);
+  if (features % group_size)
+    return fail(CONVROT_ERR_INVALID, "features %lld not divisible by ConvRot group size %d", (long long)features, group_size);
+  if (features > kMaxFeatures)
+    return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot preparation supports at most %lld features, got %lld",
+                (long long)kMaxFeatures, (long long)features);
+  if (x_stride < x_features || (head_features > 0 && head_stride < head_features))
+    return fail(CONVROT_ERR_INVALID, "row strides (head %lld, x %lld) shorter than the rows", (long long)head_stride,
+                (long long)x_stride);
+  if (rows > 0x7fffffff) return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot preparation supports at most 2^31-1 rows");
+  if (rows == 0) return ok();
+  const int64_t esize = dtype == CONVROT_DTYPE_F32 ? 4 : 2;
+  if (!x || !out || (head_features > 0 && !head) || (mode != CONVROT_PREP_ROTATE && !scales))
+    return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (!aligned(x, 16) || !aligned(out, 16) || (head_features > 0 && !aligned(head, 16)) || (x_stride * esize) % 16 ||
+      (head_features > 0 && (head_stride * esize) % 16))
+    return fail(CONVROT_ERR_INVALID, "x, head and out rows must start 16-byte aligned");
+  return launch_status(convrot::launch_prep_gelu(head, head_features, head_stride, x, x_features, x_stride, dtype,
+                                                 rows, s, mode, out, scales, (hipStream_t)stream),
+                       "convrot_prepare_gelu");
+}
+
 int convrot_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
                       const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K, void* out,
                       int out_dtype, void* stream) {

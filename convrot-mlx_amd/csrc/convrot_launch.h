@@ -21,6 +21,11 @@ hipError_t launch_prep_modulated(const void* x, int dtype, int64_t rows, int64_t
                                  const void* shift, const void* scale, int64_t rows_per_vector, float eps,
                                  void* out, float* scales, hipStream_t stream);
 
+// Preparation of the rows [head | gelu_tanh(x)] (head may have 0 features).
+hipError_t launch_prep_gelu(const void* head, int64_t head_features, int64_t head_stride, const void* x,
+                            int64_t x_features, int64_t x_stride, int dtype, int64_t rows, int log4g, int mode,
+                            void* out, float* scales, hipStream_t stream);
+
 hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
                             const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
                             void* out, int out_dtype, hipStream_t stream);

@@ -225,7 +225,57 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   return v;
 }
 
-// PRE = true: the fused modulated producer.  Each row is first replaced by
+// tanh GELU of the fused GELU producer, float32, in this fixed sequence (the
+// same IEEE operations, in the same order, as the CPU oracle's gelu_tanh32):
+//   x3 = (x * x) * x;  u = kBeta * fma(kKappa, x3, x)
+//   q = 2 / (exp(2|u|) + 1)  (0 where 2|u| > 88 or u is NaN)
+//   1 + tanh(u) = u >= 0 ? 2 - q : q  (no cancellation on either side)
+//   y = (0.5 * x) * (1 + tanh(u))
+// with exp(z) = 2^n e^r, n = rint(z log2 e), r = z - n ln2 by two fmas
+// (Cody-Waite), e^r by its degree-7 Taylor polynomial (Horner, fma).
+__device__ __forceinline__ float gelu_tanh32(float x) {
+  const float x3 = (x * x) * x;
+  const float u = 0x1.988454p-1f * __builtin_fmaf(0x1.6e4e26p-5f, x3, x);
+  const float z = fabsf(u) + fabsf(u);
+  float q = 0.0f;
+  if (z <= 88.0f) {
+    const float n = rintf(z * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-n, 0x1.62e4p-1f, z);
+    r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0x1p-1f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    q = 2.0f / (ldexpf(p, (int)n) + 1.0f);
+  }
+  const float onept = u >= 0.0f ? 2.0f - q : q;
+  return (0.5f * x) * onept;
+}
+
+// Producers: what the preparation reads as its input rows.
+enum Producer : int {
+  kProPlain = 0,     // x
+  kProModulate = 1,  // (1 + scale) * layer_norm(x) + shift
+  kProGelu = 2,      // [head | gelu_tanh(x)], each with its own row stride
+};
+
+// Arguments of the producers beyond x (unused fields are ignored).
+struct ProducerArgs {
+  const void* shift;  // kProModulate: [vectors, K] shift and scale rows
+  const void* scale;
+  int rows_per_vector;
+  float eps;
+  const void* head;     // kProGelu: [rows, head_features] at head_stride elements per row
+  int head_features;    //   (0: no head), a multiple of 16
+  int64_t head_stride;
+  int64_t x_stride;     // kProGelu: elements per row of x (x has K - head_features features)
+};
+
+// PRO = kProModulate: the fused modulated producer.  Each row is first replaced by
 //   y = rb(rb(rb(1 + scale) * rb((x - mean) * rstd)) + shift)
 // (LayerNorm without affine parameters, then the adaLN modulation with a
 // dtype rounding after every op), with the shift / scale row
@@ -234,12 +284,14 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 // depend on the launch plan: lane l of 1024-feature block b adds features
 // 16l .. 16l+15 in order, the 64 lanes are combined by the xor butterfly of
 // wave_sum_f64, and the block sums are added in block order.
-template <int DT, int S, int NI, int MODE, bool PRE>
+//
+// PRO = kProGelu: the fused GELU producer.  Feature f of a row is head[f] for
+// f < head_features and rb(gelu_tanh32(x[f - head_features])) after that;
+// padding past K reads zeros, and gelu(0) = 0.
+template <int DT, int S, int NI, int MODE, int PRO>
 __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, void* __restrict__ out,
-                                                     float* __restrict__ scales, int K,
-                                                     const void* __restrict__ shift,
-                                                     const void* __restrict__ scalev, int rows_per_vector,
-                                                     float eps) {
+                                                     float* __restrict__ scales, int K, ProducerArgs pa) {
+  constexpr bool PRE = PRO == kProModulate;
   extern __shared__ float lds[];
   __shared__ float wave_max[kMaxWaves];
   __shared__ double block_moments[PRE ? kMaxBlocks : 1][2];
@@ -257,7 +309,12 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
   const int chunks = K >> 4;
   constexpr int kEsize = DT == kF32 ? 4 : 2;
   const __amdgpu_buffer_rsrc_t xrow = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const char*)x + row * K * kEsize), (short)0, K * kEsize, 0x00020000);
+      (void*)((const char*)x + row * (PRO == kProGelu ? pa.x_stride : (int64_t)K) * kEsize), (short)0,
+      (PRO == kProGelu ? K - pa.head_features : K) * kEsize, 0x00020000);
+  const __amdgpu_buffer_rsrc_t hrow = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(PRO == kProGelu && pa.head_features ? (const char*)pa.head + row * pa.head_stride * kEsize
+                                                  : (const char*)x),
+      (short)0, PRO == kProGelu ? pa.head_features * kEsize : 0, 0x00020000);
   float* region = lds + wave * kRegionFloats + (lane / LG) * (G + G / 4);
   const int p = lane % LG;
 
@@ -294,12 +351,12 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
     double var = s2 / (double)K - m64 * m64;
     var = var > 0.0 ? var : 0.0;
     const float mean = (float)m64;
-    const float rstd = (float)(1.0 / sqrt(var + (double)eps));
-    const int64_t vrow = row / rows_per_vector;
+    const float rstd = (float)(1.0 / sqrt(var + (double)pa.eps));
+    const int64_t vrow = row / pa.rows_per_vector;
     const __amdgpu_buffer_rsrc_t shrow = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const char*)shift + vrow * K * kEsize), (short)0, K * kEsize, 0x00020000);
+        (void*)((const char*)pa.shift + vrow * K * kEsize), (short)0, K * kEsize, 0x00020000);
     const __amdgpu_buffer_rsrc_t scrow = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const char*)scalev + vrow * K * kEsize), (short)0, K * kEsize, 0x00020000);
+        (void*)((const char*)pa.scale + vrow * K * kEsize), (short)0, K * kEsize, 0x00020000);
 #pragma unroll
     for (int it = 0; it < NI; ++it) {
       const int chunk = (wave * NI + it) * 64 + lane;
@@ -326,7 +383,24 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
     const int block = wave * NI + it;
     const int chunk = block * 64 + lane;
     float (&v)[16] = keep[it];
-    if constexpr (!PRE) load16<DT>(xrow, (uint32_t)chunk * (16u * kEsize), v);  // chunks past the row end read zeros
+    if constexpr (PRO == kProPlain) {
+      load16<DT>(xrow, (uint32_t)chunk * (16u * kEsize), v);  // chunks past the row end read zeros
+    } else if constexpr (PRO == kProGelu) {
+      const int f0 = chunk * 16;  // head_features % 16 == 0: a chunk lies in one segment
+      if (f0 < pa.head_features) {
+        load16<DT>(hrow, (uint32_t)f0 * kEsize, v);
+      } else {
+        load16<DT>(xrow, (uint32_t)(f0 - pa.head_features) * kEsize, v);  // past the end: zeros
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          // the float32 result is rounded on its own, as the oracle does (no
+          // multiply-and-narrow folding into one v_fma_mix for f16)
+          float g = gelu_tanh32(v[j]);
+          asm volatile("" : "+v"(g));
+          v[j] = rnd<DT>(g);
+        }
+      }
+    }
     rotate16<DT, S>(v, region, p);
     if constexpr (!kImplicitNorm && S > 0 && MODE != CONVROT_PREP_ROTATE) {
 #pragma unroll
@@ -395,24 +469,25 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
   }
 }
 
-// Optional input transform of a launch (the fused modulated producer).
+// The producer of a launch and its arguments.
 struct Modulation {
-  const void* shift;  // nullptr: plain preparation
-  const void* scale;
-  int rows_per_vector;
-  float eps;
+  int producer;  // kProPlain, kProModulate or kProGelu
+  ProducerArgs args;
 };
 
 template <int DT, int S, int NI, int MODE>
 hipError_t launch_prep_t(const void* x, void* out, float* scales, int64_t rows, int K, int waves,
                          const Modulation& mod, hipStream_t stream) {
   const size_t lds_bytes = (S >= 3) ? (size_t)waves * kRegionFloats * sizeof(float) : 0;
-  if (mod.shift)
-    hipLaunchKernelGGL((prep_kernel<DT, S, NI, MODE, true>), dim3((unsigned)rows), dim3(64 * waves), lds_bytes,
-                       stream, x, out, scales, K, mod.shift, mod.scale, mod.rows_per_vector, mod.eps);
+  if (mod.producer == kProModulate)
+    hipLaunchKernelGGL((prep_kernel<DT, S, NI, MODE, kProModulate>), dim3((unsigned)rows), dim3(64 * waves),
+                       lds_bytes, stream, x, out, scales, K, mod.args);
+  else if (mod.producer == kProGelu)
+    hipLaunchKernelGGL((prep_kernel<DT, S, NI, MODE, kProGelu>), dim3((unsigned)rows), dim3(64 * waves),
+                       lds_bytes, stream, x, out, scales, K, mod.args);
   else
-    hipLaunchKernelGGL((prep_kernel<DT, S, NI, MODE, false>), dim3((unsigned)rows), dim3(64 * waves), lds_bytes,
-                       stream, x, out, scales, K, nullptr, nullptr, 1, 0.0f);
+    hipLaunchKernelGGL((prep_kernel<DT, S, NI, MODE, kProPlain>), dim3((unsigned)rows), dim3(64 * waves),
+                       lds_bytes, stream, x, out, scales, K, mod.args);
   return hipGetLastError();
 }
 
@@ -513,15 +588,33 @@ hipError_t launch_prep_any(const void* x, int dtype, int64_t rows, int64_t K, in
 
 hipError_t launch_prep(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode, void* out,
                        float* scales, hipStream_t stream) {
-  return launch_prep_any(x, dtype, rows, K, log4g, mode, out, scales, Modulation{nullptr, nullptr, 1, 0.0f},
-                         stream);
+  Modulation mod{};
+  mod.producer = kProPlain;
+  return launch_prep_any(x, dtype, rows, K, log4g, mode, out, scales, mod, stream);
 }
 
 hipError_t launch_prep_modulated(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode,
                                  const void* shift, const void* scale, int64_t rows_per_vector, float eps,
                                  void* out, float* scales, hipStream_t stream) {
-  return launch_prep_any(x, dtype, rows, K, log4g, mode, out, scales,
-                         Modulation{shift, scale, (int)rows_per_vector, eps}, stream);
+  Modulation mod{};
+  mod.producer = kProModulate;
+  mod.args.shift = shift;
+  mod.args.scale = scale;
+  mod.args.rows_per_vector = (int)rows_per_vector;
+  mod.args.eps = eps;
+  return launch_prep_any(x, dtype, rows, K, log4g, mode, out, scales, mod, stream);
+}
+
+hipError_t launch_prep_gelu(const void* head, int64_t head_features, int64_t head_stride, const void* x,
+                            int64_t x_features, int64_t x_stride, int dtype, int64_t rows, int log4g, int mode,
+                            void* out, float* scales, hipStream_t stream) {
+  Modulation mod{};
+  mod.producer = kProGelu;
+  mod.args.head = head;
+  mod.args.head_features = (int)head_features;
+  mod.args.head_stride = head_stride;
+  mod.args.x_stride = x_stride;
+  return launch_prep_any(x, dtype, rows, head_features + x_features, log4g, mode, out, scales, mod, stream);
 }
 
 }  // namespace convrot

@@ -162,6 +162,15 @@ def set_fused_modulation(model: nn.Module, on: bool) -> None:
             m.fused_modulation = on
 
 
+def set_fused_gelu(model: nn.Module, on: bool) -> None:
+    """With `on`, each single block feeds linear2 through ConvRotLinear.forward_gelu: the tanh
+    GELU of the MLP half and its concatenation with the attention output run inside the
+    activation preparation, reading the MLP slice of linear1's output in place."""
+    for m in model.modules():
+        if hasattr(m, "fused_gelu"):
+            m.fused_gelu = on
+
+
 def _split_heads(qkv: torch.Tensor, heads: int):
     b, l, _ = qkv.shape
     q, k, v = qkv.reshape(b, l, 3, heads, -1).permute(2, 0, 3, 1, 4).unbind(0)
@@ -209,6 +218,7 @@ class SingleStreamBlock(nn.Module):
         self.norm = QKNorm(hidden // heads)
         self.modulation = Modulation(hidden, double=False)
         self.fused_modulation = False
+        self.fused_gelu = False
 
     def forward(self, x, vec, pe):
         (shift, scale, gate), _ = self.modulation(vec)
@@ -216,7 +226,11 @@ class SingleStreamBlock(nn.Module):
         qkv, mlp = torch.split(h, [3 * self.hidden, self.mlp_hidden], dim=-1)
         q, k, v = _split_heads(qkv, self.heads)
         q, k = self.norm(q, k)
-        out = self.linear2(torch.cat([attention(q, k, v, pe), F.gelu(mlp, approximate="tanh")], dim=-1))
+        attn = attention(q, k, v, pe)
+        if self.fused_gelu and hasattr(self.linear2, "forward_gelu"):
+            out = self.linear2.forward_gelu(mlp, head=attn)
+        else:
+            out = self.linear2(torch.cat([attn, F.gelu(mlp, approximate="tanh")], dim=-1))
         return x + gate * out
 
 
@@ -351,6 +365,9 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
     set_fused_modulation(model, True)
     fused, fused_ms, fused_graph_ms = time_step(model, inputs, steps)
     fused = fused.float()
+    set_fused_gelu(model, True)
+    both, both_ms, both_graph_ms = time_step(model, inputs, steps)
+    both = both.float()
 
     def dev_stats(out):
         diff = out - dense
@@ -360,6 +377,7 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
 
     rel, cos, mad = dev_stats(quant)
     frel, fcos, _ = dev_stats(fused)
+    brel, bcos, _ = dev_stats(both)
     return {
         "what": "random-init FLUX.1-dev DiT, one denoising step, batch 1, "
                 f"{img_tokens} image + {txt_tokens} text tokens, bf16",
@@ -376,6 +394,14 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
             "rel_l2_vs_dense": frel, "cosine_vs_dense": fcos,
             "rel_l2_vs_unfused": round(((fused - quant).norm() / quant.norm()).item(), 5),
         },
+        "fused_modulation_and_gelu": {
+            "what": "as fused_modulation, and each single block's tanh GELU + concatenation fused into "
+                    "linear2's activation preparation (38 sites)",
+            "eager_ms": round(both_ms, 2), "graph_ms": round(both_graph_ms, 2),
+            "graph_speedup_vs_dense": round(dense_graph_ms / both_graph_ms, 3),
+            "rel_l2_vs_dense": brel, "cosine_vs_dense": bcos,
+            "rel_l2_vs_fused_modulation": round(((both - fused).norm() / fused.norm()).item(), 5),
+        },
     }
 
 
@@ -387,9 +413,10 @@ def profile_variant(variant: str, steps: int, group_size: int = 64) -> dict:
     dev = torch.device("cuda:0")
     model = build(p, dev)
     inputs = make_inputs(p, 1024, 512, dev)
-    if variant in ("convrot", "fused"):
+    if variant in ("convrot", "fused", "fused_gelu"):
         replace_convrot_linears(model, backend="hip-w4a4", group_size=group_size)
-        set_fused_modulation(model, variant == "fused")
+        set_fused_modulation(model, variant in ("fused", "fused_gelu"))
+        set_fused_gelu(model, variant == "fused_gelu")
     with torch.no_grad():
         model(**inputs)
         torch.cuda.synchronize()
@@ -402,9 +429,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--group-size", type=int, default=64)
-    ap.add_argument("--variant", choices=["both", "dense", "convrot", "fused"], default="both",
-                    help="'dense', 'convrot' or 'fused' (convrot with fused modulation) runs eager steps of "
-                         "that model only, for profiling")
+    ap.add_argument("--variant", choices=["both", "dense", "convrot", "fused", "fused_gelu"], default="both",
+                    help="'dense', 'convrot', 'fused' (convrot with fused modulation) or 'fused_gelu' (and "
+                         "the single blocks' GELU fused too) runs eager steps of that model only, for profiling")
     args = ap.parse_args()
     if args.variant == "both":
         print(json.dumps(config5_figure(group_size=args.group_size, steps=args.steps)), flush=True)

@@ -95,6 +95,23 @@ int convrot_prepare_modulated(const void* x, int dtype, int64_t rows, int64_t fe
                               const void* shift, const void* scale, int64_t rows_per_vector, float eps, void* out,
                               float* scales, void* stream);
 
+/* Fused GELU producer: the preparation of the rows [head | gelu_tanh(x)],
+ * features head_features + x_features, in the modes of convrot_prepare.  It has
+ * no counterpart in the reference; it fuses the producer that feeds a DiT's
+ * MLP-down Linear, linear2(cat(attn, gelu(mlp))) in the FLUX single blocks,
+ * into the preparation (the reference names fusing the preparation passes as
+ * its open target, /root/reference/docs/design.md:54-64).
+ * gelu_tanh is the tanh GELU, nn.GELU(approximate="tanh"), evaluated as a
+ * fixed float32 sequence (x^3, fma, exp by Cody-Waite reduction and a degree-7
+ * polynomial, one IEEE division) and rounded once to the dtype.
+ * head: [rows] rows of head_features elements, head_stride elements apart (NULL
+ * when head_features == 0); x: rows of x_features elements, x_stride apart; both
+ * 16-byte aligned per row; both feature counts divisible by 16; out and scales
+ * as convrot_prepare for features = head_features + x_features. */
+int convrot_prepare_gelu(const void* head, int64_t head_features, int64_t head_stride, const void* x,
+                         int64_t x_features, int64_t x_stride, int dtype, int64_t rows, int group_size, int mode,
+                         void* out, float* scales, void* stream);
+
 /*
  * W4A4 GEMM with fused epilogue:
  *   out[m, n] = out_dtype(((float(sum_k a[m,k] * w[n,k]) * xscales[m]) * wscales[n]) + bias[n])

@@ -345,3 +345,55 @@ int cr_oracle_modulate(const void* x, int dt, int64_t rows, int64_t K, const voi
     }
     return 0;
 }
+
+/* ------------------------------------------------- tanh GELU (producer input)
+ *
+ * Input transform of the fused GELU producer; it has no reference counterpart.
+ * The FLUX MLP activation nn.GELU(approximate="tanh"),
+ *   gelu(x) = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))),
+ * evaluated in float32 in this fixed sequence, rounded once to the dtype:
+ *   x3    = (x * x) * x
+ *   u     = kBeta * fma(kKappa, x3, x)
+ *   q     = 2 / (exp(2|u|) + 1)            (q = 0 where 2|u| > 88 or u is NaN)
+ *   onept = u >= 0 ? 2 - q : q             (= 1 + tanh(u), without cancellation)
+ *   y     = (0.5 * x) * onept
+ * exp(z), 0 <= z <= 88, is Cody-Waite reduced, z = n ln2 + r with
+ * n = rint(z log2 e), r = fma(-n, ln2_lo, fma(-n, ln2_hi, z)), |r| <= ln2/2, then
+ * 2^n times the degree-7 Taylor polynomial of e^r (Horner, fma), whose
+ * truncation error r^8/8! < 6e-9 is below float32 resolution.  Every step is an
+ * IEEE float32 operation (+ - * /, fma, rint, ldexp), so any IEEE machine that
+ * runs the same sequence (the HIP producer kernel does) gets the same bits.
+ */
+#define GELU_BETA 0x1.988454p-1f   /* float32(sqrt(2/pi)) */
+#define GELU_KAPPA 0x1.6e4e26p-5f  /* float32(0.044715) */
+#define EXP_LOG2E 0x1.715476p+0f
+#define EXP_LN2_HI 0x1.62e4p-1f
+#define EXP_LN2_LO 0x1.7f7d1cp-20f
+
+static float gelu_tanh32(float x) {
+    const float x3 = (x * x) * x;
+    const float u = GELU_BETA * fmaf(GELU_KAPPA, x3, x);
+    const float z = fabsf(u) + fabsf(u);
+    float q = 0.0f;
+    if (z <= 88.0f) {
+        const float n = rintf(z * EXP_LOG2E);
+        float r = fmaf(-n, EXP_LN2_HI, z);
+        r = fmaf(-n, EXP_LN2_LO, r);
+        float p = 0x1.a01a02p-13f;         /* 1/7! */
+        p = fmaf(p, r, 0x1.6c16c2p-10f);   /* 1/6! */
+        p = fmaf(p, r, 0x1.111112p-7f);    /* 1/5! */
+        p = fmaf(p, r, 0x1.555556p-5f);    /* 1/4! */
+        p = fmaf(p, r, 0x1.555556p-3f);    /* 1/3! */
+        p = fmaf(p, r, 0x1p-1f);           /* 1/2! */
+        p = fmaf(p, r, 1.0f);
+        p = fmaf(p, r, 1.0f);
+        q = 2.0f / (ldexpf(p, (int)n) + 1.0f);
+    }
+    const float onept = u >= 0.0f ? 2.0f - q : q;
+    return (0.5f * x) * onept;
+}
+
+int cr_oracle_gelu(const void* x, int dt, int64_t n, void* out) {
+    for (int64_t i = 0; i < n; ++i) store_elem(dt, out, i, rb(dt, gelu_tanh32(load_elem(dt, x, i))));
+    return 0;
+}

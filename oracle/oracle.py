@@ -57,6 +57,7 @@ def lib() -> ctypes.CDLL:
         L.cr_oracle_w4a16_matmul.argtypes = [vp, i32, vp, vp, vp, i64, i64, i64, i32, vp, vp, vp]
         L.cr_oracle_f32_to_dtype.argtypes = [vp, i64, i32, vp]
         L.cr_oracle_modulate.argtypes = [vp, i32, i64, i64, vp, vp, i64, ctypes.c_float, vp]
+        L.cr_oracle_gelu.argtypes = [vp, i32, i64, vp]
         L.cr_oracle_dtype_to_f32.argtypes = [vp, i64, i32, vp]
         L.cr_f32_to_bf16.argtypes = [ctypes.c_float]
         L.cr_f32_to_bf16.restype = ctypes.c_uint16
@@ -193,6 +194,24 @@ def modulate(x: np.ndarray, dtype: str, shift: np.ndarray, scale: np.ndarray, ro
                                   rows_per_vector, eps, _ptr(out))
     assert rc == 0
     return out
+
+
+def gelu_tanh(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Input transform of the fused GELU producer (no reference counterpart: the FLUX MLP
+    activation nn.GELU(approximate="tanh")), C restatement: the fixed float32 sequence of
+    convrot_oracle.c (exp by Cody-Waite reduction and a degree-7 polynomial, fma, one IEEE
+    division), rounded once to the dtype."""
+    x = np.ascontiguousarray(x)
+    out = np.empty_like(x)
+    rc = lib().cr_oracle_gelu(_ptr(x), DTYPE_CODES[dtype], x.size, _ptr(out))
+    assert rc == 0
+    return out
+
+
+def gelu_producer_rows(head: np.ndarray | None, x: np.ndarray, dtype: str) -> np.ndarray:
+    """The rows the fused GELU producer prepares: [head | gelu_tanh(x)] along features."""
+    g = gelu_tanh(x, dtype)
+    return g if head is None or head.shape[-1] == 0 else np.ascontiguousarray(np.concatenate([head, g], axis=-1))
 
 
 def w4a4_matmul_codes(a_codes, w_codes, xscales, wscales, bias, out_dtype: str, want_dots: bool = False):

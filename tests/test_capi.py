@@ -109,6 +109,22 @@ def test_gemm_validation(lib):
     assert _err(lib) == "null pointer argument"
 
 
+def test_prepare_gelu_validation(lib):
+    """convrot_prepare_gelu(head, Kh, head_stride, x, Kx, x_stride, dtype, rows, G, mode, out, scales, stream)."""
+    g = lib.convrot_prepare_gelu
+    assert g(None, 0, 0, None, 64, 64, BF16, 4, 64, 1 | 0x10, None, None, None) == 1
+    assert _err(lib) == "the GELU producer always rotates (no CONVROT_PREP_NO_ROTATE)"
+    assert g(None, 8, 8, None, 56, 56, BF16, 4, 64, 1, None, None, None) == 2
+    assert _err(lib) == "the GELU producer requires head and x features divisible by 16, got 8 and 56"
+    assert g(None, 16, 16, None, 64, 64, BF16, 4, 64, 1, None, None, None) == 1
+    assert _err(lib) == "features 80 not divisible by ConvRot group size 64"
+    assert g(None, 0, 0, None, 128, 64, BF16, 4, 64, 1, None, None, None) == 1
+    assert _err(lib) == "row strides (head 0, x 64) shorter than the rows"
+    assert g(None, 0, 0, None, 128, 128, BF16, 0, 64, 1, None, None, None) == 0  # no rows: nothing to do
+    assert g(None, 0, 0, None, 128, 128, BF16, 4, 64, 1, None, None, None) == 1
+    assert _err(lib) == "null pointer argument"
+
+
 def test_repack_validation(lib):
     assert lib.convrot_repack_weight(None, 0, None, 1, 33, 64, None) == 1
     assert _err(lib) == "MPP int4 packing requires even out_features, got 33"
