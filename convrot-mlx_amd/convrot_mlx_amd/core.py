@@ -21,6 +21,7 @@ Weight layouts
 
 from __future__ import annotations
 
+import math
 import os
 
 import torch
@@ -472,7 +473,67 @@ def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
     return None if t is None else t.to(torch.float32).contiguous()
 
 
-def _w4a4(act: torch.Tensor, act_format: int, k: int, qweight, xscales, wscales, bias, output_dtype, n=None):
+class GatedResidual:
+    """The gated residual a W4A4 GEMM applies in its epilogue:
+    out = residual + gate * linear, each op rounded to the output dtype.
+
+    residual: [M, N] contiguous, the output dtype.  gate: None (plain residual
+    add) or a tensor whose row m // rows_per_gate, `stride` elements per row,
+    gates output row m.  `inplace` writes the result into `residual`."""
+
+    __slots__ = ("residual", "gate", "stride", "rows_per_gate", "inplace")
+
+    def __init__(self, residual, gate=None, stride=0, rows_per_gate=1, inplace=False):
+        self.residual, self.gate, self.stride = residual, gate, stride
+        self.rows_per_gate, self.inplace = rows_per_gate, inplace
+
+
+def _gate_rows(gate: torch.Tensor, out_shape: tuple) -> tuple[torch.Tensor, int, int]:
+    """A gate broadcastable to out_shape ([*lead, N]) as (tensor, row stride, rows per gate
+    row) over the flattened [M, N] output: trailing lead dims the gate broadcasts over
+    (stride 0 once expanded) become rows_per_gate, the others must step through the gate's
+    rows at one stride.  Gates of any other form are expanded into a contiguous [M, N] copy."""
+    n = out_shape[-1]
+    try:
+        g = gate.expand(out_shape)
+    except RuntimeError as e:
+        raise ValueError(f"gate {tuple(gate.shape)} does not broadcast to the output {tuple(out_shape)}") from e
+    lead, strides = out_shape[:-1], g.stride()[:-1]
+    i = len(lead)
+    while i > 0 and (strides[i - 1] == 0 or lead[i - 1] == 1):
+        i -= 1
+    rows_per_gate = math.prod(lead[i:])
+    prefix = [(lead[j], strides[j]) for j in range(i) if lead[j] != 1]
+    stride = prefix[-1][1] if prefix else n
+    nested = all(prefix[j][1] == prefix[j + 1][1] * prefix[j + 1][0] for j in range(len(prefix) - 1))
+    if (n > 1 and g.stride(-1) != 1) or not nested or stride < n or g.data_ptr() % 16:
+        return g.reshape(-1, n).contiguous(), n, 1
+    return g, stride, max(1, rows_per_gate)
+
+
+def _gated_residual(residual: torch.Tensor, gate: torch.Tensor | None, out_shape: tuple,
+                    dtype: torch.dtype, inplace: bool = False) -> GatedResidual:
+    """Validate `residual + gate * linear` operands against the linear's output."""
+    if tuple(residual.shape) != tuple(out_shape):
+        raise ValueError(f"residual {tuple(residual.shape)} must have the output shape {tuple(out_shape)}")
+    if residual.dtype != dtype or (gate is not None and gate.dtype != dtype):
+        raise ValueError(f"residual and gate must have the output dtype {dtype}")
+    nat.require_device(residual, gate)
+    if inplace and not residual.is_contiguous():
+        raise ValueError("an in-place gated residual must be contiguous")
+    res = residual if residual.is_contiguous() else residual.contiguous()
+    if res.data_ptr() % 16:
+        if inplace:
+            raise ValueError("an in-place gated residual must be 16-byte aligned")
+        res = res.clone()
+    if gate is None:
+        return GatedResidual(res, None, 0, 1, inplace)
+    g, stride, rpg = _gate_rows(gate, tuple(out_shape))
+    return GatedResidual(res, g, stride, rpg, inplace)
+
+
+def _w4a4(act: torch.Tensor, act_format: int, k: int, qweight, xscales, wscales, bias, output_dtype, n=None,
+          gr: GatedResidual | None = None):
     m = act.shape[0]
     n_layout = _weight_n(qweight, k)
     n = n if n is not None else n_layout
@@ -481,38 +542,71 @@ def _w4a4(act: torch.Tensor, act_format: int, k: int, qweight, xscales, wscales,
     _validate_mpp_epilogue(m, n, xscales, wscales, bias)
     nat.require_device(act, qweight, xscales, wscales, bias)
     w = _as_cdna4(qweight, n, k)
-    out = torch.empty((m, n), dtype=output_dtype, device=act.device)
     xs, ws, b = _f32(xscales), _f32(wscales), _f32(bias)
+    if gr is None:
+        out = torch.empty((m, n), dtype=output_dtype, device=act.device)
+        nat.check(
+            nat.load().convrot_w4a4_gemm(
+                nat.ptr(act), act_format, nat.ptr(xs), nat.ptr(w), nat.ptr(ws), nat.ptr(b), m, n, k,
+                nat.ptr(out), nat.dtype_code(output_dtype), nat.stream_of(act.device),
+            )
+        )
+        return out
+    if gr.residual.numel() != m * n:
+        raise ValueError(f"residual has {gr.residual.numel()} elements, the output {m * n}")
+    out = gr.residual.view(m, n) if gr.inplace else torch.empty((m, n), dtype=output_dtype, device=act.device)
     nat.check(
-        nat.load().convrot_w4a4_gemm(
+        nat.load().convrot_w4a4_gemm_residual(
             nat.ptr(act), act_format, nat.ptr(xs), nat.ptr(w), nat.ptr(ws), nat.ptr(b), m, n, k,
+            nat.ptr(gr.residual), nat.ptr(gr.gate), gr.stride, gr.rows_per_gate,
             nat.ptr(out), nat.dtype_code(output_dtype), nat.stream_of(act.device),
         )
     )
     return out
 
 
-def hip_w4a4_matmul(qact, qweight, xscales, wscales, bias, *, output_dtype, out_features=None):
+def _residual_arg(m: int, qweight, k: int, out_features, output_dtype, residual, gate, inplace):
+    if residual is None:
+        if gate is not None or inplace:
+            raise ValueError("gate and inplace need a residual")
+        return None
+    n = out_features if out_features is not None else _weight_n(qweight, k)
+    if residual.ndim < 1 or residual.shape[-1] != n or residual.numel() != m * n:
+        raise ValueError(f"residual {tuple(residual.shape)} must hold the [{m}, {n}] output as [..., {n}]")
+    # [*lead, N] residuals (e.g. [B, L, N]) let the gate broadcast over their leading dims
+    return _gated_residual(residual, gate, tuple(residual.shape), output_dtype, inplace)
+
+
+def hip_w4a4_matmul(qact, qweight, xscales, wscales, bias, *, output_dtype, out_features=None, residual=None,
+                    gate=None, inplace=False):
     """Packed-A4 activations [M, K/2] x W4 weight -> output_dtype [M, N] (core.py:1061-1085).
 
     qweight: CDNA4 blocks (3-D; pass out_features when N is not a multiple of
-    16) or the reference's K x packed-N layout (2-D).
+    16) or the reference's K x packed-N layout (2-D).  With `residual` ([M, N],
+    output_dtype) the kernel returns residual + gate * product (see
+    ConvRotLinear.forward), in place into `residual` when `inplace`; the residual
+    may be shaped [..., N] (M rows in all) for the gate to broadcast against.
     """
     if qact.ndim != 2:
         raise ValueError(f"MPP W4A4 activation must be 2D, got {tuple(qact.shape)}")
     k = qact.shape[1] * 2
-    return _w4a4(qact.contiguous(), nat.ACT_PACKED, k, qweight, xscales, wscales, bias, output_dtype, out_features)
+    gr = _residual_arg(qact.shape[0], qweight, k, out_features, output_dtype, residual, gate, inplace)
+    return _w4a4(qact.contiguous(), nat.ACT_PACKED, k, qweight, xscales, wscales, bias, output_dtype, out_features,
+                 gr)
 
 
-def hip_w4a4_int8_matmul(activations, qweight, xscales, wscales, bias, *, output_dtype, out_features=None):
-    """int8 A4 activations [M, K] x W4 weight -> output_dtype [M, N] (core.py:1088-1120)."""
+def hip_w4a4_int8_matmul(activations, qweight, xscales, wscales, bias, *, output_dtype, out_features=None,
+                         residual=None, gate=None, inplace=False):
+    """int8 A4 activations [M, K] x W4 weight -> output_dtype [M, N] (core.py:1088-1120);
+    residual, gate and inplace as in hip_w4a4_matmul."""
     if activations.ndim != 2 or activations.dtype != torch.int8:
         raise ValueError(
             f"MPP W4A4 requires a 2D int8 activation, got {tuple(activations.shape)} {activations.dtype}"
         )
     k = activations.shape[1]
+    gr = _residual_arg(activations.shape[0], qweight, k, out_features, output_dtype, residual, gate, inplace)
     return _w4a4(activations.contiguous(), nat.ACT_INT8, k, qweight, xscales, wscales, bias, output_dtype,
-                 out_features)
+                 out_features, gr)
 
 
 def hip_w4a16_matmul(activations, qweight, wscales, bias, *, output_dtype, out_features=None):
@@ -659,62 +753,69 @@ class ConvRotLinear(nn.Module):
             self._cdna4_cache = (key, repack_mpp_weight_for_cdna4(q))
         return self._cdna4_cache[1]
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if x.shape[-1] != self.in_features:
-            raise ValueError(f"ConvRotLinear expected K={self.in_features}, got {x.shape[-1]}")
-        lead = x.shape[:-1]
-        x2d = x.reshape(-1, self.in_features)
+    def _project(self, prep, lead: tuple, dtype: torch.dtype, residual, gate, inplace: bool) -> torch.Tensor:
+        """Run the prepared activation `prep(mode)` through this layer's GEMM, then the
+        optional gated residual (residual + gate * linear).  W4A4 applies the residual in
+        the GEMM's epilogue; W4A16 applies it with torch's eager ops (the same numerics)."""
+        if residual is None and (gate is not None or inplace):
+            raise ValueError("gate and inplace need a residual")
+        out_shape = (*lead, self.out_features)
         w = self._device_weight()
         if self.a4:
-            qact, xscales = _prepare(x2d, self.group_size, nat.PREP_INT8)
-            out = _w4a4(qact, nat.ACT_INT8, self.in_features, w, xscales, self.scales, self.bias, x.dtype,
-                        self.out_features)
-        else:
-            rotated = _prepare(x2d, self.group_size, nat.PREP_ROTATE)[0]
-            out = hip_w4a16_matmul(rotated, w, self.scales, self.bias, output_dtype=x.dtype,
-                                   out_features=self.out_features)
-        return out.reshape(*lead, self.out_features)
+            gr = None if residual is None else _gated_residual(residual, gate, out_shape, dtype, inplace)
+            qact, xscales = prep(nat.PREP_INT8)
+            out = _w4a4(qact, nat.ACT_INT8, self.in_features, w, xscales, self.scales, self.bias, dtype,
+                        self.out_features, gr)
+            return residual if inplace else out.reshape(out_shape)
+        if residual is not None:
+            _gated_residual(residual, gate, out_shape, dtype, inplace)  # same argument checks
+        rotated = prep(nat.PREP_ROTATE)[0]
+        out = hip_w4a16_matmul(rotated, w, self.scales, self.bias, output_dtype=dtype,
+                               out_features=self.out_features).reshape(out_shape)
+        if residual is None:
+            return out
+        update = out if gate is None else gate * out
+        return residual.add_(update) if inplace else residual + update
+
+    def forward(self, x: torch.Tensor, *, residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
+                inplace: bool = False) -> torch.Tensor:
+        """linear(x); with `residual`, residual + gate * linear(x) (gate None: residual +
+        linear(x)), each op rounded to x.dtype as torch evaluates it eagerly.  The gate
+        broadcasts to the output ([B, 1, N] per image, [N], or full); `inplace` writes the
+        result into `residual` and returns it."""
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"ConvRotLinear expected K={self.in_features}, got {x.shape[-1]}")
+        x2d = x.reshape(-1, self.in_features)
+        return self._project(lambda mode: _prepare(x2d, self.group_size, mode), x.shape[:-1], x.dtype,
+                             residual, gate, inplace)
 
     def forward_modulated(self, x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
-                          eps: float = 1e-6) -> torch.Tensor:
+                          eps: float = 1e-6, *, residual: torch.Tensor | None = None,
+                          gate: torch.Tensor | None = None, inplace: bool = False) -> torch.Tensor:
         """self((1 + scale) * layer_norm(x) + shift) with the normalization and modulation
-        fused into the activation preparation (see hip_fused_modulated_prepare)."""
+        fused into the activation preparation (see hip_fused_modulated_prepare); residual,
+        gate and inplace as in forward."""
         if x.shape[-1] != self.in_features:
             raise ValueError(f"ConvRotLinear expected K={self.in_features}, got {x.shape[-1]}")
-        lead = x.shape[:-1]
         x2d = x.reshape(-1, self.in_features)
-        w = self._device_weight()
-        if self.a4:
-            qact, xscales = _prepare_modulated(x2d, shift, scale, self.group_size, nat.PREP_INT8, eps)
-            out = _w4a4(qact, nat.ACT_INT8, self.in_features, w, xscales, self.scales, self.bias, x.dtype,
-                        self.out_features)
-        else:
-            rotated = _prepare_modulated(x2d, shift, scale, self.group_size, nat.PREP_ROTATE, eps)[0]
-            out = hip_w4a16_matmul(rotated, w, self.scales, self.bias, output_dtype=x.dtype,
-                                   out_features=self.out_features)
-        return out.reshape(*lead, self.out_features)
+        return self._project(lambda mode: _prepare_modulated(x2d, shift, scale, self.group_size, mode, eps),
+                             x.shape[:-1], x.dtype, residual, gate, inplace)
 
-    def forward_gelu(self, x: torch.Tensor, head: torch.Tensor | None = None) -> torch.Tensor:
+    def forward_gelu(self, x: torch.Tensor, head: torch.Tensor | None = None, *,
+                     residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
+                     inplace: bool = False) -> torch.Tensor:
         """self(cat([head, gelu(x)], -1)) (or self(gelu(x))) with the tanh GELU and the
-        concatenation fused into the activation preparation (see hip_fused_gelu_prepare)."""
+        concatenation fused into the activation preparation (see hip_fused_gelu_prepare);
+        residual, gate and inplace as in forward."""
         head_features = 0 if head is None else head.shape[-1]
         if head_features + x.shape[-1] != self.in_features:
             raise ValueError(f"ConvRotLinear expected K={self.in_features}, got {head_features} + {x.shape[-1]}")
         if head is not None and head.shape[:-1] != x.shape[:-1]:
             raise ValueError(f"GELU producer head {tuple(head.shape)} and x {tuple(x.shape)} differ in leading shape")
-        lead = x.shape[:-1]
         x2d = x.reshape(-1, x.shape[-1])
         h2d = None if head is None else head.reshape(-1, head_features)
-        w = self._device_weight()
-        if self.a4:
-            qact, xscales = _prepare_gelu(x2d, h2d, self.group_size, nat.PREP_INT8)
-            out = _w4a4(qact, nat.ACT_INT8, self.in_features, w, xscales, self.scales, self.bias, x.dtype,
-                        self.out_features)
-        else:
-            rotated = _prepare_gelu(x2d, h2d, self.group_size, nat.PREP_ROTATE)[0]
-            out = hip_w4a16_matmul(rotated, w, self.scales, self.bias, output_dtype=x.dtype,
-                                   out_features=self.out_features)
-        return out.reshape(*lead, self.out_features)
+        return self._project(lambda mode: _prepare_gelu(x2d, h2d, self.group_size, mode), x.shape[:-1], x.dtype,
+                             residual, gate, inplace)
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, group_size={self.group_size}, "

@@ -86,6 +86,160 @@ __device__ __forceinline__ void store_out4(void* base, int64_t idx, float a, flo
   }
 }
 
+// ---- gated residual epilogue
+//
+// A diffusion transformer block ends every branch in x + gate * linear(...),
+// evaluated by torch as two eager ops, each rounding to the array dtype.  The
+// W4A4 GEMM can apply it after the linear's own rounding:
+//   out[m][n] = dt(residual[m][n] + dt(gate[m / rows_per_gate][n] * dt(lin)))
+// with `gate` null meaning a plain residual add, dt(residual + dt(lin)).
+// residual is [M][N] contiguous in the output dtype and may be `out` itself:
+// every lane loads the residual elements it stores, before storing them, and
+// no other lane touches them.  gate rows are gate_stride elements apart.
+struct GatedResidual {
+  const void* residual;  // null: no residual (plain linear)
+  const void* gate;      // null: no gate
+  int64_t gate_stride;
+  int rows_per_gate;
+};
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* base, int64_t i) {
+  return (float)((const typename Elem<DT>::T*)base)[i];
+}
+
+// dt(res + dt(g * dt(lin))), returned unrounded (the store rounds it).
+template <int DT>
+__device__ __forceinline__ float gated_sum(float lin, float res, float g) {
+  return res + rnd<DT>(g * rnd<DT>(lin));
+}
+
+// Four consecutive element values at element index i (16-byte aligned for
+// float32, 8-byte for 16-bit dtypes).
+template <int DT>
+__device__ __forceinline__ void load_elem4(const void* base, int64_t i, float (&v)[4]) {
+  if constexpr (DT == kF32) {
+    const float4 f = *(const float4*)((const float*)base + i);
+    v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+  } else {
+    const uint2 w = *(const uint2*)((const uint16_t*)base + i);
+    if constexpr (DT == kBF16) {
+      v[0] = bf16_lo(w.x), v[1] = bf16_hi(w.x), v[2] = bf16_lo(w.y), v[3] = bf16_hi(w.y);
+    } else {
+      const _Float16* h = (const _Float16*)&w;
+      v[0] = (float)h[0], v[1] = (float)h[1], v[2] = (float)h[2], v[3] = (float)h[3];
+    }
+  }
+}
+
+// Residual and gate operands of 4 outputs (row m, columns n..n+3 < N where
+// `vec`, with N a multiple of 4; else those < N).  Loading them apart from
+// gate_apply4 lets a caller issue the loads of several output groups before
+// their stores: the compiler cannot move a load above a store that may alias it.
+struct Gated4 {
+  float r[4], g[4];
+};
+
+template <int DT>
+__device__ __forceinline__ void gate_load4(const GatedResidual& gr, int m, int n, int N, bool vec, Gated4& v) {
+  const int64_t idx = (int64_t)m * N + n;
+  const int64_t gi = (int64_t)(m / gr.rows_per_gate) * gr.gate_stride + n;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v.g[j] = 1.0f;
+  if (vec) {
+    load_elem4<DT>(gr.residual, idx, v.r);
+    if (gr.gate) {
+      if ((gr.gate_stride & 3) == 0) {
+        load_elem4<DT>(gr.gate, gi, v.g);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v.g[j] = load_elem<DT>(gr.gate, gi + j);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v.r[j] = n + j < N ? load_elem<DT>(gr.residual, idx + j) : 0.0f;
+      if (gr.gate && n + j < N) v.g[j] = load_elem<DT>(gr.gate, gi + j);
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void gate_apply4(const Gated4& v, float (&o)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = gated_sum<DT>(o[j], v.r[j], v.g[j]);
+}
+
+template <int DT>
+__device__ __forceinline__ void gate_residual4(const GatedResidual& gr, int m, int n, int N, bool vec,
+                                               float (&o)[4]) {
+  Gated4 v;
+  gate_load4<DT>(gr, m, n, N, vec, v);
+  gate_apply4<DT>(v, o);
+}
+
+// The same for 8 16-bit outputs (row m, columns n..n+7): raw residual and gate
+// bits, and the combination with 8 outputs already rounded and packed in `lin`.
+struct Gated8 {
+  uint4 r, g;
+};
+
+template <int DT>
+__device__ __forceinline__ void gate_load8(const GatedResidual& gr, int m, int n, int N, bool vec, Gated8& v) {
+  static_assert(DT == kBF16 || DT == kF16, "16-bit outputs only");
+  const int64_t idx = (int64_t)m * N + n;
+  const int64_t gi = (int64_t)(m / gr.rows_per_gate) * gr.gate_stride + n;
+  const uint16_t* res = (const uint16_t*)gr.residual + idx;
+  const uint16_t* gp = (const uint16_t*)gr.gate + gi;
+  const uint32_t one = DT == kBF16 ? 0x3f80u : 0x3c00u;
+  if (vec) {
+    v.r = *(const uint4*)res;
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (n + 2 * i < N ? (uint32_t)res[2 * i] : 0u) | (n + 2 * i + 1 < N ? (uint32_t)res[2 * i + 1] << 16 : 0u);
+    v.r = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  if (!gr.gate) {
+    v.g = make_uint4(one * 0x10001u, one * 0x10001u, one * 0x10001u, one * 0x10001u);
+  } else if (vec && (gr.gate_stride & 7) == 0) {
+    v.g = *(const uint4*)gp;
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (n + 2 * i < N ? (uint32_t)gp[2 * i] : one) | (n + 2 * i + 1 < N ? (uint32_t)gp[2 * i + 1] : one) << 16;
+    v.g = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ uint4 gate_apply8(const Gated8& v, uint4 lin) {
+  const uint32_t lw[4] = {lin.x, lin.y, lin.z, lin.w};
+  const uint32_t rw[4] = {v.r.x, v.r.y, v.r.z, v.r.w};
+  const uint32_t gw[4] = {v.g.x, v.g.y, v.g.z, v.g.w};
+  uint32_t ow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float lo, hi;
+    if constexpr (DT == kBF16) {
+      lo = gated_sum<DT>(bf16_lo(lw[i]), bf16_lo(rw[i]), bf16_lo(gw[i]));
+      hi = gated_sum<DT>(bf16_hi(lw[i]), bf16_hi(rw[i]), bf16_hi(gw[i]));
+      ow[i] = pack_bf16x2(lo, hi);
+    } else {
+      typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+      const f16x2 l = __builtin_bit_cast(f16x2, lw[i]), r = __builtin_bit_cast(f16x2, rw[i]),
+                  g = __builtin_bit_cast(f16x2, gw[i]);
+      lo = gated_sum<DT>((float)l.x, (float)r.x, (float)g.x);
+      hi = gated_sum<DT>((float)l.y, (float)r.y, (float)g.y);
+      ow[i] = pack_f16x2(lo, hi);
+    }
+  }
+  return make_uint4(ow[0], ow[1], ow[2], ow[3]);
+}
+
 // Signed nibbles of one 32-bit word of a CDNA4 weight block, expanded to int8
 // scaled by 16: byte j of `lo` is 16*k[j], byte j of `hi` is 16*k[j+4], where
 // k[j] is the low nibble and k[j+4] the high nibble of byte j.

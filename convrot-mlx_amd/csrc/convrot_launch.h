@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include "../../include/convrot_amd.h"
+#include "convrot_device.h"
 
 namespace convrot {
 
@@ -28,13 +29,14 @@ hipError_t launch_prep_gelu(const void* head, int64_t head_features, int64_t hea
 
 hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
                             const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
-                            void* out, int out_dtype, hipStream_t stream);
+                            void* out, int out_dtype, hipStream_t stream,
+                            const GatedResidual& gr = GatedResidual{});
 
 // Few-row W4A4 kernel (int8 activation codes only); launch_w4a4_gemm routes
 // small M here.
 hipError_t launch_w4a4_smallm(const int8_t* act, const float* xscales, const uint8_t* qweight,
                               const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K, void* out,
-                              int out_dtype, hipStream_t stream);
+                              int out_dtype, hipStream_t stream, const GatedResidual& gr = GatedResidual{});
 
 // Compute units of the current device (cached per device).
 int device_cus();

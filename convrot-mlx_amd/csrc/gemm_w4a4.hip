@@ -50,7 +50,7 @@ template <int BM, int BN, int WM, int WN, bool APACK, int ODT>
 __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_kernel(
     const uint8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
-    int K, int nblocks, int kblocks, int tiles_m, int tiles_n) {
+    int K, int nblocks, int kblocks, int tiles_m, int tiles_n, GatedResidual gr) {
   constexpr int NT = WM * WN * 64;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 16, FN = TN / 16;
@@ -194,6 +194,7 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_kernel(
         v = v + bv[r];
         o[r] = v;
       }
+      if (gr.residual) gate_residual4<ODT>(gr, m, n, N, vec_ok, o);
       const int64_t idx = (int64_t)m * N + n;
       if (vec_ok) {
         store_out4<ODT>(out, idx, o[0], o[1], o[2], o[3]);
@@ -218,11 +219,17 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_kernel(
 // Operands: xs[m], ws[n] and bias[n] come from global memory, or (LDS_OPS)
 // from the tile's LDS copies xs[m - m0], ws[n - n0], bias[n - n0] (rows and
 // columns past M / N hold zeros there and are never stored).
+//
+// With gr.residual set, the gated residual follows the rounding of the linear
+// (GatedResidual); for 16-bit outputs it is applied in the write-back loop,
+// where each lane holds 8 consecutive outputs of one row and loads the
+// matching residual and gate elements as 16-byte reads.
 template <int ODT, int TM, int TN, int SHIFT, bool LDS_OPS = false>
 __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], uint8_t* region, int lane,
                                          int mw, int nw, int M, int N, const float* __restrict__ xscales,
                                          const float* __restrict__ wscales, const float* __restrict__ bias,
-                                         void* __restrict__ out, int m0 = 0, int n0 = 0) {
+                                         void* __restrict__ out, const GatedResidual& gr, int m0 = 0,
+                                         int n0 = 0) {
   constexpr int FM = TM / 16, FN = TN / 16;
   float xs[FM];
 #pragma unroll
@@ -251,13 +258,29 @@ __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], u
           bv[r] = bias ? bias[nn] : 0.0f;
         }
       }
+      // Residual / gate operands of FB fragments at a time go out before
+      // their stores.  The accumulators are still live here: the 128 x 64
+      // wave tile (256 x 256 workgroup) has no registers to spare for them.
+      constexpr int FB = TM * TN >= 128 * 64 ? 1 : FM;
+      Gated4 ops[FB];
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
+        if (FB > 1 && gr.residual && fm % FB == 0) {
+#pragma unroll
+          for (int i = 0; i < FB; ++i) {
+            const int m = mw + (fm + i) * 16 + (lane & 15);
+            if (m < M) gate_load4<ODT>(gr, m, n, N, vec_ok, ops[i]);
+          }
+        }
         const int m = mw + fm * 16 + (lane & 15);
         if (m >= M) continue;
         float o[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = (((float)(acc[fn][fm][r] >> SHIFT) * xs[fm]) * wsv[r]) + bv[r];
+        if (gr.residual) {
+          if constexpr (FB > 1) gate_apply4<ODT>(ops[fm % FB], o);
+          else gate_residual4<ODT>(gr, m, n, N, vec_ok, o);
+        }
         const int64_t idx = (int64_t)m * N + n;
         if (vec_ok) {
           store_out4<ODT>(out, idx, o[0], o[1], o[2], o[3]);
@@ -302,22 +325,48 @@ __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], u
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     constexpr int CPR = TN / 8;        // 16-byte chunks per row
     constexpr int RPI = 64 / CPR;      // rows per wave instruction
+    constexpr int NIT = TM / RPI;      // write-back iterations
     const int cr = lane / CPR, cc = lane % CPR;
-    const bool vec_ok = (N & 7) == 0;
-#pragma unroll
-    for (int r0 = 0; r0 < TM; r0 += RPI) {
-      const int rl = r0 + cr;
-      const int m = mw + rl, n = nw + cc * 8;
-      if (m >= M || n >= N) continue;
-      const uint4 v = *(const uint4*)(region + rl * RS + cc * 16);
-      uint16_t* dst = (uint16_t*)out + (int64_t)m * N + n;
-      if (vec_ok && n + 8 <= N) {
+    const int n = nw + cc * 8;
+    const bool vec = (N & 7) == 0 && n + 8 <= N;
+    auto store_row = [&](int it, uint4 v) {
+      uint16_t* dst = (uint16_t*)out + (int64_t)(mw + it * RPI + cr) * N + n;
+      if (vec) {
         *(uint4*)dst = v;
       } else {
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           if (n + j < N) dst[j] = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+      }
+    };
+    if (!gr.residual) {
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int rl = it * RPI + cr;
+        if (mw + rl >= M || n >= N) continue;
+        store_row(it, *(const uint4*)(region + rl * RS + cc * 16));
+      }
+    } else {
+      // Residual and gate loads of BATCH rows go out before their stores (a
+      // load cannot be moved above a store that may alias it, so one row at a
+      // time would wait a memory round trip per row).
+      constexpr int BATCH = NIT < 8 ? NIT : 8;
+      static_assert(NIT % BATCH == 0, "write-back batches");
+#pragma unroll
+      for (int b0 = 0; b0 < NIT; b0 += BATCH) {
+        Gated8 ops[BATCH];
+#pragma unroll
+        for (int i = 0; i < BATCH; ++i) {
+          const int m = mw + (b0 + i) * RPI + cr;
+          if (m < M && n < N) gate_load8<ODT>(gr, m, n, N, vec, ops[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < BATCH; ++i) {
+          const int rl = (b0 + i) * RPI + cr;
+          if (mw + rl >= M || n >= N) continue;
+          store_row(b0 + i, gate_apply8<ODT>(ops[i], *(const uint4*)(region + rl * RS + cc * 16)));
+        }
       }
     }
   }
@@ -607,7 +656,7 @@ template <int BM, int BN, int WM, int WN, int PIPE, int STAGES, int ODT>
 __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
     const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
-    int K, int nblocks, int kblocks, int tiles_m, int tiles_n) {
+    int K, int nblocks, int kblocks, int tiles_m, int tiles_n, GatedResidual gr) {
   using E = DmaEngine<BM, BN, WM, WN, PIPE, STAGES>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
   E e(smem);
@@ -629,7 +678,7 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
   e.run(0, kblocks, acc);
   __syncthreads();  // all waves done with the LDS ring before it is reused for output staging
   epilogue<ODT, E::TM, E::TN, E::SHIFT, true>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M,
-                                              N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, m0, n0);
+                                              N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, gr, m0, n0);
 }
 
 // ---- stream-K
@@ -754,7 +803,8 @@ template <int BM, int BN, int WM, int WN, int PIPE, int STAGES, int ODT>
 __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
     const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
-    int K, int nblocks, int kblocks, int tiles_m, int tiles_n, uint8_t* __restrict__ work, int min_iters) {
+    int K, int nblocks, int kblocks, int tiles_m, int tiles_n, uint8_t* __restrict__ work, int min_iters,
+    GatedResidual gr) {
   using E = DmaEngine<BM, BN, WM, WN, PIPE, STAGES>;
   constexpr int FN = E::FN, FM = E::FM, NW = E::NW;
   static_assert(NW <= kSkMaxWaves, "flag block sized for 8 waves");
@@ -869,7 +919,7 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
       }
       __syncthreads();  // ring -> epilogue staging
       epilogue<ODT, E::TM, E::TN, E::SHIFT, true>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN,
-                                                  M, N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, m0, n0);
+                                                  M, N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, gr, m0, n0);
       __syncthreads();  // staging -> next item's DMA
     }
     t = nt;
@@ -1072,18 +1122,19 @@ size_t sk_workspace_bytes(const Plan& plan) {
 
 template <int BM, int BN, int WM, int WN, bool APACK, int ODT>
 hipError_t launch_tile(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
-                       int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+                       int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
   const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
   hipLaunchKernelGGL((w4a4_gemm_kernel<BM, BN, WM, WN, APACK, ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
                      0, stream, (const uint8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks,
-                     tm, tn);
+                     tm, tn, gr);
   return hipGetLastError();
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES, int ODT>
 hipError_t launch_dma(const Plan& plan, const void* act, const float* xs, const uint8_t* wq, const float* ws,
-                      const float* bias, int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+                      const float* bias, int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr,
+                      hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
   const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
   // Double-buffered fragments except on the 8-wave 256x256 tile, whose
@@ -1093,26 +1144,26 @@ hipError_t launch_dma(const Plan& plan, const void* act, const float* xs, const 
     if (uint8_t* work = sk_workspace(stream, sk_workspace_bytes(plan))) {
       hipLaunchKernelGGL((w4a4_gemm_sk_kernel<BM, BN, WM, WN, kPP, STAGES, ODT>), dim3((unsigned)plan.grid),
                          dim3(WM * WN * 64), 0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N,
-                         (int)K, nblocks, kblocks, tm, tn, work, plan.min_iters);
+                         (int)K, nblocks, kblocks, tm, tn, work, plan.min_iters, gr);
       return hipGetLastError();
     }
   }
   hipLaunchKernelGGL((w4a4_gemm_dma_kernel<BM, BN, WM, WN, kPP, STAGES, ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
                      0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks,
-                     tm, tn);
+                     tm, tn, gr);
   return hipGetLastError();
 }
 
 template <bool APACK, int ODT>
 hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
-                    int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+                    int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
   const bool dma = !APACK && !getenv("CONVROT_GEMM_NO_DMA");
   const Plan plan = choose_plan(M, N, K, dma);
   const Tile t = plan.t;
   if (dma) {
 #define CONVROT_DMA(BM_, BN_, WM_, WN_, S_)                                       \
   if (t.bm == BM_ && t.bn == BN_ && t.wm == WM_ && t.wn == WN_ && t.stages == S_) \
-    return launch_dma<BM_, BN_, WM_, WN_, S_, ODT>(plan, act, xs, wq, ws, bias, M, N, K, out, stream);
+    return launch_dma<BM_, BN_, WM_, WN_, S_, ODT>(plan, act, xs, wq, ws, bias, M, N, K, out, gr, stream);
     CONVROT_DMA(256, 256, 2, 4, 3)
     CONVROT_DMA(256, 128, 4, 2, 3)
     CONVROT_DMA(128, 256, 2, 4, 3)
@@ -1122,7 +1173,7 @@ hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const f
   }
 #define CONVROT_TILE(BM_, BN_, WM_, WN_)                    \
   if (t.bm == BM_ && t.bn == BN_ && t.wm == WM_ && t.wn == WN_) \
-    return launch_tile<BM_, BN_, WM_, WN_, APACK, ODT>(act, xs, wq, ws, bias, M, N, K, out, stream);
+    return launch_tile<BM_, BN_, WM_, WN_, APACK, ODT>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
   CONVROT_TILE(256, 256, 2, 4)
   CONVROT_TILE(256, 256, 4, 2)
   CONVROT_TILE(256, 256, 2, 2)
@@ -1131,16 +1182,17 @@ hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const f
   CONVROT_TILE(128, 256, 2, 2)
   CONVROT_TILE(128, 256, 2, 4)
 #undef CONVROT_TILE
-  return launch_tile<128, 128, 2, 2, APACK, ODT>(act, xs, wq, ws, bias, M, N, K, out, stream);
+  return launch_tile<128, 128, 2, 2, APACK, ODT>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
 }
 
 template <bool APACK>
 hipError_t launch_odt(int odt, const void* act, const float* xs, const uint8_t* wq, const float* ws,
-                      const float* bias, int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+                      const float* bias, int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr,
+                      hipStream_t stream) {
   switch (odt) {
-    case kF32: return launch_t<APACK, kF32>(act, xs, wq, ws, bias, M, N, K, out, stream);
-    case kF16: return launch_t<APACK, kF16>(act, xs, wq, ws, bias, M, N, K, out, stream);
-    default: return launch_t<APACK, kBF16>(act, xs, wq, ws, bias, M, N, K, out, stream);
+    case kF32: return launch_t<APACK, kF32>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
+    case kF16: return launch_t<APACK, kF16>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
+    default: return launch_t<APACK, kBF16>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
   }
 }
 
@@ -1152,10 +1204,10 @@ constexpr int64_t kSmallMWideElems = 40000000;  // N * K, i.e. 20 MB of int4 wei
 
 hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
                             const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
-                            void* out, int out_dtype, hipStream_t stream) {
+                            void* out, int out_dtype, hipStream_t stream, const GatedResidual& gr) {
   if (M == 0 || N == 0) return hipSuccess;
   if (act_format == CONVROT_ACT_PACKED)
-    return launch_odt<true>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, stream);
+    return launch_odt<true>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, gr, stream);
   // Few rows: the weight-streaming kernel (same results bit for bit).  It
   // wins up to M = 32 everywhere measured, and up to 64 while the int4 weight
   // is at most ~20 MB (beyond that the tiled kernel's 16-17 us floor is lower).
@@ -1163,8 +1215,9 @@ hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscale
   int64_t small_max = N * K <= kSmallMWideElems ? kSmallMMaxWide : kSmallMMax;
   if (const char* env = getenv("CONVROT_GEMM_SMALLM_MAX")) small_max = atoll(env);
   if (M <= small_max)
-    return launch_w4a4_smallm((const int8_t*)act, xscales, qweight, wscales, bias, M, N, K, out, out_dtype, stream);
-  return launch_odt<false>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, stream);
+    return launch_w4a4_smallm((const int8_t*)act, xscales, qweight, wscales, bias, M, N, K, out, out_dtype, stream,
+                              gr);
+  return launch_odt<false>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, gr, stream);
 }
 
 }  // namespace convrot

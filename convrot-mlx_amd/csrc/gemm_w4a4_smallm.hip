@@ -33,7 +33,7 @@ __global__ __launch_bounds__(SPLIT * 64) __attribute__((amdgpu_waves_per_eu(FM =
 void w4a4_smallm_kernel(const int8_t* __restrict__ act, const float* __restrict__ xscales,
                         const uint8_t* __restrict__ wq, const float* __restrict__ wscales,
                         const float* __restrict__ bias, void* __restrict__ out, int M, int N, int K, int nblocks,
-                        int kblocks) {
+                        int kblocks, GatedResidual gr) {
   __shared__ __attribute__((aligned(16))) i32x4 red[SPLIT > 1 ? SPLIT : 1][NB * FM][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nb0 = blockIdx.x * NB;
@@ -106,7 +106,8 @@ void w4a4_smallm_kernel(const int8_t* __restrict__ act, const float* __restrict_
       }
   }
 
-  // ---- epilogue (core.py:1168-1170 order): ((f(dot) * xs) * ws) + bias, one rounding per op
+  // ---- epilogue (core.py:1168-1170 order): ((f(dot) * xs) * ws) + bias, one rounding per op,
+  // then the optional gated residual
   const bool vec_ok = (N & 3) == 0;
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
@@ -123,6 +124,9 @@ void w4a4_smallm_kernel(const int8_t* __restrict__ act, const float* __restrict_
         const int nn = n + j < N ? n + j : N - 1;
         o[j] = (((float)(acc[t][fm][j] >> 4) * xs) * wscales[nn]) + (bias ? bias[nn] : 0.0f);
       }
+      // One fragment at a time: holding the operands of all FM x NB fragments
+      // raises the register count (and lowers occupancy) of every launch.
+      if (gr.residual) gate_residual4<ODT>(gr, m, n, N, vec_ok, o);
       const int64_t idx = (int64_t)m * N + n;
       if (vec_ok) {
         store_out4<ODT>(out, idx, o[0], o[1], o[2], o[3]);
@@ -137,11 +141,11 @@ void w4a4_smallm_kernel(const int8_t* __restrict__ act, const float* __restrict_
 
 template <int ODT, int FM, int NB, int SPLIT, int KPW>
 hipError_t launch_t(const int8_t* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
-                    int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+                    int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
   dim3 grid((unsigned)((nblocks + NB - 1) / NB), (unsigned)((M + 16 * FM - 1) / (16 * FM)));
   hipLaunchKernelGGL((w4a4_smallm_kernel<ODT, FM, NB, SPLIT, KPW>), grid, dim3(64 * SPLIT), 0, stream, act, xs, wq,
-                     ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks);
+                     ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, gr);
   return hipGetLastError();
 }
 
@@ -158,16 +162,16 @@ hipError_t launch_t(const int8_t* act, const float* xs, const uint8_t* wq, const
 // overrides the choice.
 template <int ODT>
 hipError_t launch_shape(const int8_t* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
-                        int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+                        int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
   const int64_t nblocks = (N + 15) / 16;
   char cfg = M > 32 ? 'C' : (M <= 16 && nblocks <= 256 ? 'B' : 'A');
   if (const char* env = getenv("CONVROT_W4A4_SMALLM_CFG"))
     if (env[0] == 'A' || env[0] == 'B' || env[0] == 'C' || env[0] == 'F') cfg = env[0];
   switch (cfg) {
-    case 'A': return launch_t<ODT, 1, 2, 8, 3>(act, xs, wq, ws, bias, M, N, K, out, stream);
-    case 'B': return launch_t<ODT, 1, 1, 16, 4>(act, xs, wq, ws, bias, M, N, K, out, stream);
-    case 'C': return launch_t<ODT, 2, 2, 8, 2>(act, xs, wq, ws, bias, M, N, K, out, stream);
-    default: return launch_t<ODT, 4, 2, 4, 2>(act, xs, wq, ws, bias, M, N, K, out, stream);
+    case 'A': return launch_t<ODT, 1, 2, 8, 3>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'B': return launch_t<ODT, 1, 1, 16, 4>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'C': return launch_t<ODT, 2, 2, 8, 2>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
+    default: return launch_t<ODT, 4, 2, 4, 2>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
   }
 }
 
@@ -175,12 +179,12 @@ hipError_t launch_shape(const int8_t* act, const float* xs, const uint8_t* wq, c
 
 hipError_t launch_w4a4_smallm(const int8_t* act, const float* xscales, const uint8_t* qweight,
                               const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K, void* out,
-                              int out_dtype, hipStream_t stream) {
+                              int out_dtype, hipStream_t stream, const GatedResidual& gr) {
   if (M == 0 || N == 0) return hipSuccess;
   switch (out_dtype) {
-    case kF32: return launch_shape<kF32>(act, xscales, qweight, wscales, bias, M, N, K, out, stream);
-    case kF16: return launch_shape<kF16>(act, xscales, qweight, wscales, bias, M, N, K, out, stream);
-    default: return launch_shape<kBF16>(act, xscales, qweight, wscales, bias, M, N, K, out, stream);
+    case kF32: return launch_shape<kF32>(act, xscales, qweight, wscales, bias, M, N, K, out, gr, stream);
+    case kF16: return launch_shape<kF16>(act, xscales, qweight, wscales, bias, M, N, K, out, gr, stream);
+    default: return launch_shape<kBF16>(act, xscales, qweight, wscales, bias, M, N, K, out, gr, stream);
   }
 }
 

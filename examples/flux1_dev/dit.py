@@ -163,12 +163,42 @@ def set_fused_modulation(model: nn.Module, on: bool) -> None:
 
 
 def set_fused_gelu(model: nn.Module, on: bool) -> None:
-    """With `on`, each single block feeds linear2 through ConvRotLinear.forward_gelu: the tanh
-    GELU of the MLP half and its concatenation with the attention output run inside the
-    activation preparation, reading the MLP slice of linear1's output in place."""
+    """With `on`, every MLP-down Linear takes its input through ConvRotLinear.forward_gelu: the
+    tanh GELU (and, in the single blocks, the concatenation with the attention output, read
+    from linear1's output in place) runs inside the activation preparation."""
     for m in model.modules():
         if hasattr(m, "fused_gelu"):
             m.fused_gelu = on
+
+
+def set_fused_residual(model: nn.Module, on: bool) -> None:
+    """With `on`, every gated residual `x + gate * linear(...)` that closes a block branch runs
+    in the ConvRotLinear's GEMM epilogue (residual=, gate=) instead of two torch ops."""
+    for m in model.modules():
+        if hasattr(m, "fused_residual"):
+            m.fused_residual = on
+
+
+def project(linear: nn.Module, x: torch.Tensor, *, gelu: bool = False, head: torch.Tensor | None = None,
+            residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
+            fused_gelu: bool = False, fused_residual: bool = False) -> torch.Tensor:
+    """residual + gate * linear(input) (or linear(input) without a residual), where input is
+    x, gelu_tanh(x) (`gelu`) or cat([head, gelu_tanh(x)]).  The GELU / concatenation and the
+    gated residual move into a ConvRotLinear's preparation and epilogue when their flags are
+    set; otherwise they are the torch ops FLUX uses."""
+    convrot = hasattr(linear, "forward_gelu")
+    kw = dict(residual=residual, gate=gate) if fused_residual and convrot and residual is not None else {}
+    if gelu and fused_gelu and convrot:
+        out = linear.forward_gelu(x, head=head, **kw)
+    else:
+        if gelu:
+            x = F.gelu(x, approximate="tanh")
+        if head is not None:
+            x = torch.cat([head, x], dim=-1)
+        out = linear(x, **kw)
+    if residual is None or kw:
+        return out
+    return residual + gate * out
 
 
 def _split_heads(qkv: torch.Tensor, heads: int):
@@ -182,7 +212,7 @@ class DoubleStreamBlock(nn.Module):
         super().__init__()
         mlp_hidden = int(hidden * mlp_ratio)
         self.heads = heads
-        self.fused_modulation = False
+        self.fused_modulation = self.fused_gelu = self.fused_residual = False
         for side in ("img", "txt"):
             setattr(self, f"{side}_mod", Modulation(hidden, double=True))
             setattr(self, f"{side}_qkv", nn.Linear(hidden, 3 * hidden, bias=qkv_bias))
@@ -201,10 +231,14 @@ class DoubleStreamBlock(nn.Module):
         tq, tk = self.txt_qknorm(tq, tk)
         attn = attention(torch.cat([tq, iq], 2), torch.cat([tk, ik], 2), torch.cat([tv, iv], 2), pe)
         t_attn, i_attn = attn[:, : txt.shape[1]], attn[:, txt.shape[1]:]
-        img = img + i_gate1 * self.img_proj(i_attn)
-        img = img + i_gate2 * self.img_mlp[2](self.img_mlp[1](modulated(self.img_mlp[0], img, i_shift2, i_scale2, fu)))
-        txt = txt + t_gate1 * self.txt_proj(t_attn)
-        txt = txt + t_gate2 * self.txt_mlp[2](self.txt_mlp[1](modulated(self.txt_mlp[0], txt, t_shift2, t_scale2, fu)))
+        flags = dict(fused_gelu=self.fused_gelu, fused_residual=self.fused_residual)
+        # img_mlp[1] / txt_mlp[1] are nn.GELU(approximate="tanh"): project applies it (gelu=True)
+        img = project(self.img_proj, i_attn, residual=img, gate=i_gate1, **flags)
+        img = project(self.img_mlp[2], modulated(self.img_mlp[0], img, i_shift2, i_scale2, fu), gelu=True,
+                      residual=img, gate=i_gate2, **flags)
+        txt = project(self.txt_proj, t_attn, residual=txt, gate=t_gate1, **flags)
+        txt = project(self.txt_mlp[2], modulated(self.txt_mlp[0], txt, t_shift2, t_scale2, fu), gelu=True,
+                      residual=txt, gate=t_gate2, **flags)
         return img, txt
 
 
@@ -217,8 +251,7 @@ class SingleStreamBlock(nn.Module):
         self.linear2 = nn.Linear(hidden + self.mlp_hidden, hidden)
         self.norm = QKNorm(hidden // heads)
         self.modulation = Modulation(hidden, double=False)
-        self.fused_modulation = False
-        self.fused_gelu = False
+        self.fused_modulation = self.fused_gelu = self.fused_residual = False
 
     def forward(self, x, vec, pe):
         (shift, scale, gate), _ = self.modulation(vec)
@@ -227,11 +260,8 @@ class SingleStreamBlock(nn.Module):
         q, k, v = _split_heads(qkv, self.heads)
         q, k = self.norm(q, k)
         attn = attention(q, k, v, pe)
-        if self.fused_gelu and hasattr(self.linear2, "forward_gelu"):
-            out = self.linear2.forward_gelu(mlp, head=attn)
-        else:
-            out = self.linear2(torch.cat([attn, F.gelu(mlp, approximate="tanh")], dim=-1))
-        return x + gate * out
+        return project(self.linear2, mlp, gelu=True, head=attn, residual=x, gate=gate,
+                       fused_gelu=self.fused_gelu, fused_residual=self.fused_residual)
 
 
 class Flux(nn.Module):
@@ -368,6 +398,9 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
     set_fused_gelu(model, True)
     both, both_ms, both_graph_ms = time_step(model, inputs, steps)
     both = both.float()
+    set_fused_residual(model, True)
+    allf, all_ms, all_graph_ms = time_step(model, inputs, steps)
+    allf = allf.float()
 
     def dev_stats(out):
         diff = out - dense
@@ -378,6 +411,7 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
     rel, cos, mad = dev_stats(quant)
     frel, fcos, _ = dev_stats(fused)
     brel, bcos, _ = dev_stats(both)
+    arel, acos, _ = dev_stats(allf)
     return {
         "what": "random-init FLUX.1-dev DiT, one denoising step, batch 1, "
                 f"{img_tokens} image + {txt_tokens} text tokens, bf16",
@@ -395,12 +429,20 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
             "rel_l2_vs_unfused": round(((fused - quant).norm() / quant.norm()).item(), 5),
         },
         "fused_modulation_and_gelu": {
-            "what": "as fused_modulation, and each single block's tanh GELU + concatenation fused into "
-                    "linear2's activation preparation (38 sites)",
+            "what": "as fused_modulation, and every MLP-down Linear's tanh GELU (with the single blocks' "
+                    "concatenation) fused into its activation preparation (76 sites)",
             "eager_ms": round(both_ms, 2), "graph_ms": round(both_graph_ms, 2),
             "graph_speedup_vs_dense": round(dense_graph_ms / both_graph_ms, 3),
             "rel_l2_vs_dense": brel, "cosine_vs_dense": bcos,
             "rel_l2_vs_fused_modulation": round(((both - fused).norm() / fused.norm()).item(), 5),
+        },
+        "fused_producers_and_residual": {
+            "what": "as fused_modulation_and_gelu, and every gated residual x + gate * linear(...) in the "
+                    "W4A4 GEMM epilogue (114 sites: 4 per double block, 1 per single block)",
+            "eager_ms": round(all_ms, 2), "graph_ms": round(all_graph_ms, 2),
+            "graph_speedup_vs_dense": round(dense_graph_ms / all_graph_ms, 3),
+            "rel_l2_vs_dense": arel, "cosine_vs_dense": acos,
+            "identical_to_fused_modulation_and_gelu": bool(torch.equal(allf, both)),
         },
     }
 
@@ -413,10 +455,11 @@ def profile_variant(variant: str, steps: int, group_size: int = 64) -> dict:
     dev = torch.device("cuda:0")
     model = build(p, dev)
     inputs = make_inputs(p, 1024, 512, dev)
-    if variant in ("convrot", "fused", "fused_gelu"):
+    if variant in ("convrot", "fused", "fused_gelu", "fused_all"):
         replace_convrot_linears(model, backend="hip-w4a4", group_size=group_size)
-        set_fused_modulation(model, variant in ("fused", "fused_gelu"))
-        set_fused_gelu(model, variant == "fused_gelu")
+        set_fused_modulation(model, variant in ("fused", "fused_gelu", "fused_all"))
+        set_fused_gelu(model, variant in ("fused_gelu", "fused_all"))
+        set_fused_residual(model, variant == "fused_all")
     with torch.no_grad():
         model(**inputs)
         torch.cuda.synchronize()
@@ -429,9 +472,11 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--group-size", type=int, default=64)
-    ap.add_argument("--variant", choices=["both", "dense", "convrot", "fused", "fused_gelu"], default="both",
-                    help="'dense', 'convrot', 'fused' (convrot with fused modulation) or 'fused_gelu' (and "
-                         "the single blocks' GELU fused too) runs eager steps of that model only, for profiling")
+    ap.add_argument("--variant", choices=["both", "dense", "convrot", "fused", "fused_gelu", "fused_all"],
+                    default="both",
+                    help="'dense', 'convrot', 'fused' (convrot with fused modulation), 'fused_gelu' (and the "
+                         "MLP GELUs fused too) or 'fused_all' (and the gated residuals in the GEMM epilogue) "
+                         "runs eager steps of that model only, for profiling")
     args = ap.parse_args()
     if args.variant == "both":
         print(json.dumps(config5_figure(group_size=args.group_size, steps=args.steps)), flush=True)

@@ -130,6 +130,29 @@ int convrot_w4a4_gemm(const void* act, int act_format, const float* xscales,
                       void* stream);
 
 /*
+ * convrot_w4a4_gemm followed, inside the same kernel, by a gated residual:
+ *   lin = the output convrot_w4a4_gemm would store (rounded to out_dtype)
+ *   out[m, n] = out_dtype(residual[m, n] + out_dtype(gate[m / rows_per_gate, n] * lin))
+ * each op in float32 and rounded to out_dtype, as torch evaluates
+ * `residual + gate * linear(x)` eagerly.  No counterpart in the reference: it
+ * fuses the consumer of a DiT block's projection Linears (FLUX's
+ * x + gate * proj(...) after every attention and MLP branch) into the GEMM, the
+ * consumer side of the fused preparation the reference names as its open
+ * target (/root/reference/docs/design.md:54-64).
+ * residual: [M, N] contiguous, out_dtype, 16-byte aligned; it may be `out`
+ * itself (in place) but must not otherwise overlap it.  gate: NULL for a plain
+ * residual add (out = out_dtype(residual + lin)), else out_dtype rows of N
+ * elements, gate_stride elements apart, 16-byte aligned, not overlapping out;
+ * output row m reads gate row m / rows_per_gate (rows_per_gate >= 1; any value
+ * >= M broadcasts gate row 0).  Other arguments as convrot_w4a4_gemm.
+ */
+int convrot_w4a4_gemm_residual(const void* act, int act_format, const float* xscales,
+                               const uint8_t* qweight, const float* wscales, const float* bias,
+                               int64_t M, int64_t N, int64_t K, const void* residual,
+                               const void* gate, int64_t gate_stride, int64_t rows_per_gate,
+                               void* out, int out_dtype, void* stream);
+
+/*
  * W4A16 GEMM: out[m, n] = out_dtype((dot_f32(act[m, :], w[n, :]) * wscales[n]) + bias[n]).
  * Replaces mpp_w4a16_matmul (core.py:1123-1152): the MPP float x int4 TensorOp
  * (core.py:877-912) plus the elementwise epilogue (core.py:1151-1152).

@@ -214,6 +214,24 @@ def gelu_producer_rows(head: np.ndarray | None, x: np.ndarray, dtype: str) -> np
     return g if head is None or head.shape[-1] == 0 else np.ascontiguousarray(np.concatenate([head, g], axis=-1))
 
 
+def gated_residual(lin: np.ndarray, residual: np.ndarray, gate: np.ndarray | None, rows_per_gate: int,
+                   dtype: str) -> np.ndarray:
+    """Consumer of the gated-residual GEMM epilogue (no reference counterpart: a DiT
+    block's `x + gate * linear(...)`, two eager elementwise ops):
+        out[m] = dt(residual[m] + dt(gate[m // rows_per_gate] * lin[m]))
+    on [M, N] arrays of dtype bits (float32 values for "float32"), each op one float32
+    IEEE operation rounded once to dtype (numpy float32 arithmetic, then from_f32).
+    gate: [G, N] rows, or None for dt(residual + lin)."""
+    lin32 = to_f32(lin, dtype)
+    res32 = to_f32(residual, dtype)
+    if gate is None:
+        return from_f32(res32 + lin32, dtype)
+    rows = np.arange(lin.shape[0]) // rows_per_gate
+    g32 = to_f32(np.ascontiguousarray(gate), dtype)[rows]
+    prod = to_f32(from_f32(g32 * lin32, dtype), dtype)
+    return from_f32(res32 + prod, dtype)
+
+
 def w4a4_matmul_codes(a_codes, w_codes, xscales, wscales, bias, out_dtype: str, want_dots: bool = False):
     """reference_w4a4_matmul (core.py:1155-1171) on unpacked codes (w in NK orientation)."""
     a_codes = np.ascontiguousarray(a_codes, dtype=np.int8)

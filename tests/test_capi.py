@@ -125,6 +125,29 @@ def test_prepare_gelu_validation(lib):
     assert _err(lib) == "null pointer argument"
 
 
+def test_gemm_residual_validation(lib):
+    """convrot_w4a4_gemm_residual(act, fmt, xs, qw, ws, bias, M, N, K, residual, gate, gate_stride,
+    rows_per_gate, out, dtype, stream): every call below fails its checks before any launch
+    (the non-null pointers are placeholders that are never dereferenced)."""
+    g = lib.convrot_w4a4_gemm_residual
+    p = 0x10000  # 16-byte aligned placeholder
+    assert g(None, 1, None, None, None, None, 4, 32, 48, None, None, 0, 1, None, BF16, None) == 1
+    assert _err(lib) == "W4A4 GEMM requires K divisible by 32, got 48"
+    assert g(p, 1, p, p, p, None, 4, 32, 64, p, p, 32, 0, p, BF16, None) == 1
+    assert _err(lib) == "rows_per_gate must be positive, got 0"
+    assert g(p, 1, p, p, p, None, 0, 32, 64, None, None, 0, 1, p, BF16, None) == 0  # no rows: nothing to do
+    assert g(p, 1, p, p, p, None, 4, 32, 64, None, None, 0, 1, p, BF16, None) == 1
+    assert _err(lib) == "null pointer argument"
+    assert g(p, 1, p, p, p, None, 4, 32, 64, p + 8, None, 0, 1, p, BF16, None) == 1
+    assert _err(lib) == "residual and gate must be 16-byte aligned"
+    assert g(p, 1, p, p, p, None, 4, 32, 64, p, p + 4, 32, 2, p, BF16, None) == 1
+    assert _err(lib) == "residual and gate must be 16-byte aligned"
+    assert g(p, 1, p, p, p, None, 4, 32, 64, p, p, 16, 2, p, BF16, None) == 1
+    assert _err(lib) == "gate rows 16 elements apart overlap (N=32)"
+    assert g(p, 1, p, p, p, None, 4, 32, 64, p, p, 16, 2, p + 4, BF16, None) == 1
+    assert _err(lib) == "act, qweight and out must be 16-byte aligned"
+
+
 def test_repack_validation(lib):
     assert lib.convrot_repack_weight(None, 0, None, 1, 33, 64, None) == 1
     assert _err(lib) == "MPP int4 packing requires even out_features, got 33"

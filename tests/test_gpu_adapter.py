@@ -113,10 +113,10 @@ def test_fused_modulation_tracks_unfused(dev):
 
 
 def test_fused_gelu_tracks_unfused(dev):
-    """The converted tiny DiT with each single block's GELU + concatenation fused into
-    linear2's preparation stays next to the same model with torch's GELU and cat: the two
-    GELUs (torch's float32 tanh and the producer's fixed sequence) differ by at most one bf16
-    ulp, on about 0.1 % of the MLP activations."""
+    """The converted tiny DiT with every MLP-down Linear's GELU (and, in the single blocks,
+    the concatenation) fused into its preparation stays next to the same model with torch's
+    GELU and cat: the two GELUs (torch's float32 tanh and the producer's fixed sequence)
+    differ by at most one bf16 ulp, on about 0.1 % of the MLP activations."""
     from convrot_mlx_amd import replace_convrot_linears
     from examples.flux1_dev.dit import set_fused_gelu
 
@@ -133,3 +133,25 @@ def test_fused_gelu_tracks_unfused(dev):
     rel_dense = ((fused - ref).norm() / ref.norm()).item()
     print(f"fused GELU vs unfused rel_l2={rel:.5f}; vs dense {rel_dense:.4f}")
     assert rel < 0.05 and rel_dense < 0.35
+
+
+def test_fused_residual_is_exact(dev):
+    """Every gated residual of the converted tiny DiT moved into the GEMM epilogue gives the
+    model's output bit for bit (the epilogue rounds as torch's two eager ops do), alone and
+    on top of the fused modulation and GELU producers."""
+    from convrot_mlx_amd import replace_convrot_linears
+    from examples.flux1_dev.dit import set_fused_gelu, set_fused_modulation, set_fused_residual
+
+    p = _tiny()
+    model = build(p, dev, seed=7)
+    inputs = make_inputs(p, img_tokens=64, txt_tokens=24, device=dev, seed=8)
+    replace_convrot_linears(model, group_size=G)
+    unfused = _run(model, inputs)
+    set_fused_residual(model, True)
+    assert torch.equal(_run(model, inputs), unfused)
+    set_fused_residual(model, False)
+    set_fused_modulation(model, True)
+    set_fused_gelu(model, True)
+    producers = _run(model, inputs)
+    set_fused_residual(model, True)
+    assert torch.equal(_run(model, inputs), producers)
