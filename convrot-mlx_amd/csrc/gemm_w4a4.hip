@@ -1000,12 +1000,19 @@ constexpr int kSkMinIters = 4;
 // k-block at full efficiency.
 double block_cost(const Cand& c) { return (double)c.t.bm * c.t.bn / 65536.0 / c.eff; }
 
+// A workgroup alone on a CU (fewer tiles than CUs) runs a k-block in
+// kLoneBlocks x block_cost: measured on the 128x128 tile at M = 256 .. 1024
+// (K = 3072 .. 15360), a lone workgroup takes 0.62 of the time two
+// co-resident ones take for a k-block each, not 0.5.
+constexpr double kLoneBlocks = 1.1;
+
 // Modelled run time of the busiest CU, in units of one 256x256 k-block.  With
 // per_cu workgroups resident on a CU they share it, so a CU's load counts in
 // steps of 1/per_cu of a tile.
 double dp_time(const Cand& c, int64_t tiles, int64_t kb, int cus) {
-  const int64_t steps = (tiles * c.per_cu + cus - 1) / cus;  // ceil(tiles per CU * per_cu)
   const double partial = tiles < cus ? c.eff / c.eff_partial : 1.0;
+  if (c.per_cu > 1 && tiles < cus) return (double)kb * block_cost(c) * kLoneBlocks * partial;
+  const int64_t steps = (tiles * c.per_cu + cus - 1) / cus;  // ceil(tiles per CU * per_cu)
   return (double)steps / c.per_cu * (double)kb * block_cost(c) * partial;
 }
 
