@@ -586,13 +586,21 @@ def hip_w4a4_matmul(qact, qweight, xscales, wscales, bias, *, output_dtype, out_
     output_dtype) the kernel returns residual + gate * product (see
     ConvRotLinear.forward), in place into `residual` when `inplace`; the residual
     may be shaped [..., N] (M rows in all) for the gate to broadcast against.
+
+    The packed codes are first unpacked to int8 (one HBM pass over M*K/2 + M*K
+    bytes) so that the product runs in the int8 kernels: direct-to-LDS tiles
+    and the few-row kernel.  The integer dots are exact either way, so the
+    output is the same bits as convrot_w4a4_gemm(ACT_PACKED), whose
+    register-staged kernel reads the packed codes itself without a buffer.
     """
     if qact.ndim != 2:
         raise ValueError(f"MPP W4A4 activation must be 2D, got {tuple(qact.shape)}")
     k = qact.shape[1] * 2
     gr = _residual_arg(qact.shape[0], qweight, k, out_features, output_dtype, residual, gate, inplace)
-    return _w4a4(qact.contiguous(), nat.ACT_PACKED, k, qweight, xscales, wscales, bias, output_dtype, out_features,
-                 gr)
+    if k % 32:
+        raise ValueError(f"MPP W4 TensorOp requires K divisible by 32, got {k}")
+    return _w4a4(unpack_signed_int4(qact), nat.ACT_INT8, k, qweight, xscales, wscales, bias, output_dtype,
+                 out_features, gr)
 
 
 def hip_w4a4_int8_matmul(activations, qweight, xscales, wscales, bias, *, output_dtype, out_features=None,

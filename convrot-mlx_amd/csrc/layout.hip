@@ -30,6 +30,28 @@ __global__ void unpack_kernel(const uint8_t* __restrict__ packed, int8_t* __rest
   *(uint16_t*)(out + 2 * i) = (uint16_t)((uint8_t)lo | ((uint32_t)(uint8_t)hi << 8));
 }
 
+// Four packed bytes -> eight int8 (two words), low nibble first.  Each nibble
+// n becomes n | 0xf0 where its bit 3 is set: m = bit 3 of every byte, and
+// m * 0xf0 sets the high half of exactly those bytes (no carries).
+__device__ __forceinline__ uint2 unpack_word(uint32_t w) {
+  uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  lo |= ((lo & 0x08080808u) >> 3) * 0xf0u;
+  hi |= ((hi & 0x08080808u) >> 3) * 0xf0u;
+  // interleave: bytes (lo0 hi0 lo1 hi1) and (lo2 hi2 lo3 hi3)
+  return make_uint2(__builtin_amdgcn_perm(hi, lo, 0x05010400u), __builtin_amdgcn_perm(hi, lo, 0x07030602u));
+}
+
+// The same 16 packed bytes per thread: one 16-byte load, two 16-byte stores.
+// Needs total % 16 == 0 and 16-byte aligned buffers (checked by the launcher).
+__global__ void unpack16_kernel(const uint4* __restrict__ packed, uint4* __restrict__ out, int64_t vecs) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= vecs) return;
+  const uint4 p = packed[i];
+  const uint2 a = unpack_word(p.x), b = unpack_word(p.y), c = unpack_word(p.z), d = unpack_word(p.w);
+  out[2 * i] = make_uint4(a.x, a.y, b.x, b.y);
+  out[2 * i + 1] = make_uint4(c.x, c.y, d.x, d.y);
+}
+
 // Nibble (two's complement, 4 bits) of weight element (n, k) in a layout;
 // zero outside the N x K weight (CDNA4 padding).
 __device__ __forceinline__ uint32_t nibble_at(const uint8_t* __restrict__ in, int layout, int64_t n, int64_t k,
@@ -101,7 +123,13 @@ hipError_t launch_unpack_int4(const uint8_t* packed, int64_t rows, int64_t packe
                               hipStream_t stream) {
   const int64_t total = rows * packed_cols;
   if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(unpack_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream, packed, out, total);
+  if (total % 16 == 0 && (uintptr_t)packed % 16 == 0 && (uintptr_t)out % 16 == 0) {
+    const int64_t vecs = total / 16;
+    hipLaunchKernelGGL(unpack16_kernel, dim3(grid_for(vecs, 256)), dim3(256), 0, stream, (const uint4*)packed,
+                       (uint4*)out, vecs);
+  } else {
+    hipLaunchKernelGGL(unpack_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream, packed, out, total);
+  }
   return hipGetLastError();
 }
 

@@ -27,8 +27,16 @@ def _dev_u8(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
+# Output names of _run_both, in order: the C ABI's packed-activation kernel (register-staged,
+# reads the packed codes itself), the packed Python entry point (unpacks to int8, then the
+# int8 kernels) and the int8 entry point.
+_BOTH = ("packed-kernel", "packed-api", "int8")
+
+
 def _run_both(orc, dev, a_codes, w_codes, xs, ws, bias, out_dtype):
-    """Run the packed-A and int8-A entry points with a CDNA4 weight; return both outputs."""
+    """Run the packed-A kernel, the packed-A and the int8-A entry points with a CDNA4 weight."""
+    from convrot_mlx_amd import _native as nat
+
     api = _api()
     N, K = w_codes.shape
     wq = _dev_u8(orc.codes_to_cdna4(w_codes), dev)
@@ -37,10 +45,15 @@ def _run_both(orc, dev, a_codes, w_codes, xs, ws, bias, out_dtype):
     xs_d, ws_d = torch.from_numpy(xs).to(dev), torch.from_numpy(ws).to(dev)
     b_d = torch.from_numpy(bias).to(dev)
     dt = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}[out_dtype]
+    M = a_codes.shape[0]
+    out_k = torch.empty((M, N), dtype=dt, device=dev)
+    nat.check(nat.load().convrot_w4a4_gemm(nat.ptr(qact), nat.ACT_PACKED, nat.ptr(xs_d), nat.ptr(wq), nat.ptr(ws_d),
+                                           nat.ptr(b_d), M, N, K, nat.ptr(out_k), nat.dtype_code(dt),
+                                           nat.stream_of(dev)))
     out_p = api.hip_w4a4_matmul(qact, wq, xs_d, ws_d, b_d, output_dtype=dt, out_features=N)
     out_8 = api.hip_w4a4_int8_matmul(a8, wq, xs_d, ws_d, b_d, output_dtype=dt, out_features=N)
     torch.cuda.synchronize()
-    return from_dev(out_p), from_dev(out_8)
+    return from_dev(out_k), from_dev(out_p), from_dev(out_8)
 
 
 def _assert_exact(got, expected, label):
@@ -61,7 +74,7 @@ def test_edges_37x64x46(orc, dev, out_dtype):
     ws = rng.uniform(0.01, 0.2, size=(46,)).astype(np.float32)
     b = rng.normal(size=(46,)).astype(np.float32)
     expected = orc.w4a4_matmul_codes(a, w, xs, ws, b, out_dtype)
-    for got, name in zip(_run_both(orc, dev, a, w, xs, ws, b, out_dtype), ("packed", "int8")):
+    for got, name in zip(_run_both(orc, dev, a, w, xs, ws, b, out_dtype), _BOTH):
         _assert_exact(got, expected, f"{name} {out_dtype}")
 
 
@@ -72,7 +85,7 @@ def test_exact_integer_dots(orc, dev):
     w = rng.integers(-8, 8, size=(46, 320), dtype=np.int8)
     ones_m, ones_n, zeros_n = np.ones(37, np.float32), np.ones(46, np.float32), np.zeros(46, np.float32)
     dots = a.astype(np.int64) @ w.astype(np.int64).T
-    for got, name in zip(_run_both(orc, dev, a, w, ones_m, ones_n, zeros_n, "float32"), ("packed", "int8")):
+    for got, name in zip(_run_both(orc, dev, a, w, ones_m, ones_n, zeros_n, "float32"), _BOTH):
         assert np.array_equal(got, dots.astype(np.float32)), name
 
 
@@ -85,7 +98,7 @@ def test_max_magnitude_accumulators(orc, dev):
     w[::3] = 7
     ones_m, ones_n, zeros_n = np.ones(16, np.float32), np.ones(32, np.float32), np.zeros(32, np.float32)
     dots = a.astype(np.int64) @ w.astype(np.int64).T
-    for got, name in zip(_run_both(orc, dev, a, w, ones_m, ones_n, zeros_n, "float32"), ("packed", "int8")):
+    for got, name in zip(_run_both(orc, dev, a, w, ones_m, ones_n, zeros_n, "float32"), _BOTH):
         assert np.array_equal(got, dots.astype(np.float32)), name
 
 
@@ -102,7 +115,7 @@ def test_odd_shapes_bf16(orc, dev, seed, M, K, N):
     ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
     b = rng.normal(size=(N,)).astype(np.float32)
     expected = orc.w4a4_matmul_codes(a, w, xs, ws, b, "bfloat16")
-    for got, name in zip(_run_both(orc, dev, a, w, xs, ws, b, "bfloat16"), ("packed", "int8")):
+    for got, name in zip(_run_both(orc, dev, a, w, xs, ws, b, "bfloat16"), _BOTH):
         _assert_exact(got, expected, f"{name} seed {seed}")
 
 
@@ -130,7 +143,7 @@ def test_every_tile_config(orc, dev, monkeypatch, tile, no_dma, seed, M, K, N):
     ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
     b = rng.normal(size=(N,)).astype(np.float32)
     expected = orc.w4a4_matmul_codes(a, w, xs, ws, b, "bfloat16")
-    for got, name in zip(_run_both(orc, dev, a, w, xs, ws, b, "bfloat16"), ("packed", "int8")):
+    for got, name in zip(_run_both(orc, dev, a, w, xs, ws, b, "bfloat16"), _BOTH):
         _assert_exact(got, expected, f"{name} tile {tile}")
 
 

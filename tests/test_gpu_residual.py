@@ -37,6 +37,7 @@ PATHS = {
                   "CONVROT_GEMM_SK_MIN": "1"}, 2, 130, 1024, 270, "int8"),
     "register": ({"CONVROT_GEMM_SMALLM_MAX": "0", "CONVROT_GEMM_NO_DMA": "1"}, 2, 90, 256, 100, "int8"),
     "packed": ({"CONVROT_GEMM_SMALLM_MAX": "0"}, 2, 90, 256, 102, "packed"),
+    "packed_kernel": ({}, 2, 90, 256, 102, "packed_kernel"),
 }
 _ENV_KEYS = ("CONVROT_W4A4_SMALLM_CFG", "CONVROT_GEMM_SMALLM_MAX", "CONVROT_GEMM_TILE", "CONVROT_GEMM_SK",
              "CONVROT_GEMM_SK_MIN", "CONVROT_GEMM_NO_DMA")
@@ -93,6 +94,23 @@ def _call(api, orc, dev, fmt, a, w, xs, ws, b, dtype, residual, gate, inplace=Fa
     if fmt == "packed":
         qact = torch.from_numpy(orc.pack_signed_int4(a)).to(dev)
         return api.hip_w4a4_matmul(qact, wq, *args, **kw)
+    if fmt == "packed_kernel":  # the C ABI's register-staged kernel on the packed codes
+        from convrot_mlx_amd import _native as nat
+
+        qact = torch.from_numpy(orc.pack_signed_int4(a)).to(dev)
+        M = a.shape[0]
+        res = residual.reshape(M, N)
+        g = gate.expand(residual.shape) if gate is not None else None
+        assert g is None or g.stride(-2) == 0, "per-image gates only"
+        out = res if inplace else torch.empty((M, N), dtype=TORCH_DT[dtype], device=dev)
+        gp = nat.ptr(g) if g is not None else nat.ptr(None)
+        gstride = g.stride(0) if g is not None else 0
+        rpg = residual.shape[1] if residual.dim() == 3 else M
+        nat.check(nat.load().convrot_w4a4_gemm_residual(
+            nat.ptr(qact), nat.ACT_PACKED, nat.ptr(args[0]), nat.ptr(wq), nat.ptr(args[1]), nat.ptr(args[2]),
+            M, N, a.shape[1], nat.ptr(res), gp, gstride, rpg, nat.ptr(out), nat.dtype_code(TORCH_DT[dtype]),
+            nat.stream_of(dev)))
+        return out
     return api.hip_w4a4_int8_matmul(torch.from_numpy(a).to(dev), wq, *args, **kw)
 
 
