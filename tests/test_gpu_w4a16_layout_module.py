@@ -132,6 +132,21 @@ def test_unpack_matches_oracle(orc, dev):
     assert np.array_equal(from_dev(api.metal_unpack_signed_int4(_u8(packed, dev))), orc.unpack_signed_int4(packed))
 
 
+@pytest.mark.parametrize("rows,cols,offset", [(4608, 1536, 0), (3, 16, 0), (5, 7, 0), (2, 32, 1)])
+def test_unpack_kernels(orc, dev, rows, cols, offset):
+    """Both unpack kernels: 16 packed bytes per thread (size a multiple of 16, aligned) and one
+    byte per thread (ragged size, or a buffer starting off a 16-byte boundary), every byte
+    value included."""
+    api = _api()
+    rng = np.random.default_rng(rows * 7 + cols)
+    packed = rng.integers(0, 256, size=rows * cols + offset, dtype=np.uint8)
+    packed[offset:offset + 256] = np.arange(256, dtype=np.uint8)[: min(256, rows * cols)]
+    dev_buf = _u8(packed, dev)
+    view = dev_buf[offset:].view(rows, cols)
+    want = orc.unpack_signed_int4(packed[offset:].reshape(rows, cols))
+    assert np.array_equal(from_dev(api.unpack_signed_int4(view)), want)
+
+
 def test_mpp_repack_round_trip(orc, dev):
     """test_core.py:203-211: (46, 64) codes -> KN (64, 23) and back, bit-exact."""
     api = _api()
