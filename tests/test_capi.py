@@ -40,6 +40,24 @@ def test_every_declared_symbol_is_exported(lib):
     assert set(names) == set(_native.SIGNATURES), "ctypes binding and header disagree"
 
 
+def test_integration_stub_binds_every_entry_point():
+    """The reference-side ctypes stub in INTEGRATION.md sets argtypes for every function the
+    header declares, with as many arguments as the package's own binding."""
+    from convrot_mlx_amd import _native
+
+    doc = (ROOT / "INTEGRATION.md").read_text()
+    stub = doc[doc.index("# convrot_mlx/_amd.py"):]
+    stub = stub[: stub.index("```")]
+    for name in header_functions():
+        if name in ("convrot_last_error", "convrot_version"):
+            assert name in stub
+            continue
+        m = re.search(rf"_lib\.{name}\.argtypes = \[([^\]]*)\]", stub)
+        assert m, f"{name} has no argtypes in the INTEGRATION.md stub"
+        n_args = len([a for a in m.group(1).replace("\n", " ").split(",") if a.strip()])
+        assert n_args == len(_native.SIGNATURES[name][1]), f"{name}: stub binds {n_args} arguments"
+
+
 def test_constants_match_binding():
     from convrot_mlx_amd import _native as n
 
