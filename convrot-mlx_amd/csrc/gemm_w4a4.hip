@@ -986,7 +986,7 @@ struct Cand {
   bool dma_only;  // no register-staged (packed-activation) variant
 };
 constexpr Cand kCands[5] = {{{256, 256, 2, 4, 3}, 1, 1.0, 1.0, false, false},
-                            {{128, 256, 2, 4, 3}, 1, 0.85, 0.85, true, false},
+                            {{128, 256, 2, 4, 4}, 1, 0.85, 0.85, true, false},
                             {{256, 128, 4, 2, 3}, 1, 0.8, 0.8, true, false},
                             {{128, 128, 2, 2, 3}, 2, 0.8, 0.8, false, false},
                             {{192, 128, 4, 2, 3}, 1, 0.75, 0.83, false, true}};
@@ -1029,7 +1029,7 @@ double sk_time(const Cand& c, int64_t tiles, int64_t kb, int cus, int min_iters)
 }
 
 // Pick the tile and kernel with the least modelled time.  Overrides for
-// tuning sweeps and tests: CONVROT_GEMM_TILE=BMxBN[wWMxWN] forces the tile,
+// tuning sweeps and tests: CONVROT_GEMM_TILE=BMxBN[wWMxWN[sS]] forces the tile,
 // CONVROT_GEMM_SK=0|1 forces the kernel kind, CONVROT_GEMM_SK_MIN sets the
 // shortest stream-K range.
 Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_sk) {
@@ -1044,7 +1044,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_sk) {
   const Tile* forced = nullptr;
   Tile ft{};
   if (const char* env = getenv("CONVROT_GEMM_TILE")) {
-    int bm = 0, bn = 0, wm = 2, wn = 2, stages = 3;
+    int bm = 0, bn = 0, wm = 2, wn = 2, stages = 0;  // 0: the candidate's own ring depth
     if (sscanf(env, "%dx%dw%dx%ds%d", &bm, &bn, &wm, &wn, &stages) >= 2) {
       ft = {bm, bn, wm, wn, stages};
       forced = &ft;
@@ -1054,7 +1054,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_sk) {
   double best_time = 1e300;
   for (const Cand& c : kCands) {
     const bool match = forced && c.t.bm == forced->bm && c.t.bn == forced->bn && c.t.wm == forced->wm &&
-                       c.t.wn == forced->wn && c.t.stages == forced->stages;
+                       c.t.wn == forced->wn && (forced->stages == 0 || c.t.stages == forced->stages);
     if ((forced && !match) || (c.dma_only && !allow_sk)) continue;
     const int64_t tiles = ((M + c.t.bm - 1) / c.t.bm) * ((N + c.t.bn - 1) / c.t.bn);
     const double td = dp_time(c, tiles, kb, cus);
@@ -1173,7 +1173,7 @@ hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const f
     return launch_dma<BM_, BN_, WM_, WN_, S_, ODT>(plan, act, xs, wq, ws, bias, M, N, K, out, gr, stream);
     CONVROT_DMA(256, 256, 2, 4, 3)
     CONVROT_DMA(256, 128, 4, 2, 3)
-    CONVROT_DMA(128, 256, 2, 4, 3)
+    CONVROT_DMA(128, 256, 2, 4, 4)
     CONVROT_DMA(128, 128, 2, 2, 3)
     CONVROT_DMA(192, 128, 4, 2, 3)
 #undef CONVROT_DMA
