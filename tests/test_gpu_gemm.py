@@ -222,12 +222,15 @@ def test_kn_layout_entry_matches(orc, dev):
     _assert_exact(from_dev(out), orc.w4a4_matmul_codes(a, w, xs, ws, b, "float32"), "kn entry")
 
 
-@pytest.mark.parametrize("K,N", [(3072, 9216), (3072, 3072), (3072, 12288), (12288, 3072), (3072, 21504), (15360, 3072)])
-def test_flux_shapes_complete_path(orc, dev, K, N):
-    """benchmark configs 2/3 at full size: prep (HIP) -> GEMM (HIP).  Codes and scales must equal
-    the oracle's everywhere; outputs are compared exactly on a seeded sample of 48 rows x all columns."""
+@pytest.mark.parametrize("M,G,K,N", [(1536, 64, 3072, 9216), (1536, 64, 3072, 3072), (1536, 64, 3072, 12288),
+                                     (1536, 64, 12288, 3072), (1536, 64, 3072, 21504), (1536, 64, 15360, 3072),
+                                     (4608, 256, 3072, 12288), (4608, 256, 15360, 3072)])
+def test_flux_shapes_complete_path(orc, dev, M, G, K, N):
+    """benchmark configs 2/3 at full size (M = 1536, G = 64; and M = 4608, G = 256 on the
+    config-3 MLP-up and single-block down shapes): prep (HIP) -> GEMM (HIP).  Codes and scales
+    must equal the oracle's everywhere; outputs are compared exactly on a seeded sample of 48
+    rows x all columns."""
     api = _api()
-    M, G = 1536, 64
     x = outlier_input(K + N, (M, K), "bfloat16", orc)
     w = outlier_input(K * 3 + N, (N, K), "bfloat16", orc, std=0.02, frac=0.01, factor=10.0)
     bias = np.random.default_rng(N).normal(0.0, 0.02, size=N).astype(np.float32)
