@@ -617,8 +617,10 @@ def hip_w4a4_int8_matmul(activations, qweight, xscales, wscales, bias, *, output
                  out_features, gr)
 
 
-def hip_w4a16_matmul(activations, qweight, wscales, bias, *, output_dtype, out_features=None):
-    """Rotated bf16/f16 activations x W4 weight -> output_dtype (core.py:1123-1152)."""
+def hip_w4a16_matmul(activations, qweight, wscales, bias, *, output_dtype, out_features=None, residual=None,
+                     gate=None, inplace=False):
+    """Rotated bf16/f16 activations x W4 weight -> output_dtype (core.py:1123-1152);
+    residual, gate and inplace as in hip_w4a4_matmul (applied in the GEMM's epilogue)."""
     if activations.ndim != 2:
         raise ValueError(f"MPP W4A16 activation must be 2D, got {tuple(activations.shape)}")
     if activations.dtype not in (torch.float16, torch.bfloat16):
@@ -629,14 +631,25 @@ def hip_w4a16_matmul(activations, qweight, wscales, bias, *, output_dtype, out_f
     if k % 32:
         raise ValueError(f"MPP W4 TensorOp requires K divisible by 32, got {k}")
     _validate_mpp_epilogue(m, n, None, wscales, bias)
+    gr = _residual_arg(m, qweight, k, n, output_dtype, residual, gate, inplace)
     nat.require_device(activations, qweight, wscales, bias)
     act = activations.contiguous()
     w = _as_cdna4(qweight, n, k)
-    out = torch.empty((m, n), dtype=output_dtype, device=act.device)
     ws, b = _f32(wscales), _f32(bias)
+    if gr is None:
+        out = torch.empty((m, n), dtype=output_dtype, device=act.device)
+        nat.check(
+            nat.load().convrot_w4a16_gemm(
+                nat.ptr(act), nat.dtype_code(act.dtype), nat.ptr(w), nat.ptr(ws), nat.ptr(b), m, n, k,
+                nat.ptr(out), nat.dtype_code(output_dtype), nat.stream_of(act.device),
+            )
+        )
+        return out
+    out = gr.residual.view(m, n) if gr.inplace else torch.empty((m, n), dtype=output_dtype, device=act.device)
     nat.check(
-        nat.load().convrot_w4a16_gemm(
+        nat.load().convrot_w4a16_gemm_residual(
             nat.ptr(act), nat.dtype_code(act.dtype), nat.ptr(w), nat.ptr(ws), nat.ptr(b), m, n, k,
+            nat.ptr(gr.residual), nat.ptr(gr.gate), gr.stride, gr.rows_per_gate,
             nat.ptr(out), nat.dtype_code(output_dtype), nat.stream_of(act.device),
         )
     )
@@ -763,8 +776,7 @@ class ConvRotLinear(nn.Module):
 
     def _project(self, prep, lead: tuple, dtype: torch.dtype, residual, gate, inplace: bool) -> torch.Tensor:
         """Run the prepared activation `prep(mode)` through this layer's GEMM, then the
-        optional gated residual (residual + gate * linear).  W4A4 applies the residual in
-        the GEMM's epilogue; W4A16 applies it with torch's eager ops (the same numerics)."""
+        optional gated residual (residual + gate * linear) in the GEMM's epilogue."""
         if residual is None and (gate is not None or inplace):
             raise ValueError("gate and inplace need a residual")
         out_shape = (*lead, self.out_features)
@@ -774,16 +786,13 @@ class ConvRotLinear(nn.Module):
             qact, xscales = prep(nat.PREP_INT8)
             out = _w4a4(qact, nat.ACT_INT8, self.in_features, w, xscales, self.scales, self.bias, dtype,
                         self.out_features, gr)
-            return residual if inplace else out.reshape(out_shape)
-        if residual is not None:
-            _gated_residual(residual, gate, out_shape, dtype, inplace)  # same argument checks
-        rotated = prep(nat.PREP_ROTATE)[0]
-        out = hip_w4a16_matmul(rotated, w, self.scales, self.bias, output_dtype=dtype,
-                               out_features=self.out_features).reshape(out_shape)
-        if residual is None:
-            return out
-        update = out if gate is None else gate * out
-        return residual.add_(update) if inplace else residual + update
+        else:
+            if residual is not None:
+                _gated_residual(residual, gate, out_shape, dtype, inplace)  # checks before any launch
+            rotated = prep(nat.PREP_ROTATE)[0]
+            out = hip_w4a16_matmul(rotated, w, self.scales, self.bias, output_dtype=dtype,
+                                   out_features=self.out_features, residual=residual, gate=gate, inplace=inplace)
+        return residual if inplace else out.reshape(out_shape)
 
     def forward(self, x: torch.Tensor, *, residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
                 inplace: bool = False) -> torch.Tensor:

@@ -218,14 +218,12 @@ int convrot_w4a4_gemm(const void* act, int act_format, const float* xscales, con
                        "convrot_w4a4_gemm");
 }
 
-int convrot_w4a4_gemm_residual(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
-                               const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
-                               const void* residual, const void* gate, int64_t gate_stride,
-                               int64_t rows_per_gate, void* out, int out_dtype, void* stream) {
-  if (int rc = check_w4a4(act, act_format, xscales, qweight, wscales, M, N, K, out, out_dtype)) return rc;
-  if (gate && rows_per_gate <= 0)
-    return fail(CONVROT_ERR_INVALID, "rows_per_gate must be positive, got %lld", (long long)rows_per_gate);
-  if (M == 0 || N == 0) return ok();
+namespace {
+
+// Checks of the gated-residual arguments shared by both GEMMs (after the GEMM's
+// own checks, with M, N > 0); fills `gr` on success.
+int check_residual(const void* residual, const void* gate, int64_t gate_stride, int64_t rows_per_gate, int64_t M,
+                   int64_t N, convrot::GatedResidual* gr) {
   if (!residual) return fail(CONVROT_ERR_INVALID, "null pointer argument");
   if (!aligned(residual, 16) || (gate && !aligned(gate, 16)))
     return fail(CONVROT_ERR_INVALID, "residual and gate must be 16-byte aligned");
@@ -234,14 +232,33 @@ int convrot_w4a4_gemm_residual(const void* act, int act_format, const float* xsc
   if (gate && (M + rpg - 1) / rpg > 1 && gate_stride < N)
     return fail(CONVROT_ERR_INVALID, "gate rows %lld elements apart overlap (N=%lld)", (long long)gate_stride,
                 (long long)N);
-  const convrot::GatedResidual gr{residual, gate, gate ? gate_stride : 0, (int)rpg};
+  *gr = convrot::GatedResidual{residual, gate, gate ? gate_stride : 0, (int)rpg};
+  return ok();
+}
+
+}  // namespace
+
+int convrot_w4a4_gemm_residual(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
+                               const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
+                               const void* residual, const void* gate, int64_t gate_stride,
+                               int64_t rows_per_gate, void* out, int out_dtype, void* stream) {
+  if (int rc = check_w4a4(act, act_format, xscales, qweight, wscales, M, N, K, out, out_dtype)) return rc;
+  if (gate && rows_per_gate <= 0)
+    return fail(CONVROT_ERR_INVALID, "rows_per_gate must be positive, got %lld", (long long)rows_per_gate);
+  if (M == 0 || N == 0) return ok();
+  convrot::GatedResidual gr{};
+  if (int rc = check_residual(residual, gate, gate_stride, rows_per_gate, M, N, &gr)) return rc;
   return launch_status(convrot::launch_w4a4_gemm(act, act_format, xscales, qweight, wscales, bias, M, N, K, out,
                                                  out_dtype, (hipStream_t)stream, gr),
                        "convrot_w4a4_gemm_residual");
 }
 
-int convrot_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales,
-                       const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype, void* stream) {
+namespace {
+
+// Argument checks of the W4A16 GEMM entry points; CONVROT_OK when the launch
+// may proceed (M == 0 or N == 0 included).
+int check_w4a16(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales, int64_t M, int64_t N,
+                int64_t K, void* out, int out_dtype) {
   if (act_dtype != CONVROT_DTYPE_F16 && act_dtype != CONVROT_DTYPE_BF16)
     return fail(CONVROT_ERR_INVALID, "MPP W4A16 requires float16 or bfloat16 activation, got %s", dtype_name(act_dtype));
   if (!valid_dtype(out_dtype)) return fail(CONVROT_ERR_INVALID, "unsupported output dtype code %d", out_dtype);
@@ -257,9 +274,33 @@ int convrot_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight, c
   if (!act || !qweight || !wscales || !out) return fail(CONVROT_ERR_INVALID, "null pointer argument");
   if (!aligned(act, 16) || !aligned(qweight, 16) || !aligned(out, 16))
     return fail(CONVROT_ERR_INVALID, "act, qweight and out must be 16-byte aligned");
+  return ok();
+}
+
+}  // namespace
+
+int convrot_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales,
+                       const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype, void* stream) {
+  if (int rc = check_w4a16(act, act_dtype, qweight, wscales, M, N, K, out, out_dtype)) return rc;
+  if (M == 0 || N == 0) return ok();
   return launch_status(convrot::launch_w4a16_gemm(act, act_dtype, qweight, wscales, bias, M, N, K, out, out_dtype,
                                                   (hipStream_t)stream),
                        "convrot_w4a16_gemm");
+}
+
+int convrot_w4a16_gemm_residual(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales,
+                                const float* bias, int64_t M, int64_t N, int64_t K, const void* residual,
+                                const void* gate, int64_t gate_stride, int64_t rows_per_gate, void* out,
+                                int out_dtype, void* stream) {
+  if (int rc = check_w4a16(act, act_dtype, qweight, wscales, M, N, K, out, out_dtype)) return rc;
+  if (gate && rows_per_gate <= 0)
+    return fail(CONVROT_ERR_INVALID, "rows_per_gate must be positive, got %lld", (long long)rows_per_gate);
+  if (M == 0 || N == 0) return ok();
+  convrot::GatedResidual gr{};
+  if (int rc = check_residual(residual, gate, gate_stride, rows_per_gate, M, N, &gr)) return rc;
+  return launch_status(convrot::launch_w4a16_gemm(act, act_dtype, qweight, wscales, bias, M, N, K, out, out_dtype,
+                                                  (hipStream_t)stream, gr),
+                       "convrot_w4a16_gemm_residual");
 }
 
 int convrot_pack_int4(const int8_t* values, int64_t rows, int64_t packed_cols, uint8_t* out, void* stream) {

@@ -43,7 +43,7 @@ int device_cus();
 
 hipError_t launch_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales,
                              const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
-                             hipStream_t stream);
+                             hipStream_t stream, const GatedResidual& gr = GatedResidual{});
 
 hipError_t launch_pack_int4(const int8_t* values, int64_t rows, int64_t packed_cols, uint8_t* out,
                             hipStream_t stream);

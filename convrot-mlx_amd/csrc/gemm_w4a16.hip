@@ -64,7 +64,7 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
                                                                 const float* __restrict__ wscales,
                                                                 const float* __restrict__ bias,
                                                                 void* __restrict__ out, int M, int N, int K,
-                                                                int nblocks, int kblocks) {
+                                                                int nblocks, int kblocks, GatedResidual gr) {
   __shared__ __attribute__((aligned(16))) f32x4 red[SPLIT > 1 ? SPLIT : 1][NB * FM][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nb0 = blockIdx.x * NB;
@@ -160,6 +160,7 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
         v = v + (bias ? bias[nn] : 0.0f);
         o[j] = v;
       }
+      if (gr.residual) gate_residual4<ODT>(gr, m, n, N, vec_ok, o);
       const int64_t idx = (int64_t)m * N + n;
       if (vec_ok) {
         store_out4<ODT>(out, idx, o[0], o[1], o[2], o[3]);
@@ -206,7 +207,7 @@ template <int ADT, int ODT, int BM, int BN>
 __global__ __launch_bounds__(kTileWaves * 64) __attribute__((amdgpu_waves_per_eu(BM * BN <= 128 * 128 ? 4 : 2)))
 void w4a16_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ wq,
                         const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out,
-                        int M, int N, int K, int nblocks, int kblocks, int tiles_m, int tiles_n) {
+                        int M, int N, int K, int nblocks, int kblocks, int tiles_m, int tiles_n, GatedResidual gr) {
   using S = TiledShape<BM, BN>;
   constexpr int FM = S::FM, FN = S::FN;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * S::StageBytes];
@@ -320,6 +321,7 @@ void w4a16_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restr
         float o[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = acc[fn][fm][j] * wsv[j] + bv[j];
+        if (gr.residual) gate_residual4<ODT>(gr, m, n, N, vec_ok, o);
         const int64_t idx = (int64_t)m * N + n;
         if (vec_ok) {
           store_out4<ODT>(out, idx, o[0], o[1], o[2], o[3]);
@@ -359,16 +361,13 @@ void w4a16_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restr
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     constexpr int CPR = BN / 32;         // 16-byte chunks per staged row
     constexpr int RPI = 64 / CPR;        // rows per instruction
+    constexpr int NIT = (BM / 2) / RPI;  // write-back iterations
     const int cr = lane / CPR, cc = lane % CPR;
-    const bool vec_ok = (N & 7) == 0;
-#pragma unroll
-    for (int r0 = 0; r0 < BM / 2; r0 += RPI) {
-      const int rl = r0 + cr;
-      const int m = mw + rl, n = nw + cc * 8;
-      if (m >= M || n >= N) continue;
-      const uint4 v = *(const uint4*)(region + rl * S::RS + cc * 16);
-      uint16_t* dst = (uint16_t*)out + (int64_t)m * N + n;
-      if (vec_ok && n + 8 <= N) {
+    const int n = nw + cc * 8;
+    const bool vec = (N & 7) == 0 && n + 8 <= N;
+    auto store_row = [&](int it, uint4 v) {
+      uint16_t* dst = (uint16_t*)out + (int64_t)(mw + it * RPI + cr) * N + n;
+      if (vec) {
         *(uint4*)dst = v;
       } else {
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -376,18 +375,46 @@ void w4a16_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restr
         for (int j = 0; j < 8; ++j)
           if (n + j < N) dst[j] = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
       }
+    };
+    if (!gr.residual) {
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int rl = it * RPI + cr;
+        if (mw + rl >= M || n >= N) continue;
+        store_row(it, *(const uint4*)(region + rl * S::RS + cc * 16));
+      }
+    } else {
+      // Gated residual: the residual / gate loads of BATCH rows go out before
+      // their stores (a load cannot move above a store that may alias it).
+      constexpr int BATCH = NIT < 8 ? NIT : 8;
+      static_assert(NIT % BATCH == 0, "write-back batches");
+#pragma unroll
+      for (int b0 = 0; b0 < NIT; b0 += BATCH) {
+        Gated8 ops[BATCH];
+#pragma unroll
+        for (int i = 0; i < BATCH; ++i) {
+          const int m = mw + (b0 + i) * RPI + cr;
+          if (m < M && n < N) gate_load8<ODT>(gr, m, n, N, vec, ops[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < BATCH; ++i) {
+          const int rl = (b0 + i) * RPI + cr;
+          if (mw + rl >= M || n >= N) continue;
+          store_row(b0 + i, gate_apply8<ODT>(ops[i], *(const uint4*)(region + rl * S::RS + cc * 16)));
+        }
+      }
     }
   }
 }
 
 template <int ADT, int ODT, int BM, int BN>
 hipError_t launch_tiled_t(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
-                          int64_t N, int64_t K, void* out, hipStream_t stream) {
+                          int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
   const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
   hipLaunchKernelGGL((w4a16_tiled_kernel<ADT, ODT, BM, BN>), dim3((unsigned)(tm * tn)), dim3(kTileWaves * 64), 0,
                      stream, (const uint16_t*)act, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, tm,
-                     tn);
+                     tn, gr);
   return hipGetLastError();
 }
 
@@ -438,23 +465,23 @@ TiledPlan tiled_plan(int64_t M, int64_t N, int64_t K) {
 
 template <int ADT, int ODT>
 hipError_t launch_tiled(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
-                        int64_t N, int64_t K, void* out, hipStream_t stream) {
+                        int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
   const int pick = tiled_plan(M, N, K).pick;
   switch (pick) {
-    case 0: return launch_tiled_t<ADT, ODT, 256, 256>(act, wq, ws, bias, M, N, K, out, stream);
-    case 1: return launch_tiled_t<ADT, ODT, 256, 128>(act, wq, ws, bias, M, N, K, out, stream);
-    case 2: return launch_tiled_t<ADT, ODT, 128, 256>(act, wq, ws, bias, M, N, K, out, stream);
-    default: return launch_tiled_t<ADT, ODT, 128, 128>(act, wq, ws, bias, M, N, K, out, stream);
+    case 0: return launch_tiled_t<ADT, ODT, 256, 256>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 1: return launch_tiled_t<ADT, ODT, 256, 128>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 2: return launch_tiled_t<ADT, ODT, 128, 256>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    default: return launch_tiled_t<ADT, ODT, 128, 128>(act, wq, ws, bias, M, N, K, out, gr, stream);
   }
 }
 
 template <int ADT, int ODT, int FM, int NB, int SPLIT, int KPW>
 hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M, int64_t N,
-                    int64_t K, void* out, hipStream_t stream) {
+                    int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
   dim3 grid((unsigned)((nblocks + NB - 1) / NB), (unsigned)((M + 16 * FM - 1) / (16 * FM)));
   hipLaunchKernelGGL((w4a16_gemm_kernel<ADT, ODT, FM, NB, SPLIT, KPW>), grid, dim3(64 * SPLIT), 0, stream,
-                     (const uint16_t*)act, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks);
+                     (const uint16_t*)act, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, gr);
   return hipGetLastError();
 }
 
@@ -477,7 +504,7 @@ hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const f
 constexpr int64_t kTiledMinM = 64;
 template <int ADT, int ODT>
 hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
-                        int64_t N, int64_t K, void* out, hipStream_t stream) {
+                        int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
   const int64_t nblocks = (N + 15) / 16;
   char cfg = (M <= 16 && nblocks <= 256) ? 'B' : 'A';
   // From kTiledMinM rows on, the tiled kernel takes over where its modelled
@@ -490,21 +517,21 @@ hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, con
   if (const char* env = getenv("CONVROT_W4A16_CFG"))
     if (env[0] == 'A' || env[0] == 'B' || env[0] == 'C' || env[0] == 'F' || env[0] == 'T') cfg = env[0];
   switch (cfg) {
-    case 'T': return launch_tiled<ADT, ODT>(act, wq, ws, bias, M, N, K, out, stream);
-    case 'C': return launch_t<ADT, ODT, 2, 2, 8, 2>(act, wq, ws, bias, M, N, K, out, stream);
-    case 'A': return launch_t<ADT, ODT, 1, 2, 8, 3>(act, wq, ws, bias, M, N, K, out, stream);
-    case 'B': return launch_t<ADT, ODT, 1, 1, 16, 4>(act, wq, ws, bias, M, N, K, out, stream);
-    default: return launch_t<ADT, ODT, 4, 2, 4, 2>(act, wq, ws, bias, M, N, K, out, stream);
+    case 'T': return launch_tiled<ADT, ODT>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'C': return launch_t<ADT, ODT, 2, 2, 8, 2>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'A': return launch_t<ADT, ODT, 1, 2, 8, 3>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'B': return launch_t<ADT, ODT, 1, 1, 16, 4>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    default: return launch_t<ADT, ODT, 4, 2, 4, 2>(act, wq, ws, bias, M, N, K, out, gr, stream);
   }
 }
 
 template <int ADT>
 hipError_t launch_odt(int odt, const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
-                      int64_t N, int64_t K, void* out, hipStream_t stream) {
+                      int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
   switch (odt) {
-    case kF32: return launch_shape<ADT, kF32>(act, wq, ws, bias, M, N, K, out, stream);
-    case kF16: return launch_shape<ADT, kF16>(act, wq, ws, bias, M, N, K, out, stream);
-    default: return launch_shape<ADT, kBF16>(act, wq, ws, bias, M, N, K, out, stream);
+    case kF32: return launch_shape<ADT, kF32>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case kF16: return launch_shape<ADT, kF16>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    default: return launch_shape<ADT, kBF16>(act, wq, ws, bias, M, N, K, out, gr, stream);
   }
 }
 
@@ -512,10 +539,10 @@ hipError_t launch_odt(int odt, const void* act, const uint8_t* wq, const float* 
 
 hipError_t launch_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales,
                              const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
-                             hipStream_t stream) {
+                             hipStream_t stream, const GatedResidual& gr) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (act_dtype == kF16) return launch_odt<kF16>(out_dtype, act, qweight, wscales, bias, M, N, K, out, stream);
-  return launch_odt<kBF16>(out_dtype, act, qweight, wscales, bias, M, N, K, out, stream);
+  if (act_dtype == kF16) return launch_odt<kF16>(out_dtype, act, qweight, wscales, bias, M, N, K, out, gr, stream);
+  return launch_odt<kBF16>(out_dtype, act, qweight, wscales, bias, M, N, K, out, gr, stream);
 }
 
 }  // namespace convrot

@@ -162,6 +162,18 @@ int convrot_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight,
                        const float* wscales, const float* bias, int64_t M, int64_t N,
                        int64_t K, void* out, int out_dtype, void* stream);
 
+/*
+ * convrot_w4a16_gemm followed, in the same kernel, by the gated residual of
+ * convrot_w4a4_gemm_residual (same arguments, rounding and aliasing rules):
+ *   out[m, n] = out_dtype(residual[m, n] + out_dtype(gate[m / rows_per_gate, n] * lin)).
+ * No counterpart in the reference (see convrot_w4a4_gemm_residual).
+ */
+int convrot_w4a16_gemm_residual(const void* act, int act_dtype, const uint8_t* qweight,
+                                const float* wscales, const float* bias, int64_t M, int64_t N,
+                                int64_t K, const void* residual, const void* gate,
+                                int64_t gate_stride, int64_t rows_per_gate, void* out,
+                                int out_dtype, void* stream);
+
 /* pack_signed_int4 (core.py:97-105): int8 [rows, 2*packed_cols] -> uint8 [rows, packed_cols]. */
 int convrot_pack_int4(const int8_t* values, int64_t rows, int64_t packed_cols, uint8_t* out,
                       void* stream);

@@ -164,6 +164,16 @@ def test_gemm_residual_validation(lib):
     assert _err(lib) == "gate rows 16 elements apart overlap (N=32)"
     assert g(p, 1, p, p, p, None, 4, 32, 64, p, p, 16, 2, p + 4, BF16, None) == 1
     assert _err(lib) == "act, qweight and out must be 16-byte aligned"
+    # the W4A16 variant: its own GEMM checks, then the same residual checks
+    h = lib.convrot_w4a16_gemm_residual
+    assert h(p, 0, p, p, None, 4, 32, 64, p, None, 0, 1, p, BF16, None) == 1
+    assert _err(lib) == "MPP W4A16 requires float16 or bfloat16 activation, got float32"
+    assert h(p, BF16, p, p, None, 4, 32, 64, p, p, 32, 0, p, BF16, None) == 1
+    assert _err(lib) == "rows_per_gate must be positive, got 0"
+    assert h(p, BF16, p, p, None, 4, 32, 64, None, None, 0, 1, p, BF16, None) == 1
+    assert _err(lib) == "null pointer argument"
+    assert h(p, BF16, p, p, None, 4, 32, 64, p, p, 16, 2, p, BF16, None) == 1
+    assert _err(lib) == "gate rows 16 elements apart overlap (N=32)"
 
 
 def test_repack_validation(lib):

@@ -226,3 +226,36 @@ def test_layer_forwards(orc, dev, backend):
         r2 = res.clone()
         assert call(residual=r2, gate=gate, inplace=True) is r2
         assert torch.equal(r2, want), name
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("cfg,B,L,K,N", [("A", 1, 5, 256, 200), ("B", 2, 4, 384, 70), ("C", 2, 20, 256, 136),
+                                         ("F", 1, 40, 512, 96), ("T", 2, 100, 384, 260)])
+def test_w4a16_kernels(orc, dev, monkeypatch, cfg, B, L, K, N, dtype):
+    """The W4A16 GEMM's gated-residual epilogue on each of its kernels (splits A, B, C, F and
+    the tiled kernel, forced), per-image gates, ragged N: residual + gate * linear equals
+    torch's composition on the same kernel's plain output, bit for bit, out of place and in
+    place (the product itself is W4A16 arithmetic, checked against the oracle elsewhere)."""
+    api = _api()
+    monkeypatch.setenv("CONVROT_W4A16_CFG", cfg)
+    M = B * L
+    rng = np.random.default_rng(303)
+    act_dt = "float16" if dtype == "float16" else "bfloat16"
+    act = to_dev(orc.from_f32(rng.normal(size=(M, K)).astype(np.float32), act_dt), act_dt, dev)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    wq = torch.from_numpy(orc.codes_to_cdna4(w)).to(dev)
+    ws = torch.from_numpy(rng.uniform(0.001, 0.01, size=N).astype(np.float32)).to(dev)
+    b = torch.from_numpy(rng.normal(size=N).astype(np.float32)).to(dev)
+    res = to_dev(orc.from_f32((rng.normal(size=(M, N)) * 4).astype(np.float32), dtype), dtype, dev).reshape(B, L, N)
+    gate = to_dev(orc.from_f32(rng.normal(size=(B, N)).astype(np.float32), dtype), dtype, dev).reshape(B, 1, N)
+    kw = dict(output_dtype=TORCH_DT[dtype], out_features=N)
+    plain = api.hip_w4a16_matmul(act, wq, ws, b, **kw).reshape(B, L, N)
+    fused = api.hip_w4a16_matmul(act, wq, ws, b, residual=res, gate=gate, **kw)
+    torch.cuda.synchronize()
+    want = res + gate * plain
+    assert torch.equal(fused.reshape(B, L, N), want)
+    assert torch.equal(api.hip_w4a16_matmul(act, wq, ws, b, residual=res, **kw).reshape(B, L, N), res + plain)
+    r2 = res.clone()
+    api.hip_w4a16_matmul(act, wq, ws, b, residual=r2, gate=gate, inplace=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(r2, want)
