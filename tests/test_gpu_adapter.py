@@ -135,17 +135,18 @@ def test_fused_gelu_tracks_unfused(dev):
     assert rel < 0.05 and rel_dense < 0.35
 
 
-def test_fused_residual_is_exact(dev):
+@pytest.mark.parametrize("backend", ["hip-w4a4", "hip-w4a16"])
+def test_fused_residual_is_exact(dev, backend):
     """Every gated residual of the converted tiny DiT moved into the GEMM epilogue gives the
     model's output bit for bit (the epilogue rounds as torch's two eager ops do), alone and
-    on top of the fused modulation and GELU producers."""
+    on top of the fused modulation and GELU producers, on both backends."""
     from convrot_mlx_amd import replace_convrot_linears
     from examples.flux1_dev.dit import set_fused_gelu, set_fused_modulation, set_fused_residual
 
     p = _tiny()
     model = build(p, dev, seed=7)
     inputs = make_inputs(p, img_tokens=64, txt_tokens=24, device=dev, seed=8)
-    replace_convrot_linears(model, group_size=G)
+    replace_convrot_linears(model, backend=backend, group_size=G)
     unfused = _run(model, inputs)
     set_fused_residual(model, True)
     assert torch.equal(_run(model, inputs), unfused)
