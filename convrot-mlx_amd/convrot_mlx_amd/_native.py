@@ -32,6 +32,10 @@ SIGNATURES = {
     "convrot_w4a4_gemm": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_w4a4_gemm_residual": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64,
                                           _vp, _i32, _vp]),
+    "convrot_w4a4_workspace_bytes": (_i64, []),
+    "convrot_w4a4_gemm_ws": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp,
+                                    _i64, _vp, _i32, _vp]),
+    "convrot_w4a4_status": (_i32, [_vp, _vp]),
     "convrot_w4a16_gemm": (_i32, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_w4a16_gemm_residual": (_i32, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp,
                                            _i32, _vp]),
@@ -40,6 +44,7 @@ SIGNATURES = {
     "convrot_repack_weight": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _vp]),
     "convrot_cdna4_bytes": (_i64, [_i64, _i64]),
     "convrot_last_error": (ctypes.c_char_p, []),
+    "convrot_set_tuning": (_i32, [ctypes.c_char_p, ctypes.c_char_p]),
     "convrot_version": (ctypes.c_char_p, []),
 }
 
@@ -116,6 +121,14 @@ def check(status: int) -> None:
     if status in (ERR_INVALID, ERR_UNSUPPORTED):
         raise ValueError(msg)
     raise ConvRotNativeError(msg)
+
+
+def set_tuning(name: str, value: str | None) -> None:
+    """Force one of the library's kernel / plan choices (tuning sweeps and tests); None or ""
+    restores the automatic choice.  Names: gemm_tile ("BMxBN[wWMxWN[sS]]"), gemm_sk (0/1),
+    gemm_sk_min, gemm_no_dma, gemm_smallm_max, w4a4_smallm_cfg (A/B/C/F), w4a16_cfg
+    (A/B/C/F/T), w4a16_tile ("BMxBN"), prep_ni (1/3/4), sk_spin_limit."""
+    check(load().convrot_set_tuning(name.encode(), None if value is None else str(value).encode()))
 
 
 def cdna4_bytes(n: int, k: int) -> int:

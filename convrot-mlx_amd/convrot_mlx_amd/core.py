@@ -532,6 +532,38 @@ def _gated_residual(residual: torch.Tensor, gate: torch.Tensor | None, out_shape
     return GatedResidual(res, g, stride, rpg, inplace)
 
 
+# Stream-K workspaces of the W4A4 GEMM, one per (device index, stream handle):
+# allocated by torch (zero-filled, stream-ordered) on the stream's first eager
+# W4A4 launch and kept, so the library itself allocates nothing on this path.
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device) -> torch.Tensor | None:
+    """The stream-K workspace of `device`'s current stream, or None under graph capture
+    before one exists (the GEMM then runs a data-parallel plan, same results bit for bit)."""
+    stream = torch.cuda.current_stream(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        ws = torch.zeros(int(nat.load().convrot_w4a4_workspace_bytes()), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def w4a4_status(device=None) -> None:
+    """Raise ConvRotNativeError if a stream-K W4A4 GEMM on the current stream of `device`
+    gave up waiting for a partial tile since the last check (its output tile holds NaN).
+    Synchronizes the stream; not for use under graph capture."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    stream = torch.cuda.current_stream(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is not None:
+        nat.check(nat.load().convrot_w4a4_status(nat.ptr(ws), nat.stream_of(device)))
+
+
 def _w4a4(act: torch.Tensor, act_format: int, k: int, qweight, xscales, wscales, bias, output_dtype, n=None,
           gr: GatedResidual | None = None):
     m = act.shape[0]
@@ -543,22 +575,19 @@ def _w4a4(act: torch.Tensor, act_format: int, k: int, qweight, xscales, wscales,
     nat.require_device(act, qweight, xscales, wscales, bias)
     w = _as_cdna4(qweight, n, k)
     xs, ws, b = _f32(xscales), _f32(wscales), _f32(bias)
-    if gr is None:
-        out = torch.empty((m, n), dtype=output_dtype, device=act.device)
-        nat.check(
-            nat.load().convrot_w4a4_gemm(
-                nat.ptr(act), act_format, nat.ptr(xs), nat.ptr(w), nat.ptr(ws), nat.ptr(b), m, n, k,
-                nat.ptr(out), nat.dtype_code(output_dtype), nat.stream_of(act.device),
-            )
-        )
-        return out
-    if gr.residual.numel() != m * n:
+    if gr is not None and gr.residual.numel() != m * n:
         raise ValueError(f"residual has {gr.residual.numel()} elements, the output {m * n}")
-    out = gr.residual.view(m, n) if gr.inplace else torch.empty((m, n), dtype=output_dtype, device=act.device)
+    if gr is not None and gr.inplace:
+        out = gr.residual.view(m, n)
+    else:
+        out = torch.empty((m, n), dtype=output_dtype, device=act.device)
+    work = _workspace(act.device)
     nat.check(
-        nat.load().convrot_w4a4_gemm_residual(
+        nat.load().convrot_w4a4_gemm_ws(
             nat.ptr(act), act_format, nat.ptr(xs), nat.ptr(w), nat.ptr(ws), nat.ptr(b), m, n, k,
-            nat.ptr(gr.residual), nat.ptr(gr.gate), gr.stride, gr.rows_per_gate,
+            nat.ptr(gr.residual if gr is not None else None), nat.ptr(gr.gate if gr is not None else None),
+            gr.stride if gr is not None else 0, gr.rows_per_gate if gr is not None else 1,
+            nat.ptr(work), work.numel() if work is not None else 0,
             nat.ptr(out), nat.dtype_code(output_dtype), nat.stream_of(act.device),
         )
     )

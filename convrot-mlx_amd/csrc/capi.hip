@@ -6,8 +6,22 @@
 // (/root/reference/src/convrot_mlx/core.py:50-61,75-77,431-442,1030-1058).
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <atomic>
 
 #include "convrot_launch.h"
+
+namespace convrot {
+namespace {
+// Tuning overrides, stored as value + 1 so that the zero-initialized table
+// means "nothing set".
+std::atomic<int> g_tuning[kTuneCount] = {};
+}  // namespace
+
+int tuning(TuneKey key) { return g_tuning[key].load(std::memory_order_relaxed) - 1; }
+}  // namespace convrot
 
 namespace {
 
@@ -66,6 +80,60 @@ int64_t packed_weight_bytes(int64_t N, int64_t K) { return ((K + 127) / 128) * (
 extern "C" {
 
 const char* convrot_last_error(void) { return g_err; }
+
+int convrot_set_tuning(const char* name, const char* value) {
+  using namespace convrot;
+  if (!name) return fail(CONVROT_ERR_INVALID, "null tuning name");
+  static const struct {
+    const char* name;
+    TuneKey key;
+  } kNames[] = {{"gemm_tile", kTuneGemmTile},         {"gemm_sk", kTuneGemmSk},
+                {"gemm_sk_min", kTuneGemmSkMin},      {"gemm_no_dma", kTuneGemmNoDma},
+                {"gemm_smallm_max", kTuneGemmSmallmMax}, {"w4a4_smallm_cfg", kTuneW4a4SmallmCfg},
+                {"w4a16_cfg", kTuneW4a16Cfg},         {"w4a16_tile", kTuneW4a16Tile},
+                {"prep_ni", kTunePrepNi},             {"sk_spin_limit", kTuneSkSpinLimit}};
+  int key = -1;
+  for (const auto& n : kNames)
+    if (strcmp(n.name, name) == 0) key = n.key;
+  if (key < 0) return fail(CONVROT_ERR_INVALID, "unknown tuning override '%s'", name);
+  int v = -1;
+  if (value && value[0]) {
+    bool good = true;
+    switch (key) {
+      case kTuneGemmTile: {
+        int bm = 0, bn = 0, wm = 2, wn = 2, st = 0;
+        const int got = sscanf(value, "%dx%dw%dx%ds%d", &bm, &bn, &wm, &wn, &st);
+        good = got >= 2 && bm > 0 && bm <= 512 && bn > 0 && bn <= 512 && wm > 0 && wm < 16 && wn > 0 && wn < 16 &&
+               st >= 0 && st < 8;
+        v = bm | bn << 10 | wm << 20 | wn << 24 | st << 28;
+        break;
+      }
+      case kTuneW4a16Tile: {
+        int bm = 0, bn = 0;
+        good = sscanf(value, "%dx%d", &bm, &bn) == 2 && bm > 0 && bm <= 512 && bn > 0 && bn <= 512;
+        v = bm | bn << 10;
+        break;
+      }
+      case kTuneW4a4SmallmCfg:
+        good = strchr("ABCF", value[0]) != nullptr && value[1] == '\0';
+        v = value[0];
+        break;
+      case kTuneW4a16Cfg:
+        good = strchr("ABCFT", value[0]) != nullptr && value[1] == '\0';
+        v = value[0];
+        break;
+      default: {
+        char* end = nullptr;
+        const long long n = strtoll(value, &end, 10);
+        good = end && *end == '\0' && n >= 0 && n <= 0x7fffffff;
+        v = (int)n;
+      }
+    }
+    if (!good) return fail(CONVROT_ERR_INVALID, "invalid value '%s' for tuning override '%s'", value, name);
+  }
+  g_tuning[key].store(v + 1, std::memory_order_relaxed);
+  return ok();
+}
 
 const char* convrot_version(void) { return "convrot-mi355x 0.1.0 (gfx950)"; }
 
@@ -251,6 +319,39 @@ int convrot_w4a4_gemm_residual(const void* act, int act_format, const float* xsc
   return launch_status(convrot::launch_w4a4_gemm(act, act_format, xscales, qweight, wscales, bias, M, N, K, out,
                                                  out_dtype, (hipStream_t)stream, gr),
                        "convrot_w4a4_gemm_residual");
+}
+
+int64_t convrot_w4a4_workspace_bytes(void) { return (int64_t)convrot::kSkWorkspaceBytes; }
+
+int convrot_w4a4_gemm_ws(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
+                         const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
+                         const void* residual, const void* gate, int64_t gate_stride, int64_t rows_per_gate,
+                         void* workspace, int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  if (int rc = check_w4a4(act, act_format, xscales, qweight, wscales, M, N, K, out, out_dtype)) return rc;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+    return fail(CONVROT_ERR_INVALID, "invalid workspace (%lld bytes)", (long long)workspace_bytes);
+  if (workspace && !aligned(workspace, 256)) return fail(CONVROT_ERR_INVALID, "workspace must be 256-byte aligned");
+  if (gate && !residual) return fail(CONVROT_ERR_INVALID, "a gate needs a residual");
+  if (gate && rows_per_gate <= 0)
+    return fail(CONVROT_ERR_INVALID, "rows_per_gate must be positive, got %lld", (long long)rows_per_gate);
+  if (M == 0 || N == 0) return ok();
+  convrot::GatedResidual gr{};
+  if (residual)
+    if (int rc = check_residual(residual, gate, gate_stride, rows_per_gate, M, N, &gr)) return rc;
+  convrot::WorkspaceSource src;
+  src.kind = convrot::WorkspaceSource::kGiven;
+  src.given = {(uint8_t*)workspace, workspace ? (size_t)workspace_bytes : 0};
+  return launch_status(convrot::launch_w4a4_gemm(act, act_format, xscales, qweight, wscales, bias, M, N, K, out,
+                                                 out_dtype, (hipStream_t)stream, gr, src),
+                       "convrot_w4a4_gemm_ws");
+}
+
+int convrot_w4a4_status(const void* workspace, void* stream) {
+  const char* what = nullptr;
+  const int rc = convrot::w4a4_workspace_status(workspace, (hipStream_t)stream, &what);
+  if (rc < 0) return fail(CONVROT_ERR_LAUNCH, "convrot_w4a4_status: %s", hipGetErrorString(hipGetLastError()));
+  if (rc > 0) return fail(CONVROT_ERR_LAUNCH, "%s", what);
+  return ok();
 }
 
 namespace {

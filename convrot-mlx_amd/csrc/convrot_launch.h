@@ -11,6 +11,24 @@
 
 namespace convrot {
 
+// Overrides of the kernel and plan choice for tuning sweeps and tests, set
+// through convrot_set_tuning (capi.hip); -1 means "not set" (automatic choice).
+// Nothing reads the environment: production dispatch depends on the shape only.
+enum TuneKey : int {
+  kTuneGemmTile = 0,     // W4A4 tile: bm | bn << 10 | wm << 20 | wn << 24 | stages << 28 (stages 0: any)
+  kTuneGemmSk,           // W4A4 kernel kind: 0 data-parallel, 1 stream-K
+  kTuneGemmSkMin,        // shortest stream-K range in k-blocks
+  kTuneGemmNoDma,        // 1: the register-staged W4A4 kernel instead of the DMA kernels
+  kTuneGemmSmallmMax,    // largest M the few-row W4A4 kernel takes (0: never)
+  kTuneW4a4SmallmCfg,    // few-row W4A4 split, as a character code ('A', 'B', 'C', 'F')
+  kTuneW4a16Cfg,         // W4A16 kernel, as a character code ('A', 'B', 'C', 'F', 'T')
+  kTuneW4a16Tile,        // W4A16 tiled kernel tile: bm | bn << 10
+  kTunePrepNi,           // prep kernel 1024-feature iterations per wave (1, 3 or 4)
+  kTuneSkSpinLimit,      // stream-K bounded wait: polls before an owner gives up
+  kTuneCount
+};
+int tuning(TuneKey key);
+
 bool prep_plan(int64_t rows, int64_t K, int* ni_out, int* waves_out);
 
 hipError_t launch_prep(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode, void* out,
@@ -27,10 +45,36 @@ hipError_t launch_prep_gelu(const void* head, int64_t head_features, int64_t hea
                             int64_t x_features, int64_t x_stride, int dtype, int64_t rows, int log4g, int mode,
                             void* out, float* scales, hipStream_t stream);
 
+// Device memory of the stream-K W4A4 GEMM: a control block (counters,
+// generation, error word, partial-ready flags) and one int32 partial tile per
+// workgroup slot.  kSkWorkspaceBytes covers every plan on up to 256 CUs (a
+// plan needing more runs data-parallel).  It must be zero-filled before its
+// first launch; launches leave it ready for the next one and must not
+// overlap in time.
+struct Workspace {
+  uint8_t* ptr = nullptr;
+  size_t bytes = 0;
+};
+constexpr size_t kSkWorkspaceBytes = 32768 + (size_t)256 * 256 * 256 * 4;
+
+// Where a W4A4 launch takes its stream-K workspace from: the library's own
+// buffer of the launch stream (made on first need), or a given one (nullptr:
+// data-parallel plans only).
+struct WorkspaceSource {
+  enum Kind { kLibrary, kGiven } kind = kLibrary;
+  Workspace given{};
+};
+
 hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
                             const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
                             void* out, int out_dtype, hipStream_t stream,
-                            const GatedResidual& gr = GatedResidual{});
+                            const GatedResidual& gr = GatedResidual{}, WorkspaceSource src = WorkspaceSource{});
+
+// Synchronizes `stream`, then reads and clears the error word of `workspace`
+// (nullptr: the library's own workspace of the stream, if any).  Returns 0
+// (no error), 1 (a bounded stream-K wait gave up since the last check; *what
+// describes it) or -1 (a HIP call failed).
+int w4a4_workspace_status(const void* workspace, hipStream_t stream, const char** what);
 
 // Few-row W4A4 kernel (int8 activation codes only); launch_w4a4_gemm routes
 // small M here.

@@ -426,7 +426,7 @@ hipError_t launch_tiled_t(const void* act, const uint8_t* wq, const float* ws, c
 // of M = 512 .. 4096, K = 3072 .. 15360, N = 3072 .. 21504: a 128 x 128 tile
 // (two per CU) sustains the 256 x 256 tile's throughput and wins whenever the
 // 256 x 256 grid leaves CUs idle or has a partial last round.
-// CONVROT_W4A16_TILE=256x256|256x128|128x256|128x128 forces one.
+// The w4a16_tile tuning override (256x256, 256x128, 128x256 or 128x128) forces one.
 struct TiledCand {
   int bm, bn, per_cu;
   double rate;
@@ -449,7 +449,7 @@ TiledPlan tiled_plan(int64_t M, int64_t N, int64_t K) {
   const int64_t cus = device_cus();
   const int64_t kb = (K + 127) / 128;
   int bm = 0, bn = 0;
-  if (const char* env = getenv("CONVROT_W4A16_TILE")) sscanf(env, "%dx%d", &bm, &bn);
+  if (const int v = tuning(kTuneW4a16Tile); v >= 0) bm = v & 1023, bn = (v >> 10) & 1023;
   TiledPlan best{3, 1e300};
   for (int i = 0; i < (int)(sizeof(kTiledCands) / sizeof(kTiledCands[0])); ++i) {
     const TiledCand& c = kTiledCands[i];
@@ -499,8 +499,8 @@ hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const f
 //   T            the tiled kernel (256 / 128 edges), M >= kTiledMinM
 // At M = 1 both stream the 18.9 MB weight matrix in ~8 us (~2.3 TB/s), where
 // a plain 19 MB device copy takes ~10 us; the rest is weight expansion
-// (~2 VALU ops per code) and the launch/tail.  CONVROT_W4A16_CFG=A|B|C|F|T
-// overrides (tuning sweeps).
+// (~2 VALU ops per code) and the launch/tail.  The w4a16_cfg tuning override
+// (A|B|C|F|T) forces the kernel (sweeps and tests).
 constexpr int64_t kTiledMinM = 64;
 template <int ADT, int ODT>
 hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
@@ -514,8 +514,7 @@ hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, con
   // tiles of long K and stays in A up to M = 256, 78 us against 99 us).
   const double m16 = (double)((M + 15) / 16 * 16);
   if (M >= kTiledMinM && tiled_plan(M, N, K).us < 2.0 * m16 * (double)N * (double)K / 246e6 + 5.0) cfg = 'T';
-  if (const char* env = getenv("CONVROT_W4A16_CFG"))
-    if (env[0] == 'A' || env[0] == 'B' || env[0] == 'C' || env[0] == 'F' || env[0] == 'T') cfg = env[0];
+  if (const int v = tuning(kTuneW4a16Cfg); v == 'A' || v == 'B' || v == 'C' || v == 'F' || v == 'T') cfg = (char)v;
   switch (cfg) {
     case 'T': return launch_tiled<ADT, ODT>(act, wq, ws, bias, M, N, K, out, gr, stream);
     case 'C': return launch_t<ADT, ODT, 2, 2, 8, 2>(act, wq, ws, bias, M, N, K, out, gr, stream);

@@ -224,12 +224,15 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_kernel(
 // (GatedResidual); for 16-bit outputs it is applied in the write-back loop,
 // where each lane holds 8 consecutive outputs of one row and loads the
 // matching residual and gate elements as 16-byte reads.
+//
+// `poison` (a stream-K owner whose bounded wait for a partial tile gave up)
+// makes every output of the wave's tile NaN instead of a silently wrong value.
 template <int ODT, int TM, int TN, int SHIFT, bool LDS_OPS = false>
 __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], uint8_t* region, int lane,
                                          int mw, int nw, int M, int N, const float* __restrict__ xscales,
                                          const float* __restrict__ wscales, const float* __restrict__ bias,
                                          void* __restrict__ out, const GatedResidual& gr, int m0 = 0,
-                                         int n0 = 0) {
+                                         int n0 = 0, bool poison = false) {
   constexpr int FM = TM / 16, FN = TN / 16;
   float xs[FM];
 #pragma unroll
@@ -237,6 +240,7 @@ __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], u
     const int m = mw + fm * 16 + (lane & 15);
     if constexpr (LDS_OPS) xs[fm] = xscales[m - m0];
     else xs[fm] = xscales[m < M ? m : M - 1];
+    if (poison) xs[fm] = __builtin_nanf("");
   }
   if constexpr (ODT == kF32) {
     const bool vec_ok = (N & 3) == 0;
@@ -395,14 +399,50 @@ __device__ __forceinline__ int a_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1
 // Fragment pipelines (how LDS reads overlap the MFMAs):
 //  kSingle   one register set, read just before the block's MFMAs (the 8-wave
 //            256x256 tile: two waves per SIMD cover each other's reads);
-//  kPingPong two full sets, block i+1 read during block i's MFMAs.
-// (A 4-wave 256x256 tile with one wave per SIMD and the accumulator in the
-// AGPRs, fed by k-step-split reads, measured 1.8x slower: the compiler cannot
-// keep a 256-register accumulator in place and spills inside the loop.)
-enum Pipe : int { kSingle = 0, kPingPong = 1 };
+//  kPingPong two full sets, block i+1 read during block i's MFMAs;
+//  kAgpr     the 4-wave 256x256 tile: one wave per SIMD owns a 128x128 corner
+//            whose 64 accumulator fragments fill the 256 AGPRs, and the wave
+//            overlaps its own LDS reads with its MFMAs k-step by k-step
+//            (body_agpr).  The MFMAs are issued through inline asm: as
+//            builtins the compiler routes every MFMA through one AGPR tuple
+//            and copies the accumulators around it inside the loop.
+enum Pipe : int { kSingle = 0, kPingPong = 1, kAgpr = 2 };
+
+// acc += b . a on the AGPR accumulator c (v_mfma_i32_16x16x64_i8).  The
+// "memory" clobber keeps the LDS reads placed between MFMAs where the code
+// puts them.  The compiler does not see an MFMA here, so it inserts none of the
+// MFMA wait states: the callers pad VALU -> MFMA operand writes
+// (hazard_pad) and MFMA -> accumulator reads (mfma_drain) themselves.  Back to
+// back accumulation into the same registers needs no padding.
+__device__ __forceinline__ void mfma_agpr(i32x4& c, const i32x4& b, const i32x4& a) {
+  asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(b), "v"(a) : "memory");
+}
+
+// Two wait states after the VALU writes of the eight unpacked weight operands,
+// ordered before the MFMAs that read them.
+__device__ __forceinline__ void hazard_pad(const i32x4 (&w)[8]) {
+  asm volatile("s_nop 1" ::"v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]),
+               "v"(w[7])
+               : "memory");
+}
+
+// Wait states between the last MFMA and any read of its accumulators (more
+// than the 16x16x64 XDL result latency).  Each accumulator is then passed
+// through an empty asm that "redefines" it: without that, the compiler is free
+// to schedule the epilogue's AGPR reads above the padding, right after the last
+// MFMA, since nothing ties them to it.
+template <int FN, int FM>
+__device__ __forceinline__ void mfma_drain(i32x4 (&acc)[FN][FM]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) asm volatile("" : "+a"(acc[fn][fm]));
+}
 
 template <int BM, int BN, int WM, int WN, int PIPE, int STAGES = 3>
 struct DmaEngine {
+  static constexpr int kBM = BM, kBN = BN;
   static constexpr int NW = WM * WN;
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int FM = TM / 16, FN = TN / 16;
@@ -561,7 +601,165 @@ struct DmaEngine {
   // of the ring (epilogue staging or the next run).
   __device__ __forceinline__ void run(int kb0, int n, i32x4 (&acc)[FN][FM]) {
     prologue(kb0, n);
-    body(kb0, n, acc, nullptr);
+    body_any(kb0, n, acc, nullptr, 0);
+  }
+
+  // The pipeline of this engine's PIPE for k-blocks kb0 .. kb0+n-1, after
+  // prologue(kb0, n).  With `flag` set, lane 0 of each wave stores `tag` there
+  // once its first DMA wait has retired everything the wave issued before the
+  // prologue (a stream-K partial tile's stores).
+  __device__ __forceinline__ void body_any(int kb0, int n, i32x4 (&acc)[FN][FM], int* flag, int tag) {
+    if constexpr (PIPE == kAgpr) body_agpr(kb0, n, acc, flag, tag);
+    else body(kb0, n, acc, flag, tag);
+  }
+
+  // ---- kAgpr: the 4-wave 256x256 tile, 128x128 per wave (FN = FM = 8)
+  //
+  // Per k-block i (two 64-feature k-steps):
+  //   k-step 0: 64 MFMAs on (w0, a0); between them the wave reads a1 (its
+  //             k-step-1 activation fragments) and unpacks w1 from bp;
+  //   middle:   the wave's DMAs of block i+1 have landed and its a1 reads are
+  //             done; a barrier publishes block i+1 to every wave and frees
+  //             block i's ring stage, which the DMA of block i+STAGES refills;
+  //   k-step 1: 64 MFMAs on (w1, a1); between them the wave reads block i+1's
+  //             packed weights bp and k-step-0 fragments a0, and unpacks w0.
+  // So the MFMA pipe never waits for a whole block's reads, and the only
+  // workgroup barrier of a block sits between its two k-steps.
+  __device__ __forceinline__ void read_bp(int stage, uint4 (&bp)[8], int fn0, int cnt) const {
+    const uint8_t* sb = smem + stage * STAGE_BYTES + (A_FRAGS + wn * FN) * 1024 + lane * 16;
+#pragma unroll
+    for (int fn = fn0; fn < fn0 + cnt; ++fn) bp[fn] = *(const uint4*)(sb + fn * 1024);
+  }
+  __device__ __forceinline__ const uint8_t* a_base(int stage, int ks) const {
+    const int r = lane & 15;
+    return smem + stage * STAGE_BYTES + (wm * FM * 16 + r) * 128 + (((2 * (lane >> 4) + ks) ^ a_swizzle(r)) * 16);
+  }
+  __device__ __forceinline__ static void unpack(const uint4& b, int ks, i32x4& w) {
+    uint32_t l0, h0, l1, h1;
+    nibbles_x16(ks ? b.z : b.x, l0, h0);
+    nibbles_x16(ks ? b.w : b.y, l1, h1);
+    w = (i32x4){(int)l0, (int)h0, (int)l1, (int)h1};
+  }
+
+  // One DMA piece of k-block kb into ring stage `stage`: pieces 0 .. APW-1
+  // are this wave's activation pieces, APW .. LPW-1 its weight blocks (the
+  // order of issue()).
+  __device__ __forceinline__ void issue_piece(int kb, int stage, int idx) {
+    const uint32_t base = smem_addr + (uint32_t)(stage * STAGE_BYTES);
+    if (idx < APW) {
+      const uint32_t j = (uint32_t)(wave * APW + idx);
+      uint32_t so = j * krow + (uint32_t)kb * a_kstride;
+      asm volatile("" : "+s"(so));
+      dma16(ra, va[idx & 1] + so, base + j * 1024u);
+    } else {
+      const uint32_t j = (uint32_t)(wave * BPW + idx - APW);
+      uint32_t so = j * 1024u + (uint32_t)kb * w_kstride;
+      asm volatile("" : "+s"(so));
+      dma16(rw, vb + so, base + (uint32_t)(A_FRAGS + j) * 1024u);
+    }
+  }
+
+  // Half of the unpack of one k-step's weight operand (two of its four
+  // dwords, from packed dword `src`), placed by the two empty asms exactly where
+  // the call sits between two MFMAs: the first makes the source look freshly
+  // produced there, the second consumes the results there.
+  __device__ __forceinline__ static void unpack_half(uint32_t src, uint32_t& lo, uint32_t& hi) {
+    asm volatile("" : "+v"(src));
+    nibbles_x16(src, lo, hi);
+    asm volatile("" ::"v"(lo), "v"(hi));
+  }
+
+  // Filler work between the MFMAs of a k-step: with one wave per SIMD the
+  // wave issues about one instruction per four cycles, so LDS reads, weight
+  // unpacks and DMA issues placed one or two at a time between MFMAs (16
+  // cycles each) run in the MFMA's shadow, where a burst of them would leave
+  // the MFMA pipe idle.  Slot t follows MFMA t = 8 * fm + fn.
+  //
+  // k-step 0 of the block in ring stage st: MFMAs on (w0, a0); reads of a1
+  // after slots 1, 5, .., 29 and the halves of the unpack of w1 after slots
+  // 3, 7, .., 63.
+  __device__ __forceinline__ void agpr_kstep0(int st, const uint4 (&bp)[8], const i32x4 (&a0)[8], i32x4 (&a1)[8],
+                                              const i32x4 (&w0)[8], i32x4 (&w1)[8], i32x4 (&acc)[FN][FM]) const {
+    hazard_pad(w0);
+    const uint8_t* sa = a_base(st, 1);
+    uint32_t u[8][4];
+#pragma unroll
+    for (int t = 0; t < 64; ++t) {
+      const int fm = t / 8, fn = t % 8;
+      mfma_agpr(acc[fn][fm], w0[fn], a0[fm]);
+      if (t % 4 == 1 && t < 32) a1[t / 4] = *(const i32x4*)(sa + (t / 4) * 2048);
+      if (t % 4 == 3) {
+        const int j = t / 8, h = (t / 4) % 2;
+        unpack_half(h ? bp[j].w : bp[j].z, u[j][2 * h], u[j][2 * h + 1]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w1[j] = (i32x4){(int)u[j][0], (int)u[j][1], (int)u[j][2], (int)u[j][3]};
+  }
+
+  // k-step 1: MFMAs on (w1, a1); reads of the next block's bp (after slots
+  // 0, 2, .., 14) and a0 (after slots 16, 18, .., 30) from ring stage nst, the
+  // 12 DMA pieces of k-block dma_kb into stage st (after slots 1, 5, .., 45),
+  // and the halves of the unpack of the next w0 (after slots 33, 35, .., 63).
+  __device__ __forceinline__ void agpr_kstep1(int st, int nst, int dma_kb, uint4 (&bp)[8], i32x4 (&a0)[8],
+                                              const i32x4 (&a1)[8], i32x4 (&w0)[8], const i32x4 (&w1)[8],
+                                              i32x4 (&acc)[FN][FM]) {
+    static_assert(LPW == 12, "12 DMA pieces per k-block");
+    hazard_pad(w1);
+    const uint8_t* sa = a_base(nst, 0);
+    const uint8_t* sb = smem + nst * STAGE_BYTES + (A_FRAGS + wn * FN) * 1024 + lane * 16;
+    uint32_t u[8][4];
+#pragma unroll
+    for (int t = 0; t < 64; ++t) {
+      const int fm = t / 8, fn = t % 8;
+      mfma_agpr(acc[fn][fm], w1[fn], a1[fm]);
+      if (t % 2 == 0 && t < 16) bp[t / 2] = *(const uint4*)(sb + (t / 2) * 1024);
+      if (t % 2 == 0 && t >= 16 && t < 32) a0[(t - 16) / 2] = *(const i32x4*)(sa + ((t - 16) / 2) * 2048);
+      if (t % 4 == 1 && t < 48) issue_piece(dma_kb, st, t / 4);
+      if (t % 2 == 1 && t >= 33) {
+        const int k = (t - 33) / 2, j = k / 2, h = k % 2;
+        unpack_half(h ? bp[j].y : bp[j].x, u[j][2 * h], u[j][2 * h + 1]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w0[j] = (i32x4){(int)u[j][0], (int)u[j][1], (int)u[j][2], (int)u[j][3]};
+  }
+
+  // The k-loop runs one branch-free body per block, so the accumulators keep
+  // one live range (and one set of AGPRs): the last block still reads a "next"
+  // block from a ring stage nothing reads afterwards, and DMAs past the run's
+  // last k-block re-fetch that last block (in range) into stages no later
+  // block uses.  Two DMA groups are therefore in flight at every middle wait.
+  __device__ __forceinline__ void body_agpr(int kb0, int n, i32x4 (&acc)[FN][FM], int* flag, int tag) {
+    static_assert(FN == 8 && FM == 8 && NW == 4 && STAGES == 3, "kAgpr is the 4-wave 256x256 tile, 3 stages");
+    uint4 bp[8];
+    i32x4 a0[8], a1[8], w0[8], w1[8];
+    wait_vmcnt<2 * LPW>();  // block 0 (and the epilogue operands) landed
+    if (flag && lane == 0) __hip_atomic_store(flag, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_barrier();
+    read_bp(0, bp, 0, 8);
+    {
+      const uint8_t* sa = a_base(0, 0);
+#pragma unroll
+      for (int fm = 0; fm < 8; ++fm) a0[fm] = *(const i32x4*)(sa + fm * 2048);
+    }
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn) unpack(bp[fn], 0, w0[fn]);
+    const int last_kb = kb0 + n - 1;
+    int st = 0;
+    for (int i = 0; i < n; ++i) {
+      const int nst = st + 1 == STAGES ? 0 : st + 1;
+      agpr_kstep0(st, bp, a0, a1, w0, w1, acc);
+      // middle: the wave's DMAs of block i+1 and its a1 reads are done; the
+      // barrier publishes block i+1 to every wave and frees stage st
+      wait_vmcnt<LPW>();
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      agpr_kstep1(st, nst, min(kb0 + i + STAGES, last_kb), bp, a0, a1, w0, w1, acc);
+      st = nst;
+    }
+    mfma_drain(acc);
+    wait_vmcnt<0>();  // the DMAs past the last block have landed before the ring is reused
   }
 
   // Wait until at most `ahead` k-blocks of this wave's DMAs (LPW each) are in
@@ -580,19 +778,21 @@ struct DmaEngine {
   // kb0 .. kb0+STAGES-2 (kSingle) into stages 0, 1, ...  The ring must be free
   // (barrier after its last reads).
   __device__ __forceinline__ void prologue(int kb0, int n) {
-    constexpr int AHEAD = PIPE == kPingPong ? STAGES : STAGES - 1;
+    constexpr int AHEAD = PIPE == kSingle ? STAGES - 1 : STAGES;
 #pragma unroll
-    for (int s = 0; s < AHEAD; ++s)
-      if (s < n) issue(kb0 + s, s);
+    for (int s = 0; s < AHEAD; ++s) {
+      if constexpr (PIPE == kAgpr) issue(kb0 + min(s, n - 1), s);  // always STAGES groups (body_agpr)
+      else if (s < n) issue(kb0 + s, s);
+    }
   }
 
   // The rest of a run after prologue(kb0, n).  The prologue's DMAs must be the
   // newest vector-memory operations of the wave.  vmcnt retires in issue
   // order, so the first wait also retires everything the wave issued before
   // the prologue; if `flag` is set, lane 0 raises it right after that wait.
-  __device__ __forceinline__ void body(int kb0, int n, i32x4 (&acc)[FN][FM], int* flag) {
+  __device__ __forceinline__ void body(int kb0, int n, i32x4 (&acc)[FN][FM], int* flag, int tag) {
     auto raise = [&]() {
-      if (flag && lane == 0) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (flag && lane == 0) __hip_atomic_store(flag, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     Frags f0;
     if constexpr (PIPE == kPingPong) {
@@ -681,27 +881,65 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
                                               N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, gr, m0, n0);
 }
 
+// The kAgpr 4-wave 256x256 tile, one workgroup per output tile: one wave per
+// SIMD may use all 512 registers (256 VGPRs + the 256 AGPRs of the
+// accumulator).
+template <int STAGES, int ODT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void w4a4_gemm_agpr_kernel(
+    const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
+    const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
+    int K, int nblocks, int kblocks, int tiles_m, int tiles_n, GatedResidual gr) {
+  using E = DmaEngine<256, 256, 2, 2, kAgpr, STAGES>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
+  E e(smem);
+
+  const int tiles = tiles_m * tiles_n;
+  int logical = blockIdx.x;
+  const int per_xcd = tiles / kXcds;
+  if (logical < per_xcd * kXcds) logical = (logical % kXcds) * per_xcd + logical / kXcds;
+  int m0, n0;
+  tile_origin(logical, tiles_m, tiles_n, 256, 256, m0, n0);
+
+  e.set_tile(act, wq, M, K, nblocks, kblocks, m0, n0);
+  e.issue_epi(xscales, wscales, bias, M, N, m0, n0);
+  i32x4 acc[E::FN][E::FM];
+#pragma unroll
+  for (int a = 0; a < E::FN; ++a)
+#pragma unroll
+    for (int b = 0; b < E::FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
+  e.run(0, kblocks, acc);
+  __syncthreads();  // all waves done with the LDS ring before it is reused for output staging
+  epilogue<ODT, E::TM, E::TN, E::SHIFT, true>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M,
+                                              N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, gr, m0, n0);
+}
+
 // ---- stream-K
 //
-// Workspace (device memory owned by the launcher, one per device and stream):
+// Workspace (device memory, zero-filled once before its first launch; every
+// launch leaves it ready for the next launch that uses it):
 //   int32 word 32 g          ticket counter of workgroup group g (one group per XCD)
 //   int32 word 256 + 32 g    finished-workgroup counter of group g
-//   int32 words [512, 512+G*NW) partial-ready flag of each (workgroup slot, wave)
+//   int32 word 512 + 32 g    generation of group g, advanced by the group's last workgroup
+//   int32 word 768           error word: nonzero once an owner's bounded wait gave up
+//   int32 words [1024, 1024+G*NW) partial-ready flag of each (workgroup slot, wave):
+//                            the generation tag (generation + 1) of the launch that raised it
 //   bytes [kSkPartialOffset, ...)  one int32 partial tile per workgroup slot
 // Each counter has a 128-byte line to itself: every workgroup of the launch
 // performs two device-scope atomics on its group's counters, and atomics on
-// one line are serialized.
-// Every counter and flag is back at zero when a launch ends, so consecutive
-// launches on one stream share the workspace; launches that overlap in time
-// (two streams) must not.
+// one line are serialized.  Flags are never cleared: a launch waits for its
+// own generation's tag, so a flag left by an earlier launch never matches.
+// Launches that use one workspace must not overlap in time (one stream).
 constexpr int kSkLineWords = 32;
 constexpr int kSkDoneWord = kXcds * kSkLineWords;
-constexpr int kSkCtlWords = 2 * kSkDoneWord;
+constexpr int kSkGenWord = 2 * kSkDoneWord;
+constexpr int kSkErrorWord = 3 * kSkDoneWord;
+constexpr int kSkCtlWords = 4 * kSkDoneWord;
 constexpr int64_t kSkPartialOffset = 32768;
 constexpr int kSkMaxGrid = 512;  // <= 64 workgroups per group: one lane per contributor when polling
 constexpr int kSkMaxWaves = 8;
 static_assert(kSkCtlWords + kSkMaxGrid * kSkMaxWaves <= kSkPartialOffset / 4, "flags overflow the control block");
-constexpr int kSkSpinLimit = 1 << 22;  // ~1 s of s_sleep: a lost flag ends the wait instead of hanging
+constexpr int kSkGenMask = 0x3fffffff;
+constexpr int kSkSpinLimit = 1 << 22;  // ~1 s of s_sleep 4 polls: a lost flag ends the wait instead of hanging
 
 // Partials and flags are exchanged with device-scope (sc1) accesses only:
 // each is coherent across CUs (and XCDs) by itself, and order is kept by
@@ -739,7 +977,7 @@ __device__ __forceinline__ void sk_store_partial(uint8_t* dst, int lane, const i
 }
 
 // acc += one wave's partial tile: loads in batches of up to 16 fragments
-// (8 beside a 32-fragment accumulator), one wait per batch.
+// (8 beside a 32- or 64-fragment accumulator), one wait per batch.
 template <int FN, int FM>
 __device__ __forceinline__ void sk_add_partial(const uint8_t* src, int lane, i32x4 (&acc)[FN][FM]) {
   constexpr int NF = FN * FM;
@@ -766,21 +1004,33 @@ __device__ __forceinline__ void sk_add_partial(const uint8_t* src, int lane, i32
   }
 }
 
-// Lane i < n waits for flag first[i * stride] (all in parallel), then clears it.
-__device__ __forceinline__ void sk_wait_flags(int* first, int stride, int n, int lane) {
-  int* f = first + (int64_t)lane * stride;
+// Lane i < n polls flag first[i * stride] until it holds `tag` (all lanes in
+// parallel), at most spin_limit times.  Returns false (wave-uniform) when some
+// flag was not seen: the caller then reports the failure and poisons its
+// output instead of proceeding with a partial missing.
+__device__ __forceinline__ bool sk_wait_flags(const int* first, int stride, int n, int lane, int tag,
+                                              int spin_limit) {
+  const int* f = first + (int64_t)lane * stride;
   bool seen = lane >= n;
-  for (int it = 0; it < kSkSpinLimit; ++it) {
-    if (!seen) seen = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+  for (int it = 0; it < spin_limit; ++it) {
+    if (!seen) seen = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag;
     if (__ballot(!seen) == 0) break;
     __builtin_amdgcn_s_sleep(4);
   }
-  if (lane < n) __hip_atomic_store(f, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __ballot(!seen) == 0;
 }
 
-// Persistent stream-K GEMM (Osama et al., "Stream-K: Work-centric Parallel
-// Decomposition for Dense Matrix-Matrix Multiplication on the GPU", 2023), in
-// its data-parallel + stream-K hybrid form, run per XCD.
+// Arguments of a stream-K launch beyond the GEMM's own.
+struct SkArgs {
+  uint8_t* work;   // workspace (layout above)
+  int min_iters;   // shortest stream-K range, in k-blocks
+  int spin_limit;  // polls of an owner's bounded wait
+};
+
+// The persistent stream-K GEMM (Osama et al., "Stream-K: Work-centric
+// Parallel Decomposition for Dense Matrix-Matrix Multiplication on the GPU",
+// 2023), in its data-parallel + stream-K hybrid form, run per XCD, for the
+// engine E (the 8-wave tiles or the 4-wave AGPR tile).
 //
 // The grid is G = 8 P workgroups; workgroup b belongs to group b % 8 (the XCD
 // it is dispatched to) and takes a ticket 0..P-1 inside its group at start,
@@ -798,27 +1048,33 @@ __device__ __forceinline__ void sk_wait_flags(int* first, int stride, int n, int
 // (integer addition: the result is bit-identical to a single pass) and the
 // workgroup runs the fused epilogue.  Waits only ever point at lower tickets,
 // i.e. at workgroups that have already started and that wait only on lower
-// tickets themselves, so the kernel finishes whatever the residency.
-template <int BM, int BN, int WM, int WN, int PIPE, int STAGES, int ODT>
-__global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
-    const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
-    const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
-    int K, int nblocks, int kblocks, int tiles_m, int tiles_n, uint8_t* __restrict__ work, int min_iters,
-    GatedResidual gr) {
-  using E = DmaEngine<BM, BN, WM, WN, PIPE, STAGES>;
-  constexpr int FN = E::FN, FM = E::FM, NW = E::NW;
+// tickets themselves, so the kernel finishes whatever the residency.  The
+// waits are bounded all the same: an owner that gives up sets the error word
+// and writes NaN over its tile.
+template <class E, int ODT>
+__device__ __forceinline__ void sk_items(uint8_t* smem, int* s_shared, const int8_t* __restrict__ act,
+                                         const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
+                                         const float* __restrict__ wscales, const float* __restrict__ bias,
+                                         void* __restrict__ out, int M, int N, int K, int nblocks, int kblocks,
+                                         int tiles_m, int tiles_n, const SkArgs& ska, const GatedResidual& gr) {
+  constexpr int FN = E::FN, FM = E::FM, NW = E::NW, BM = E::kBM, BN = E::kBN;
   static_assert(NW <= kSkMaxWaves, "flag block sized for 8 waves");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
-  __shared__ int s_ticket;
-
-  int* ctl = (int*)work;
+  int* ctl = (int*)ska.work;
   int* flags = ctl + kSkCtlWords;
-  uint8_t* partials = work + kSkPartialOffset;
+  uint8_t* partials = ska.work + kSkPartialOffset;
   const int group = blockIdx.x % kXcds;
   const int P = gridDim.x / kXcds;
-  if (threadIdx.x == 0) s_ticket = atomicAdd(&ctl[group * kSkLineWords], 1);
+  if (threadIdx.x == 0) {
+    s_shared[0] = atomicAdd(&ctl[group * kSkLineWords], 1);
+    s_shared[1] = (__hip_atomic_load(&ctl[kSkGenWord + group * kSkLineWords], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) &
+                   kSkGenMask) + 1;
+  }
   __syncthreads();
-  const int p = __builtin_amdgcn_readfirstlane(s_ticket);
+  const int p = __builtin_amdgcn_readfirstlane(s_shared[0]);
+  const int tag = __builtin_amdgcn_readfirstlane(s_shared[1]);
+  // (constructed after the ticket: built before the barrier above, this
+  // compiler loses track of the engine's wave-uniform DMA operands)
   E e(smem);
 
   const int tiles = tiles_m * tiles_n;
@@ -832,7 +1088,7 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
   // then the pieces of its stream-K range [lo, hi) from the top down.
   // (Range arithmetic fits 32 bits: fewer than 2P tiles of <= 512 k-blocks.)
   const int sk_iters = (tx - dp) * kblocks;
-  const int psk = min(P, max(1, sk_iters / max(1, min_iters)));
+  const int psk = min(P, max(1, sk_iters / max(1, ska.min_iters)));
   const bool in_sk = sk_iters > 0 && p < psk;
   const int lo = in_sk ? sk_iters * p / psk : 0;
   int hi = in_sk ? sk_iters * (p + 1) / psk : 0;
@@ -878,7 +1134,7 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
     for (int a = 0; a < FN; ++a)
 #pragma unroll
       for (int b = 0; b < FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
-    e.body(k0, k1 - k0, acc, pending);
+    e.body_any(k0, k1 - k0, acc, pending, tag);
     pending = nullptr;
 
     int nt = 0, nk0 = 0, nk1 = 0;
@@ -904,22 +1160,28 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
         pending = flag;
       } else {
         wait_vmcnt<0>();
-        if (e.lane == 0) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (e.lane == 0) __hip_atomic_store(flag, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     } else {
+      bool ok = true;
       if (k0 > 0) {
         // Lower tickets qf .. p-1 hold the tile's earlier k-blocks; ticket q's
         // range starts at sk_iters * q / psk.
         const int tstart = (t - dp) * kblocks;
         int qf = p - 1;
         while (sk_iters * qf / psk > tstart) --qf;
-        sk_wait_flags(&flags[(group * P + qf) * NW + e.wave], NW, p - qf, e.lane);
-        for (int q = qf; q < p; ++q)
-          sk_add_partial<FN, FM>(partials + (int64_t)(group * P + q) * (BM * BN * 4) + wave_off, e.lane, acc);
+        ok = sk_wait_flags(&flags[(group * P + qf) * NW + e.wave], NW, p - qf, e.lane, tag, ska.spin_limit);
+        if (ok) {
+          for (int q = qf; q < p; ++q)
+            sk_add_partial<FN, FM>(partials + (int64_t)(group * P + q) * (BM * BN * 4) + wave_off, e.lane, acc);
+        } else if (e.lane == 0) {
+          __hip_atomic_store(&ctl[kSkErrorWord], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
       __syncthreads();  // ring -> epilogue staging
       epilogue<ODT, E::TM, E::TN, E::SHIFT, true>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN,
-                                                  M, N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, gr, m0, n0);
+                                                  M, N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, gr, m0, n0,
+                                                  !ok);
       __syncthreads();  // staging -> next item's DMA
     }
     t = nt;
@@ -928,13 +1190,41 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
     have = more;
   }
 
-  // The last workgroup of the group to finish rearms the ticket counters.
+  // The last workgroup of the group to finish rearms the ticket counters and
+  // advances the generation.
   if (threadIdx.x == 0) {
     if (atomicAdd(&ctl[kSkDoneWord + group * kSkLineWords], 1) == P - 1) {
       __hip_atomic_store(&ctl[group * kSkLineWords], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&ctl[kSkDoneWord + group * kSkLineWords], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ctl[kSkGenWord + group * kSkLineWords], tag & kSkGenMask, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+}
+
+template <int BM, int BN, int WM, int WN, int PIPE, int STAGES, int ODT>
+__global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_sk_kernel(
+    const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
+    const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
+    int K, int nblocks, int kblocks, int tiles_m, int tiles_n, SkArgs ska, GatedResidual gr) {
+  using E = DmaEngine<BM, BN, WM, WN, PIPE, STAGES>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
+  __shared__ int s_shared[2];
+  sk_items<E, ODT>(smem, s_shared, act, xscales, wq, wscales, bias, out, M, N, K, nblocks, kblocks, tiles_m, tiles_n,
+                   ska, gr);
+}
+
+// The stream-K kernel of the 4-wave AGPR 256x256 tile (512 registers per wave).
+template <int STAGES, int ODT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void w4a4_gemm_agpr_sk_kernel(
+    const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
+    const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
+    int K, int nblocks, int kblocks, int tiles_m, int tiles_n, SkArgs ska, GatedResidual gr) {
+  using E = DmaEngine<256, 256, 2, 2, kAgpr, STAGES>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
+  __shared__ int s_shared[2];
+  sk_items<E, ODT>(smem, s_shared, act, xscales, wq, wscales, bias, out, M, N, K, nblocks, kblocks, tiles_m, tiles_n,
+                   ska, gr);
 }
 
 // ---- host side: plan choice, stream-K workspace, launches
@@ -968,15 +1258,18 @@ int device_cus() {
 namespace {
 
 // Candidate tiles with the relative MFMA efficiency each sustains in steady
-// state on MI355X (256x256 moves half the L2 bytes per MFMA of 128x128 but
-// runs one workgroup per CU; 128x128 fits two per CU).  `sk` marks the tiles
-// the stream-K kernel runs well: the 256x256 one spills registers there and
+// state on MI355X, in units of the 4-wave 256x256 tile (accumulator in the
+// AGPRs, software-pipelined k-steps), which measured 2-13 % faster than the
+// 8-wave 256x256 tile on every FLUX shape at M = 1536 and 4608.  The 8-wave
+// tile moves half the L2 bytes per MFMA of 128x128 but runs one workgroup per
+// CU; 128x128 fits two per CU.  `sk` marks the tiles the stream-K kernel runs
+// well: the 8-wave 256x256 one spills registers inside its k-loop there and
 // 128x128 pieces are too short.
 //
-// The 192x128 tile moves more L2 bytes per MFMA than the 256x256 one and
-// sustains 0.75 of its rate with every CU busy, but 0.83 when its grid is a
-// single round that leaves CUs idle (1536 tokens: 192 tiles at N = 3072,
-// 21.2 us against 24.2-25.4 us for every other tile).
+// The 192x128 tile moves more L2 bytes per MFMA than the 256x256 ones and
+// sustains 0.69 of the 4-wave tile's rate with every CU busy, but 0.77 when
+// its grid is a single round that leaves CUs idle (1536 tokens: 192 tiles at
+// N = 3072).
 struct Cand {
   Tile t;
   int per_cu;
@@ -985,15 +1278,16 @@ struct Cand {
   bool sk;
   bool dma_only;  // no register-staged (packed-activation) variant
 };
-constexpr Cand kCands[5] = {{{256, 256, 2, 4, 3}, 1, 1.0, 1.0, false, false},
-                            {{128, 256, 2, 4, 4}, 1, 0.85, 0.85, true, false},
-                            {{256, 128, 4, 2, 3}, 1, 0.8, 0.8, true, false},
-                            {{128, 128, 2, 2, 3}, 2, 0.8, 0.8, false, false},
-                            {{192, 128, 4, 2, 3}, 1, 0.75, 0.83, false, true}};
+constexpr Cand kCands[6] = {{{256, 256, 2, 2, 3}, 1, 1.0, 1.0, true, true},
+                            {{256, 256, 2, 4, 3}, 1, 0.92, 0.92, false, false},
+                            {{128, 256, 2, 4, 4}, 1, 0.79, 0.79, true, false},
+                            {{256, 128, 4, 2, 3}, 1, 0.74, 0.74, true, false},
+                            {{128, 128, 2, 2, 3}, 2, 0.74, 0.74, false, false},
+                            {{192, 128, 4, 2, 3}, 1, 0.69, 0.77, false, true}};
 // Fixed cost of the stream-K fix-up (ticket, partial store and reload, the
 // extra pipeline ramp of each piece, the idle tail while owners wait), in
 // units of one 256x256 k-block; fitted to M = 512 .. 4608 FLUX shapes.
-constexpr double kSkFixupBlocks = 10.0;
+constexpr double kSkFixupBlocks = 11.0;
 constexpr int kSkMinIters = 4;
 
 // Time of one k-block of the candidate's tile on a CU, in units of a 256x256
@@ -1028,39 +1322,40 @@ double sk_time(const Cand& c, int64_t tiles, int64_t kb, int cus, int min_iters)
   return (per * c.per_cu * block_cost(c)) + (iters > 0 ? kSkFixupBlocks : 0.0);
 }
 
-// Pick the tile and kernel with the least modelled time.  Overrides for
-// tuning sweeps and tests: CONVROT_GEMM_TILE=BMxBN[wWMxWN[sS]] forces the tile,
-// CONVROT_GEMM_SK=0|1 forces the kernel kind, CONVROT_GEMM_SK_MIN sets the
-// shortest stream-K range.
-Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_sk) {
+// Pick the tile and kernel with the least modelled time.  Tuning overrides
+// (convrot_set_tuning): gemm_tile forces the tile, gemm_sk the kernel kind,
+// gemm_sk_min the shortest stream-K range.
+size_t sk_bytes(const Tile& t, int grid) { return (size_t)kSkPartialOffset + (size_t)grid * t.bm * t.bn * 4; }
+
+Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_dma, size_t ws_bytes) {
+  const bool allow_sk = allow_dma;
   const int cus = device_cus();
   const int64_t kb = (K + 127) / 128;
   int min_iters = kSkMinIters;
-  if (const char* env = getenv("CONVROT_GEMM_SK_MIN")) min_iters = std::max(1, atoi(env));
+  if (const int v = tuning(kTuneGemmSkMin); v >= 0) min_iters = std::max(1, v);
   int force_sk = -1;
-  if (const char* env = getenv("CONVROT_GEMM_SK")) force_sk = atoi(env) != 0;
+  if (const int v = tuning(kTuneGemmSk); v >= 0) force_sk = v != 0;
   if (!allow_sk) force_sk = 0;
 
   const Tile* forced = nullptr;
   Tile ft{};
-  if (const char* env = getenv("CONVROT_GEMM_TILE")) {
-    int bm = 0, bn = 0, wm = 2, wn = 2, stages = 0;  // 0: the candidate's own ring depth
-    if (sscanf(env, "%dx%dw%dx%ds%d", &bm, &bn, &wm, &wn, &stages) >= 2) {
-      ft = {bm, bn, wm, wn, stages};
-      forced = &ft;
-    }
+  if (const int v = tuning(kTuneGemmTile); v >= 0) {
+    // stages 0: the candidate's own ring depth
+    ft = {v & 1023, (v >> 10) & 1023, (v >> 20) & 15, (v >> 24) & 15, (v >> 28) & 7};
+    forced = &ft;
   }
   Plan best{{128, 128, 2, 2, 3}, false, 0, min_iters};
   double best_time = 1e300;
   for (const Cand& c : kCands) {
     const bool match = forced && c.t.bm == forced->bm && c.t.bn == forced->bn && c.t.wm == forced->wm &&
                        c.t.wn == forced->wn && (forced->stages == 0 || c.t.stages == forced->stages);
-    if ((forced && !match) || (c.dma_only && !allow_sk)) continue;
+    if ((forced && !match) || (c.dma_only && !allow_dma)) continue;
     const int64_t tiles = ((M + c.t.bm - 1) / c.t.bm) * ((N + c.t.bn - 1) / c.t.bn);
     const double td = dp_time(c, tiles, kb, cus);
     const double ts = sk_time(c, tiles, kb, cus, min_iters);
     const int grid = std::min(kSkMaxGrid, cus * c.per_cu) / kXcds * kXcds;
-    const bool sk = grid >= kXcds && (force_sk == 1 || (force_sk == -1 && c.sk && ts < td));
+    const bool sk = grid >= kXcds && sk_bytes(c.t, grid) <= ws_bytes &&
+                    (force_sk == 1 || (force_sk == -1 && c.sk && ts < td));
     const double tt = sk ? ts : td;
     if (tt < best_time * (1.0 - 1e-9)) {
       best_time = tt;
@@ -1071,60 +1366,41 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_sk) {
   return best;
 }
 
-// Stream-K workspace, one per (device, stream): launches on one stream are
-// ordered and leave the control words zeroed, so they share it.  It is the
-// library's only allocation (32 MiB for the 8-wave tiles on 256 CUs), made on
-// the first stream-K launch of a stream and kept for the process;
-// CONVROT_GEMM_SK=0 keeps every launch data-parallel and allocation-free.
+// Stream-K workspace held by the library for the entry points without a
+// workspace argument: one per (device, stream), of kSkWorkspaceBytes (enough
+// for every plan), allocated and zero-filled (stream-ordered, no host
+// synchronization) by the first launch on that stream outside graph capture,
+// and kept until the process ends.  A launch under capture on a stream that
+// has none runs a data-parallel plan (same results bit for bit).
 struct SkBuffer {
   int dev;
   hipStream_t stream;
   uint8_t* ptr;
-  size_t bytes;
 };
 std::mutex g_sk_mu;
 std::vector<SkBuffer> g_sk_buffers;
 
-// Returns nullptr (and the caller runs the data-parallel kernel) when the
-// buffer cannot be made: allocation failure, or a stream under graph capture
-// that has no buffer yet.
-uint8_t* sk_workspace(hipStream_t stream, size_t bytes) {
+Workspace library_workspace(hipStream_t stream, bool create) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  if (hipGetDevice(&dev) != hipSuccess) return {};
   std::lock_guard<std::mutex> lock(g_sk_mu);
-  SkBuffer* slot = nullptr;
-  for (SkBuffer& b : g_sk_buffers)
-    if (b.dev == dev && b.stream == stream) slot = &b;
-  if (slot && slot->bytes >= bytes) return slot->ptr;
+  for (const SkBuffer& b : g_sk_buffers)
+    if (b.dev == dev && b.stream == stream) return {b.ptr, kSkWorkspaceBytes};
+  if (!create) return {};
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
-  if (slot) {  // grow: earlier launches on this stream may still use the old buffer
-    if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
-    (void)hipFree(slot->ptr);
-    slot->ptr = nullptr;
-    slot->bytes = 0;
-  } else {
-    g_sk_buffers.push_back({dev, stream, nullptr, 0});
-    slot = &g_sk_buffers.back();
-  }
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return {};
   void* p = nullptr;
-  if (hipMalloc(&p, bytes) != hipSuccess) {
+  if (hipMalloc(&p, kSkWorkspaceBytes) != hipSuccess) {
     (void)hipGetLastError();
-    return nullptr;
+    return {};
   }
-  if (hipMemsetAsync(p, 0, (size_t)kSkPartialOffset, stream) != hipSuccess || hipStreamSynchronize(stream) != hipSuccess) {
-    (void)hipFree(p);
-    return nullptr;
+  if (hipMemsetAsync(p, 0, (size_t)kSkPartialOffset, stream) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFree(p);  // never used by a launch
+    return {};
   }
-  slot->ptr = (uint8_t*)p;
-  slot->bytes = bytes;
-  return slot->ptr;
-}
-
-// Bytes a stream-K launch of the plan needs: the control block plus one int32
-// partial tile per workgroup.  The buffer of a (device, stream) only grows.
-size_t sk_workspace_bytes(const Plan& plan) {
-  return (size_t)kSkPartialOffset + (size_t)plan.grid * (size_t)plan.t.bm * (size_t)plan.t.bn * 4;
+  g_sk_buffers.push_back({dev, stream, (uint8_t*)p});
+  return {(uint8_t*)p, kSkWorkspaceBytes};
 }
 
 template <int BM, int BN, int WM, int WN, bool APACK, int ODT>
@@ -1141,19 +1417,31 @@ hipError_t launch_tile(const void* act, const float* xs, const uint8_t* wq, cons
 template <int BM, int BN, int WM, int WN, int STAGES, int ODT>
 hipError_t launch_dma(const Plan& plan, const void* act, const float* xs, const uint8_t* wq, const float* ws,
                       const float* bias, int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr,
-                      hipStream_t stream) {
+                      const Workspace& wsp, hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
   const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
+  const int spin = tuning(kTuneSkSpinLimit);
+  const SkArgs ska{wsp.ptr, plan.min_iters, spin >= 0 ? spin : kSkSpinLimit};
+  const bool sk = plan.sk && wsp.ptr && wsp.bytes >= sk_bytes(plan.t, plan.grid);
+  if constexpr (BM == 256 && BN == 256 && WM * WN == 4) {
+    if (sk)
+      hipLaunchKernelGGL((w4a4_gemm_agpr_sk_kernel<STAGES, ODT>), dim3((unsigned)plan.grid), dim3(256), 0, stream,
+                         (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, tm,
+                         tn, ska, gr);
+    else
+      hipLaunchKernelGGL((w4a4_gemm_agpr_kernel<STAGES, ODT>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream,
+                         (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, tm,
+                         tn, gr);
+    return hipGetLastError();
+  }
   // Double-buffered fragments except on the 8-wave 256x256 tile, whose
   // 128-register accumulator leaves no room for a second set.
   constexpr int kPP = (BM == 256 && BN == 256) ? kSingle : kPingPong;
-  if (plan.sk) {
-    if (uint8_t* work = sk_workspace(stream, sk_workspace_bytes(plan))) {
-      hipLaunchKernelGGL((w4a4_gemm_sk_kernel<BM, BN, WM, WN, kPP, STAGES, ODT>), dim3((unsigned)plan.grid),
-                         dim3(WM * WN * 64), 0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N,
-                         (int)K, nblocks, kblocks, tm, tn, work, plan.min_iters, gr);
-      return hipGetLastError();
-    }
+  if (sk) {
+    hipLaunchKernelGGL((w4a4_gemm_sk_kernel<BM, BN, WM, WN, kPP, STAGES, ODT>), dim3((unsigned)plan.grid),
+                       dim3(WM * WN * 64), 0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N,
+                       (int)K, nblocks, kblocks, tm, tn, ska, gr);
+    return hipGetLastError();
   }
   hipLaunchKernelGGL((w4a4_gemm_dma_kernel<BM, BN, WM, WN, kPP, STAGES, ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
                      0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks,
@@ -1163,15 +1451,22 @@ hipError_t launch_dma(const Plan& plan, const void* act, const float* xs, const 
 
 template <bool APACK, int ODT>
 hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
-                    int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
-  const bool dma = !APACK && !getenv("CONVROT_GEMM_NO_DMA");
-  const Plan plan = choose_plan(M, N, K, dma);
+                    int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr, WorkspaceSource src,
+                    hipStream_t stream) {
+  const bool dma = !APACK && tuning(kTuneGemmNoDma) != 1;
+  // The plan with the workspace this call can have; the library's own buffer
+  // is made only when the chosen plan needs it.
+  Workspace wsp = src.kind == WorkspaceSource::kLibrary ? library_workspace(stream, false) : src.given;
+  const size_t avail = src.kind == WorkspaceSource::kLibrary && !wsp.ptr ? kSkWorkspaceBytes : wsp.bytes;
+  const Plan plan = choose_plan(M, N, K, dma, dma ? avail : 0);
+  if (plan.sk && !wsp.ptr && src.kind == WorkspaceSource::kLibrary) wsp = library_workspace(stream, true);
   const Tile t = plan.t;
   if (dma) {
 #define CONVROT_DMA(BM_, BN_, WM_, WN_, S_)                                       \
   if (t.bm == BM_ && t.bn == BN_ && t.wm == WM_ && t.wn == WN_ && t.stages == S_) \
-    return launch_dma<BM_, BN_, WM_, WN_, S_, ODT>(plan, act, xs, wq, ws, bias, M, N, K, out, gr, stream);
+    return launch_dma<BM_, BN_, WM_, WN_, S_, ODT>(plan, act, xs, wq, ws, bias, M, N, K, out, gr, wsp, stream);
     CONVROT_DMA(256, 256, 2, 4, 3)
+    CONVROT_DMA(256, 256, 2, 2, 3)
     CONVROT_DMA(256, 128, 4, 2, 3)
     CONVROT_DMA(128, 256, 2, 4, 4)
     CONVROT_DMA(128, 128, 2, 2, 3)
@@ -1195,11 +1490,11 @@ hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const f
 template <bool APACK>
 hipError_t launch_odt(int odt, const void* act, const float* xs, const uint8_t* wq, const float* ws,
                       const float* bias, int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr,
-                      hipStream_t stream) {
+                      WorkspaceSource src, hipStream_t stream) {
   switch (odt) {
-    case kF32: return launch_t<APACK, kF32>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
-    case kF16: return launch_t<APACK, kF16>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
-    default: return launch_t<APACK, kBF16>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
+    case kF32: return launch_t<APACK, kF32>(act, xs, wq, ws, bias, M, N, K, out, gr, src, stream);
+    case kF16: return launch_t<APACK, kF16>(act, xs, wq, ws, bias, M, N, K, out, gr, src, stream);
+    default: return launch_t<APACK, kBF16>(act, xs, wq, ws, bias, M, N, K, out, gr, src, stream);
   }
 }
 
@@ -1211,20 +1506,40 @@ constexpr int64_t kSmallMWideElems = 40000000;  // N * K, i.e. 20 MB of int4 wei
 
 hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
                             const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
-                            void* out, int out_dtype, hipStream_t stream, const GatedResidual& gr) {
+                            void* out, int out_dtype, hipStream_t stream, const GatedResidual& gr,
+                            WorkspaceSource src) {
   if (M == 0 || N == 0) return hipSuccess;
   if (act_format == CONVROT_ACT_PACKED)
-    return launch_odt<true>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, gr, stream);
+    return launch_odt<true>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, gr, src, stream);
   // Few rows: the weight-streaming kernel (same results bit for bit).  It
   // wins up to M = 32 everywhere measured, and up to 64 while the int4 weight
   // is at most ~20 MB (beyond that the tiled kernel's 16-17 us floor is lower).
-  // CONVROT_GEMM_SMALLM_MAX sets the largest M it takes (0: never).
+  // The gemm_smallm_max tuning override sets the largest M it takes (0: never).
   int64_t small_max = N * K <= kSmallMWideElems ? kSmallMMaxWide : kSmallMMax;
-  if (const char* env = getenv("CONVROT_GEMM_SMALLM_MAX")) small_max = atoll(env);
+  if (const int v = tuning(kTuneGemmSmallmMax); v >= 0) small_max = v;
   if (M <= small_max)
     return launch_w4a4_smallm((const int8_t*)act, xscales, qweight, wscales, bias, M, N, K, out, out_dtype, stream,
                               gr);
-  return launch_odt<false>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, gr, stream);
+  return launch_odt<false>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, gr, src, stream);
+}
+
+int w4a4_workspace_status(const void* workspace, hipStream_t stream, const char** what) {
+  *what = nullptr;
+  if (hipStreamSynchronize(stream) != hipSuccess) return -1;
+  const uint8_t* bufs[2] = {(const uint8_t*)workspace, nullptr};
+  if (!workspace) bufs[0] = library_workspace(stream, false).ptr;
+  for (const uint8_t* b : bufs) {
+    if (!b) continue;
+    int err = 0;
+    if (hipMemcpy(&err, b + 4 * kSkErrorWord, 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    if (err) {
+      const int zero = 0;
+      if (hipMemcpy((uint8_t*)b + 4 * kSkErrorWord, &zero, 4, hipMemcpyHostToDevice) != hipSuccess) return -1;
+      *what = "a stream-K owner gave up waiting for a partial tile (bounded wait); its output tile was written as NaN";
+      return 1;
+    }
+  }
+  return 0;
 }
 
 }  // namespace convrot

@@ -158,15 +158,14 @@ hipError_t launch_t(const int8_t* act, const float* xs, const uint8_t* wq, const
 //   C (2,2,8,2)   32 < M <= 64
 //   F (4,2,4,2)   sweeps and tests only
 // At M = 1, 3072 -> 18432 (28.3 MB of int4 weights) takes 9.9 us (2.9 TB/s)
-// against 17.4 us in the tiled kernel.  CONVROT_W4A4_SMALLM_CFG=A|B|C|F
-// overrides the choice.
+// against 17.4 us in the tiled kernel.  The w4a4_smallm_cfg tuning override
+// (A|B|C|F) forces the choice.
 template <int ODT>
 hipError_t launch_shape(const int8_t* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
                         int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
   const int64_t nblocks = (N + 15) / 16;
   char cfg = M > 32 ? 'C' : (M <= 16 && nblocks <= 256 ? 'B' : 'A');
-  if (const char* env = getenv("CONVROT_W4A4_SMALLM_CFG"))
-    if (env[0] == 'A' || env[0] == 'B' || env[0] == 'C' || env[0] == 'F') cfg = env[0];
+  if (const int v = tuning(kTuneW4a4SmallmCfg); v == 'A' || v == 'B' || v == 'C' || v == 'F') cfg = (char)v;
   switch (cfg) {
     case 'A': return launch_t<ODT, 1, 2, 8, 3>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);
     case 'B': return launch_t<ODT, 1, 1, 16, 4>(act, xs, wq, ws, bias, M, N, K, out, gr, stream);

@@ -534,8 +534,8 @@ hipError_t launch_prep_s(int s, int ni, int mode, const void* x, void* out, floa
 // that enough waves are in flight to cover the load latency.
 bool prep_plan(int64_t rows, int64_t K, int* ni_out, int* waves_out) {
   const int64_t blocks = (K + 1023) / 1024;
-  if (const char* env = getenv("CONVROT_PREP_NI")) {  // tuning sweeps: force iterations per wave
-    const int ni = atoi(env);
+  {  // tuning override: force the iterations per wave
+    const int ni = tuning(kTunePrepNi);
     if (ni == 1 || ni == 3 || ni == 4) {
       const int64_t w = (blocks + ni - 1) / ni;
       if (w <= kMaxWaves) {

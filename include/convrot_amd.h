@@ -9,16 +9,28 @@
  *
  * Conventions
  *  - Every pointer is a device pointer the caller allocated; tensors are dense
- *    row-major unless stated.  The library's only allocation is the stream-K
- *    GEMM workspace (32 MiB per device and stream, made on the first
- *    stream-K launch of that stream and kept; CONVROT_GEMM_SK=0 disables it).
+ *    row-major unless stated.
  *  - `stream` is a hipStream_t passed as void* (NULL = the default stream).
- *    Work is enqueued asynchronously; nothing synchronizes the host.
+ *    Work is enqueued asynchronously; no entry point synchronizes the host
+ *    except convrot_w4a4_status.
  *  - Return value: CONVROT_OK or a nonzero status.  convrot_last_error()
  *    returns a thread-local message for the last failure on the calling
  *    thread (the same text the Python layer raises as ValueError).
- *  - Calls are stateless and reentrant; concurrent calls on different streams
- *    are safe.
+ *  - Scratch memory.  The W4A4 GEMM's stream-K plans need a workspace of
+ *    convrot_w4a4_workspace_bytes() (a control block plus int32 partial
+ *    tiles).  convrot_w4a4_gemm_ws takes it from the caller.  convrot_w4a4_gemm
+ *    and convrot_w4a4_gemm_residual use the library's own workspace of the
+ *    (device, stream): the first launch on that stream outside graph capture
+ *    that needs it allocates it (hipMalloc + a stream-ordered zero fill, no
+ *    host synchronization) and it is kept until the process ends; a launch
+ *    under capture on a stream without one runs a data-parallel plan (same
+ *    results bit for bit).  This is the library's only allocation and its only
+ *    global state besides convrot_set_tuning's overrides.  Launches that use
+ *    one workspace must not overlap in time: keep them on one stream, and do
+ *    not replay a captured graph concurrently with other launches on its
+ *    capture stream.
+ *  - Otherwise calls are reentrant; concurrent calls on different streams are
+ *    safe.
  */
 #ifndef CONVROT_AMD_H
 #define CONVROT_AMD_H
@@ -153,6 +165,42 @@ int convrot_w4a4_gemm_residual(const void* act, int act_format, const float* xsc
                                void* out, int out_dtype, void* stream);
 
 /*
+ * Bytes of stream-K workspace the W4A4 GEMM can use (any shape, up to 256
+ * CUs).  No counterpart in the reference (MLX allocates kernel outputs,
+ * core.py:1106-1113, and its TensorOp needs no scratch).
+ */
+int64_t convrot_w4a4_workspace_bytes(void);
+
+/*
+ * convrot_w4a4_gemm / convrot_w4a4_gemm_residual (residual NULL: the plain
+ * GEMM; gate and its arguments as there) with a caller-provided workspace:
+ * `workspace` is device memory of `workspace_bytes`, 256-byte aligned,
+ * zero-filled before its first use and then reused unchanged by later calls
+ * (each call leaves it ready for the next); NULL or fewer bytes than a
+ * stream-K plan needs restricts the call to data-parallel plans.  Calls that
+ * share a workspace must not overlap in time.  Replaces the same launch sites
+ * as convrot_w4a4_gemm (core.py:1061, 1088); the Python layer uses this form
+ * with a workspace it allocates through torch.
+ */
+int convrot_w4a4_gemm_ws(const void* act, int act_format, const float* xscales,
+                         const uint8_t* qweight, const float* wscales, const float* bias,
+                         int64_t M, int64_t N, int64_t K, const void* residual,
+                         const void* gate, int64_t gate_stride, int64_t rows_per_gate,
+                         void* workspace, int64_t workspace_bytes, void* out, int out_dtype,
+                         void* stream);
+
+/*
+ * Reports whether a stream-K owner's bounded wait gave up (a partial tile
+ * that never arrived; that owner wrote NaN over its output tile instead of a
+ * silently wrong value) since the last call: synchronizes `stream`, reads and
+ * clears the error word of `workspace` (NULL: the library's own workspace of
+ * `stream`).  Returns CONVROT_ERR_LAUNCH with a message if so, else CONVROT_OK.
+ * Not callable under graph capture.  No counterpart in the reference (its
+ * kernels have no error path, core.py:1106-1120).
+ */
+int convrot_w4a4_status(const void* workspace, void* stream);
+
+/*
  * W4A16 GEMM: out[m, n] = out_dtype((dot_f32(act[m, :], w[n, :]) * wscales[n]) + bias[n]).
  * Replaces mpp_w4a16_matmul (core.py:1123-1152): the MPP float x int4 TensorOp
  * (core.py:877-912) plus the elementwise epilogue (core.py:1151-1152).
@@ -197,6 +245,26 @@ int64_t convrot_cdna4_bytes(int64_t N, int64_t K);
 
 /* Thread-local message of the last failed call on this thread ("" if none). */
 const char* convrot_last_error(void);
+
+/*
+ * Tuning override: force one of the library's kernel / plan choices for
+ * tuning sweeps and tests (value NULL or "" restores the automatic choice,
+ * which depends on the shape only).  Process-wide; the library reads no
+ * environment variables.  No counterpart in the reference (its kernel choice
+ * is the backend name, core.py:1231-1242).  Names and values:
+ *   gemm_tile        "BMxBN[wWMxWN[sS]]"  W4A4 tile (and ring depth S)
+ *   gemm_sk          "0" | "1"            W4A4 data-parallel / stream-K kernel
+ *   gemm_sk_min      k-blocks             shortest stream-K range
+ *   gemm_no_dma      "1"                  register-staged int8 W4A4 kernel
+ *   gemm_smallm_max  rows                 largest M of the few-row W4A4 kernel (0: never)
+ *   w4a4_smallm_cfg  "A" | "B" | "C" | "F"  few-row W4A4 work split
+ *   w4a16_cfg        "A" | "B" | "C" | "F" | "T"  W4A16 split or tiled kernel
+ *   w4a16_tile       "BMxBN"              W4A16 tiled-kernel tile
+ *   prep_ni          "1" | "3" | "4"      prep kernel 1024-feature blocks per wave
+ *   sk_spin_limit    polls                stream-K bounded wait before giving up
+ * Returns CONVROT_ERR_INVALID for an unknown name or a malformed value.
+ */
+int convrot_set_tuning(const char* name, const char* value);
 
 /* Library version string. */
 const char* convrot_version(void);

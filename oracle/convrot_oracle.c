@@ -232,6 +232,27 @@ int cr_oracle_w4a4_matmul(const int8_t* a_codes, const int8_t* w_codes,
 }
 
 /*
+ * The epilogue of reference_w4a4_matmul (core.py:1168-1171) applied to exact
+ * integer dots computed elsewhere: ((dot * xscales[m]) * wscales[n]) + bias[n]
+ * as three float32 ops, then .astype(out dtype).  cr_oracle_w4a4_matmul is
+ * this loop fused with its int64 dot; the split form lets a caller compute the
+ * dots of a large product by another exact method.
+ */
+int cr_oracle_w4a4_epilogue(const int32_t* dots, const float* xscales, const float* wscales,
+                            const float* bias, int64_t M, int64_t N, int out_dt, void* out) {
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t n = 0; n < N; ++n) {
+            float v = (float)dots[m * N + n];
+            v = v * xscales[m];
+            v = v * wscales[n];
+            v = v + bias[n];
+            store_elem(out_dt, out, m * N + n, v);
+        }
+    }
+    return 0;
+}
+
+/*
  * mpp_w4a16_matmul (core.py:1123-1152): dots = act(float) . codes in float32
  * with an unspecified summation order (the Metal TensorOp), then
  * (dots * wscales[n]) + bias[n] as two float32 ops (core.py:1151) and

@@ -54,6 +54,7 @@ def lib() -> ctypes.CDLL:
         L.cr_oracle_quantize_rowwise.argtypes = [vp, i32, i64, i64, vp, vp, vp]
         L.cr_oracle_prepare.argtypes = [vp, i32, i64, i64, i32, vp, vp, vp]
         L.cr_oracle_w4a4_matmul.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, vp, vp]
+        L.cr_oracle_w4a4_epilogue.argtypes = [vp, vp, vp, vp, i64, i64, i32, vp]
         L.cr_oracle_w4a16_matmul.argtypes = [vp, i32, vp, vp, vp, i64, i64, i64, i32, vp, vp, vp]
         L.cr_oracle_f32_to_dtype.argtypes = [vp, i64, i32, vp]
         L.cr_oracle_modulate.argtypes = [vp, i32, i64, i64, vp, vp, i64, ctypes.c_float, vp]
@@ -249,6 +250,43 @@ def w4a4_matmul_codes(a_codes, w_codes, xscales, wscales, bias, out_dtype: str, 
         DTYPE_CODES[out_dtype], _ptr(out), _ptr(dots) if want_dots else None,
     )
     return (out, dots) if want_dots else out
+
+
+def w4a4_dots_exact(a_codes, w_codes) -> np.ndarray:
+    """Exact int32 dots a_codes [M, K] . w_codes [N, K]^T through a float32 matmul, the way
+    reference_w4a4_matmul (core.py:1166-1167) forms them: every product of two codes in
+    [-8, 7] is an integer of magnitude <= 64 and every partial sum an integer of magnitude
+    <= 64 K < 2^24, so each float32 add (or fma) is exact in any order and the BLAS result
+    equals the int64 dot.  Rows go through in slabs to bound the float32 copies."""
+    a_codes = np.ascontiguousarray(a_codes, dtype=np.int8)
+    w_codes = np.ascontiguousarray(w_codes, dtype=np.int8)
+    M, K = a_codes.shape
+    assert w_codes.shape[1] == K and 64 * K < 2 ** 24, "float32 dots are exact only while 64 K < 2^24"
+    wf = w_codes.astype(np.float32).T.copy()
+    out = np.empty((M, w_codes.shape[0]), dtype=np.int32)
+    slab = max(1, (1 << 26) // max(1, K + w_codes.shape[0]))
+    for m0 in range(0, M, slab):
+        out[m0:m0 + slab] = np.matmul(a_codes[m0:m0 + slab].astype(np.float32), wf)
+    return out
+
+
+def w4a4_epilogue(dots, xscales, wscales, bias, out_dtype: str) -> np.ndarray:
+    """The float32 epilogue of reference_w4a4_matmul (core.py:1168-1171) on given int32 dots."""
+    dots = np.ascontiguousarray(dots, dtype=np.int32)
+    M, N = dots.shape
+    xs = np.ascontiguousarray(xscales, dtype=np.float32)
+    ws = np.ascontiguousarray(wscales, dtype=np.float32)
+    b = np.ascontiguousarray(bias, dtype=np.float32)
+    assert xs.shape == (M,) and ws.shape == (N,) and b.shape == (N,)
+    out = np.empty((M, N), dtype=np.float32 if out_dtype == "float32" else np.uint16)
+    lib().cr_oracle_w4a4_epilogue(_ptr(dots), _ptr(xs), _ptr(ws), _ptr(b), M, N, DTYPE_CODES[out_dtype], _ptr(out))
+    return out
+
+
+def w4a4_matmul_codes_large(a_codes, w_codes, xscales, wscales, bias, out_dtype: str) -> np.ndarray:
+    """w4a4_matmul_codes for full-size products: exact dots by w4a4_dots_exact, then the C
+    epilogue (the same float32 sequence as cr_oracle_w4a4_matmul)."""
+    return w4a4_epilogue(w4a4_dots_exact(a_codes, w_codes), xscales, wscales, bias, out_dtype)
 
 
 def reference_w4a4_matmul(qact, qweight_nk, xscales, wscales, bias, out_dtype: str):

@@ -35,3 +35,21 @@ def orc():
 
     oracle.build()
     return oracle
+
+
+@pytest.fixture
+def tuning():
+    """set(name, value) forces a kernel / plan choice of the HIP library for one test
+    (convrot_set_tuning); every override is restored to automatic at teardown."""
+    from convrot_mlx_amd import _native
+
+    used = set()
+
+    class _Tuning:
+        def set(self, name, value):
+            used.add(name)
+            _native.set_tuning(name, value)
+
+    yield _Tuning()
+    for name in used:
+        _native.set_tuning(name, None)

@@ -128,14 +128,14 @@ _TILES = ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2", "192x128w4
 @pytest.mark.parametrize("no_dma", [False, True], ids=["dma", "regstaged"])
 @pytest.mark.parametrize("tile", _TILES)
 @pytest.mark.parametrize("seed,M,K,N", [(41, 300, 384, 530), (42, 17, 2688, 46), (43, 520, 256, 264)])
-def test_every_tile_config(orc, dev, monkeypatch, tile, no_dma, seed, M, K, N):
-    """Each GEMM tile variant (forced through CONVROT_GEMM_TILE; CONVROT_GEMM_NO_DMA selects the
-    register-staged int8 kernel) on ragged M/N/K tails."""
-    monkeypatch.setenv("CONVROT_GEMM_TILE", tile)
+def test_every_tile_config(orc, dev, tuning, tile, no_dma, seed, M, K, N):
+    """Each GEMM tile variant (forced through the gemm_tile tuning override; gemm_no_dma selects
+    the register-staged int8 kernel) on ragged M/N/K tails."""
+    tuning.set("gemm_tile", tile)
     if no_dma:
-        monkeypatch.setenv("CONVROT_GEMM_NO_DMA", "1")
+        tuning.set("gemm_no_dma", "1")
     else:
-        monkeypatch.delenv("CONVROT_GEMM_NO_DMA", raising=False)
+        tuning.set("gemm_no_dma", None)
     rng = np.random.default_rng(seed)
     a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
     w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
@@ -147,21 +147,22 @@ def test_every_tile_config(orc, dev, monkeypatch, tile, no_dma, seed, M, K, N):
         _assert_exact(got, expected, f"{name} tile {tile}")
 
 
-@pytest.mark.parametrize("tile", ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2", "192x128w4x2"])
+@pytest.mark.parametrize("tile", ["256x256w2x4", "256x256w2x2", "256x128w4x2", "128x256w2x4", "128x128w2x2",
+                                  "192x128w4x2"])
 @pytest.mark.parametrize(
     "seed,M,K,N,sk_min",
     [(51, 300, 2688, 530, 1),    # tiles split into up to 21 one-k-block pieces
      (52, 37, 64, 46, 1),        # a single k-block: pieces are whole tiles
      (53, 2100, 384, 16384, 4)],  # whole-tile rounds followed by a stream-K remainder
 )
-def test_stream_k(orc, dev, monkeypatch, tile, seed, M, K, N, sk_min):
+def test_stream_k(orc, dev, tuning, tile, seed, M, K, N, sk_min):
     """Stream-K kernel forced on: partial tiles summed across workgroups must give the
     single-pass result bit for bit; two launches in a row check the re-armed counters."""
     api = _api()
-    monkeypatch.setenv("CONVROT_GEMM_TILE", tile)
-    monkeypatch.setenv("CONVROT_GEMM_SK", "1")
-    monkeypatch.setenv("CONVROT_GEMM_SK_MIN", str(sk_min))
-    monkeypatch.delenv("CONVROT_GEMM_NO_DMA", raising=False)
+    tuning.set("gemm_tile", tile)
+    tuning.set("gemm_sk", "1")
+    tuning.set("gemm_sk_min", str(sk_min))
+    tuning.set("gemm_no_dma", None)
     rng = np.random.default_rng(seed)
     a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
     w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
@@ -180,16 +181,17 @@ def test_stream_k(orc, dev, monkeypatch, tile, seed, M, K, N, sk_min):
 
 
 @pytest.mark.parametrize("sk", [False, True], ids=["dp", "sk"])
-@pytest.mark.parametrize("tile", ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2", "192x128w4x2"])
+@pytest.mark.parametrize("tile", ["256x256w2x4", "256x256w2x2", "256x128w4x2", "128x256w2x4", "128x128w2x2",
+                                  "192x128w4x2"])
 @pytest.mark.parametrize("out_dtype", ["float32", "float16"])
-def test_epilogue_operands_without_bias(orc, dev, monkeypatch, tile, sk, out_dtype):
+def test_epilogue_operands_without_bias(orc, dev, tuning, tile, sk, out_dtype):
     """The DMA kernels stage xs / ws / bias of each tile in LDS: ragged M and N that are not
     multiples of 4 (the staged copies end mid-vector) and a missing bias (read as zeros)."""
     api = _api()
-    monkeypatch.setenv("CONVROT_GEMM_TILE", tile)
-    monkeypatch.setenv("CONVROT_GEMM_SK", "1" if sk else "0")
-    monkeypatch.setenv("CONVROT_GEMM_SK_MIN", "1")
-    monkeypatch.delenv("CONVROT_GEMM_NO_DMA", raising=False)
+    tuning.set("gemm_tile", tile)
+    tuning.set("gemm_sk", "1" if sk else "0")
+    tuning.set("gemm_sk_min", "1")
+    tuning.set("gemm_no_dma", None)
     M, K, N = 301, 384, 531
     rng = np.random.default_rng(61)
     a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
@@ -222,14 +224,20 @@ def test_kn_layout_entry_matches(orc, dev):
     _assert_exact(from_dev(out), orc.w4a4_matmul_codes(a, w, xs, ws, b, "float32"), "kn entry")
 
 
-@pytest.mark.parametrize("M,G,K,N", [(1536, 64, 3072, 9216), (1536, 64, 3072, 3072), (1536, 64, 3072, 12288),
-                                     (1536, 64, 12288, 3072), (1536, 64, 3072, 21504), (1536, 64, 15360, 3072),
-                                     (4608, 256, 3072, 12288), (4608, 256, 15360, 3072)])
+# Benchmark configs 2 (M = 1536, G = 64) and 3 (M = 4608, G = 256, the four FLUX double-block
+# shapes plus the fused single-block linears 3072->21504 and 15360->3072).
+FLUX_SHAPES = [(1536, 64, 3072, 9216), (1536, 64, 3072, 3072), (1536, 64, 3072, 12288), (1536, 64, 12288, 3072),
+               (1536, 64, 3072, 21504), (1536, 64, 15360, 3072),
+               (4608, 256, 3072, 9216), (4608, 256, 3072, 3072), (4608, 256, 3072, 12288), (4608, 256, 12288, 3072),
+               (4608, 256, 3072, 21504), (4608, 256, 15360, 3072)]
+
+
+@pytest.mark.parametrize("M,G,K,N", FLUX_SHAPES)
 def test_flux_shapes_complete_path(orc, dev, M, G, K, N):
-    """benchmark configs 2/3 at full size (M = 1536, G = 64; and M = 4608, G = 256 on the
-    config-3 MLP-up and single-block down shapes): prep (HIP) -> GEMM (HIP).  Codes and scales
-    must equal the oracle's everywhere; outputs are compared exactly on a seeded sample of 48
-    rows x all columns."""
+    """benchmark configs 2/3 at full size through ConvRotLinear (prep kernel -> GEMM kernel),
+    on the configs' heavy-tailed inputs.  Every weight code and scale, every activation code
+    and scale, and every output must equal the oracle's bit for bit (the oracle's dots come
+    from w4a4_dots_exact, its epilogue from the C restatement)."""
     api = _api()
     x = outlier_input(K + N, (M, K), "bfloat16", orc)
     w = outlier_input(K * 3 + N, (N, K), "bfloat16", orc, std=0.02, frac=0.01, factor=10.0)
@@ -239,24 +247,27 @@ def test_flux_shapes_complete_path(orc, dev, M, G, K, N):
     layer = api.ConvRotLinear(K, N, group_size=G, backend="hip-w4a4", device=dev)
     layer.load_nk_weight(qw, ws, torch.from_numpy(bias).to(dev))
     y = from_dev(layer(xd))
-    rows = np.sort(np.random.default_rng(K).choice(M, size=48, replace=False))
-    a_codes, xs = orc.prepare_codes(x[rows], "bfloat16", G)
+    a_dev, xs_dev = api.hip_fused_prepare_convrot_activation_i8(xd, G)
     w_codes, wscales = orc.prepare_codes(w, "bfloat16", G)
-    assert np.array_equal(from_dev(ws), wscales)
-    expected = orc.w4a4_matmul_codes(a_codes, w_codes, xs, wscales, bias, "bfloat16")
-    _assert_exact(y[rows], expected, f"{M}x{K}->{N}")
+    assert np.array_equal(from_dev(ws), wscales), "weight scales"
+    assert np.array_equal(orc.unpack_signed_int4(from_dev(qw)), w_codes), "weight codes"
+    a_codes, xs = orc.prepare_codes(x, "bfloat16", G)
+    assert np.array_equal(from_dev(xs_dev), xs), "activation scales"
+    assert np.array_equal(from_dev(a_dev), a_codes), "activation codes"
+    expected = orc.w4a4_matmul_codes_large(a_codes, w_codes, xs, wscales, bias, "bfloat16")
+    _assert_exact(y, expected, f"{M}x{K}->{N}")
 
 
 @pytest.mark.parametrize("cfg", ["A", "B", "C", "F"])
 @pytest.mark.parametrize("out_dtype", ["bfloat16", "float32", "float16"])
 @pytest.mark.parametrize("seed,M,K,N", [(61, 1, 3072, 530), (62, 5, 64, 46), (63, 16, 2688, 18432 // 8),
                                         (64, 17, 384, 100), (65, 32, 1024, 1024), (66, 47, 256, 33)])
-def test_small_m_kernel(orc, dev, monkeypatch, cfg, out_dtype, seed, M, K, N):
+def test_small_m_kernel(orc, dev, tuning, cfg, out_dtype, seed, M, K, N):
     """The few-row W4A4 kernel (every work split, forced) against the oracle bit for bit,
     on ragged N and K tails, one to three token tiles."""
     api = _api()
-    monkeypatch.setenv("CONVROT_GEMM_SMALLM_MAX", "64")
-    monkeypatch.setenv("CONVROT_W4A4_SMALLM_CFG", cfg)
+    tuning.set("gemm_smallm_max", "64")
+    tuning.set("w4a4_smallm_cfg", cfg)
     rng = np.random.default_rng(seed)
     a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
     w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
@@ -274,3 +285,69 @@ def test_small_m_kernel(orc, dev, monkeypatch, cfg, out_dtype, seed, M, K, N):
     no_bias = api.hip_w4a4_int8_matmul(a8, wq, args[0], args[1], None, output_dtype=dt, out_features=N)
     _assert_exact(from_dev(no_bias), orc.w4a4_matmul_codes(a, w, xs, ws, np.zeros(N, np.float32), out_dtype),
                   f"small-M cfg {cfg} without bias")
+
+
+@pytest.mark.parametrize("tile", ["256x256w2x4", "256x256w2x2"])
+@pytest.mark.parametrize("M,K,N", [(4608, 3072, 3072), (1536, 12288, 3072), (520, 15360, 1000), (300, 128, 264)])
+def test_large_tiles_full_output(orc, dev, tuning, tile, M, K, N):
+    """The two 256x256 tiles (8 waves with the accumulator in VGPRs; 4 waves with it in the
+    AGPRs, software-pipelined k-steps) forced on full-size and ragged shapes, every output
+    compared bit for bit: one and many k-blocks, a ragged last tile row and column."""
+    api = _api()
+    tuning.set("gemm_tile", tile)
+    tuning.set("gemm_sk", "0")
+    rng = np.random.default_rng(M + K + N)
+    a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    b = rng.normal(size=(N,)).astype(np.float32)
+    out = api.hip_w4a4_int8_matmul(torch.from_numpy(a).to(dev), _dev_u8(orc.codes_to_cdna4(w), dev),
+                                   torch.from_numpy(xs).to(dev), torch.from_numpy(ws).to(dev),
+                                   torch.from_numpy(b).to(dev), output_dtype=torch.bfloat16, out_features=N)
+    _assert_exact(from_dev(out), orc.w4a4_matmul_codes_large(a, w, xs, ws, b, "bfloat16"), f"tile {tile}")
+
+
+@pytest.mark.parametrize("tile", ["256x256w2x2", "128x256w2x4"])
+def test_stream_k_wait_timeout_is_reported(orc, dev, tuning, tile):
+    """A stream-K owner whose bounded wait for a partial tile gives up -- forced from the host
+    with zero polls, so every kernel still runs to its end -- writes NaN over its tile instead
+    of a silently wrong value and sets the workspace's error word: w4a4_status raises once and
+    clears it.  The next launch (normal bounded wait) is exact again: flags left by the failed
+    launch carry an older generation and never match."""
+    api = _api()
+    from convrot_mlx_amd import _native as nat
+
+    tuning.set("gemm_tile", tile)
+    tuning.set("gemm_sk", "1")
+    tuning.set("gemm_sk_min", "1")
+    M, K, N = 600, 2688, 600
+    rng = np.random.default_rng(71)
+    a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    b = rng.normal(size=(N,)).astype(np.float32)
+    expected = orc.w4a4_matmul_codes(a, w, xs, ws, b, "float32")
+    args = (torch.from_numpy(a).to(dev), _dev_u8(orc.codes_to_cdna4(w), dev), torch.from_numpy(xs).to(dev),
+            torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev))
+
+    def run():
+        out = api.hip_w4a4_int8_matmul(*args, output_dtype=torch.float32, out_features=N)
+        torch.cuda.synchronize()
+        return from_dev(out)
+
+    api.w4a4_status(dev)  # nothing pending from earlier tests
+    tuning.set("sk_spin_limit", "0")
+    got = run()
+    nan = np.isnan(got)
+    assert nan.any(), "no owner waited: the forced give-up did not happen"
+    assert not nan.all(), "whole tiles and single-piece tiles must not be poisoned"
+    assert np.array_equal(got[~nan].view(np.uint32), expected[~nan].view(np.uint32))
+    with pytest.raises(nat.ConvRotNativeError, match="gave up"):
+        api.w4a4_status(dev)
+    api.w4a4_status(dev)  # the error word was cleared
+    tuning.set("sk_spin_limit", None)
+    for _ in range(2):
+        _assert_exact(run(), expected, f"tile {tile} after a failed launch")
+    api.w4a4_status(dev)

@@ -25,29 +25,29 @@ def _api():
 
 # name: (environment, images B, rows per image L, K, N, activation format)
 PATHS = {
-    "smallm_A": ({"CONVROT_W4A4_SMALLM_CFG": "A"}, 1, 7, 256, 196, "int8"),
-    "smallm_C": ({"CONVROT_GEMM_SMALLM_MAX": "64", "CONVROT_W4A4_SMALLM_CFG": "C"}, 2, 20, 384, 70, "int8"),
-    "dma_128x128": ({"CONVROT_GEMM_SMALLM_MAX": "0", "CONVROT_GEMM_TILE": "128x128w2x2", "CONVROT_GEMM_SK": "0"},
+    "smallm_A": ({"w4a4_smallm_cfg": "A"}, 1, 7, 256, 196, "int8"),
+    "smallm_C": ({"gemm_smallm_max": "64", "w4a4_smallm_cfg": "C"}, 2, 20, 384, 70, "int8"),
+    "dma_128x128": ({"gemm_smallm_max": "0", "gemm_tile": "128x128w2x2", "gemm_sk": "0"},
                     2, 150, 512, 200, "int8"),
-    "dma_256x256": ({"CONVROT_GEMM_SMALLM_MAX": "0", "CONVROT_GEMM_TILE": "256x256w2x4", "CONVROT_GEMM_SK": "0"},
+    "dma_256x256": ({"gemm_smallm_max": "0", "gemm_tile": "256x256w2x4", "gemm_sk": "0"},
                     3, 100, 384, 260, "int8"),
-    "dma_192x128": ({"CONVROT_GEMM_SMALLM_MAX": "0", "CONVROT_GEMM_TILE": "192x128w4x2", "CONVROT_GEMM_SK": "0"},
+    "dma_192x128": ({"gemm_smallm_max": "0", "gemm_tile": "192x128w4x2", "gemm_sk": "0"},
                     2, 150, 256, 136, "int8"),
-    "stream_k": ({"CONVROT_GEMM_SMALLM_MAX": "0", "CONVROT_GEMM_TILE": "128x256w2x4", "CONVROT_GEMM_SK": "1",
-                  "CONVROT_GEMM_SK_MIN": "1"}, 2, 130, 1024, 270, "int8"),
-    "register": ({"CONVROT_GEMM_SMALLM_MAX": "0", "CONVROT_GEMM_NO_DMA": "1"}, 2, 90, 256, 100, "int8"),
-    "packed": ({"CONVROT_GEMM_SMALLM_MAX": "0"}, 2, 90, 256, 102, "packed"),
+    "stream_k": ({"gemm_smallm_max": "0", "gemm_tile": "128x256w2x4", "gemm_sk": "1",
+                  "gemm_sk_min": "1"}, 2, 130, 1024, 270, "int8"),
+    "register": ({"gemm_smallm_max": "0", "gemm_no_dma": "1"}, 2, 90, 256, 100, "int8"),
+    "packed": ({"gemm_smallm_max": "0"}, 2, 90, 256, 102, "packed"),
     "packed_kernel": ({}, 2, 90, 256, 102, "packed_kernel"),
 }
-_ENV_KEYS = ("CONVROT_W4A4_SMALLM_CFG", "CONVROT_GEMM_SMALLM_MAX", "CONVROT_GEMM_TILE", "CONVROT_GEMM_SK",
-             "CONVROT_GEMM_SK_MIN", "CONVROT_GEMM_NO_DMA")
+_ENV_KEYS = ("w4a4_smallm_cfg", "gemm_smallm_max", "gemm_tile", "gemm_sk",
+             "gemm_sk_min", "gemm_no_dma")
 
 
-def _set_env(monkeypatch, env):
+def _set_env(tuning, env):
     for key in _ENV_KEYS:
-        monkeypatch.delenv(key, raising=False)
+        tuning.set(key, None)
     for key, value in env.items():
-        monkeypatch.setenv(key, value)
+        tuning.set(key, value)
 
 
 def _operands(orc, seed, M, K, N, dtype):
@@ -124,11 +124,11 @@ def _assert_exact(got, want, label):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
 @pytest.mark.parametrize("path", list(PATHS))
-def test_every_kernel_path(orc, dev, monkeypatch, path, dtype):
+def test_every_kernel_path(orc, dev, tuning, path, dtype):
     """Per-image gates ([B, 1, N]) on every W4A4 kernel; out of place, then in place."""
     api = _api()
     env, B, L, K, N, fmt = PATHS[path]
-    _set_env(monkeypatch, env)
+    _set_env(tuning, env)
     M = B * L
     rng, a, w, xs, ws, b, res, lin = _operands(orc, 101, M, K, N, dtype)
     gd, g, rpg = _gate(orc, rng, "per_image", B, L, N, dtype, dev)
@@ -148,10 +148,10 @@ def test_every_kernel_path(orc, dev, monkeypatch, path, dtype):
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
 @pytest.mark.parametrize("form", ["chunk", "odd_stride", "vector", "full", "none"])
 @pytest.mark.parametrize("path", ["smallm_A", "dma_128x128", "register"])
-def test_gate_forms(orc, dev, monkeypatch, path, form, dtype):
+def test_gate_forms(orc, dev, tuning, path, form, dtype):
     api = _api()
     env, B, L, K, N, fmt = PATHS[path]
-    _set_env(monkeypatch, env)
+    _set_env(tuning, env)
     M = B * L
     rng, a, w, xs, ws, b, res, lin = _operands(orc, 202, M, K, N, dtype)
     gd, g, rpg = _gate(orc, rng, form, B, L, N, dtype, dev)
@@ -231,13 +231,13 @@ def test_layer_forwards(orc, dev, backend):
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
 @pytest.mark.parametrize("cfg,B,L,K,N", [("A", 1, 5, 256, 200), ("B", 2, 4, 384, 70), ("C", 2, 20, 256, 136),
                                          ("F", 1, 40, 512, 96), ("T", 2, 100, 384, 260)])
-def test_w4a16_kernels(orc, dev, monkeypatch, cfg, B, L, K, N, dtype):
+def test_w4a16_kernels(orc, dev, tuning, cfg, B, L, K, N, dtype):
     """The W4A16 GEMM's gated-residual epilogue on each of its kernels (splits A, B, C, F and
     the tiled kernel, forced), per-image gates, ragged N: residual + gate * linear equals
     torch's composition on the same kernel's plain output, bit for bit, out of place and in
     place (the product itself is W4A16 arithmetic, checked against the oracle elsewhere)."""
     api = _api()
-    monkeypatch.setenv("CONVROT_W4A16_CFG", cfg)
+    tuning.set("w4a16_cfg", cfg)
     M = B * L
     rng = np.random.default_rng(303)
     act_dt = "float16" if dtype == "float16" else "bfloat16"
@@ -255,6 +255,40 @@ def test_w4a16_kernels(orc, dev, monkeypatch, cfg, B, L, K, N, dtype):
     want = res + gate * plain
     assert torch.equal(fused.reshape(B, L, N), want)
     assert torch.equal(api.hip_w4a16_matmul(act, wq, ws, b, residual=res, **kw).reshape(B, L, N), res + plain)
+    r2 = res.clone()
+    api.hip_w4a16_matmul(act, wq, ws, b, residual=r2, gate=gate, inplace=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(r2, want)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("gate_kind", ["per_image", "chunked"])
+def test_w4a16_tiled_vector_residual(orc, dev, tuning, dtype, gate_kind):
+    """The tiled W4A16 kernel's 16-byte residual and gate loads (N and the gate stride
+    multiples of 8): a per-image [B, 1, N] gate and a chunk of a [B, 1, 3N] modulation
+    output, out of place and in place, equal torch's composition on the plain output."""
+    api = _api()
+    tuning.set("w4a16_cfg", "T")
+    B, L, K, N = 2, 160, 384, 256
+    M = B * L
+    rng = np.random.default_rng(404)
+    act = to_dev(orc.from_f32(rng.normal(size=(M, K)).astype(np.float32), dtype), dtype, dev)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    wq = torch.from_numpy(orc.codes_to_cdna4(w)).to(dev)
+    ws = torch.from_numpy(rng.uniform(0.001, 0.01, size=N).astype(np.float32)).to(dev)
+    b = torch.from_numpy(rng.normal(size=N).astype(np.float32)).to(dev)
+    res = to_dev(orc.from_f32((rng.normal(size=(M, N)) * 4).astype(np.float32), dtype), dtype, dev).reshape(B, L, N)
+    if gate_kind == "per_image":
+        gate = to_dev(orc.from_f32(rng.normal(size=(B, N)).astype(np.float32), dtype), dtype, dev).reshape(B, 1, N)
+    else:
+        mod = to_dev(orc.from_f32(rng.normal(size=(B, 3 * N)).astype(np.float32), dtype), dtype, dev)
+        gate = mod[:, None, :].chunk(3, dim=-1)[2]
+    kw = dict(output_dtype=TORCH_DT[dtype], out_features=N)
+    plain = api.hip_w4a16_matmul(act, wq, ws, b, **kw).reshape(B, L, N)
+    want = res + gate * plain
+    fused = api.hip_w4a16_matmul(act, wq, ws, b, residual=res, gate=gate, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.reshape(B, L, N), want)
     r2 = res.clone()
     api.hip_w4a16_matmul(act, wq, ws, b, residual=r2, gate=gate, inplace=True, **kw)
     torch.cuda.synchronize()

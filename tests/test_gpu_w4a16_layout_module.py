@@ -67,12 +67,40 @@ def test_w4a16_config4(orc, dev, M, K, N):
     _w4a16_check(orc, dev, act, "bfloat16", w, ws, b, "bfloat16")
 
 
+@pytest.mark.parametrize("M", [1, 8, 32])
+@pytest.mark.parametrize("K,N", [(3072, 12288), (12288, 3072)])
+def test_w4a16_config4_complete_path(orc, dev, M, K, N):
+    """benchmark config 4 end to end through ConvRotLinear(backend="hip-w4a16"), G = 256:
+    the weight quantized by the prep kernel (codes and scales bit-exact), the activations
+    rotated by it (bit-exact against regular_hadamard), then the W4A16 GEMM within the
+    float32-order tolerance of the oracle product of the oracle's rotation."""
+    api = _api()
+    G = 256
+    x = outlier_input(M * 5 + K, (M, K), "bfloat16", orc)
+    w = outlier_input(K + N, (N, K), "bfloat16", orc, std=0.02, frac=0.01, factor=10.0)
+    bias = np.random.default_rng(K + N).normal(0.0, 0.02, size=N).astype(np.float32)
+    xd = to_dev(x, "bfloat16", dev)
+    qw, ws = api.quantize_convrot_weight(to_dev(w, "bfloat16", dev), G)
+    layer = api.ConvRotLinear(K, N, group_size=G, backend="hip-w4a16", device=dev)
+    layer.load_nk_weight(qw, ws, torch.from_numpy(bias).to(dev))
+    got = orc.to_f32(from_dev(layer(xd)), "bfloat16")
+    w_codes, wscales = orc.prepare_codes(w, "bfloat16", G)
+    assert np.array_equal(orc.unpack_signed_int4(from_dev(qw)), w_codes)
+    assert np.array_equal(from_dev(ws), wscales)
+    rot = orc.regular_hadamard(x, "bfloat16", G)
+    assert np.array_equal(from_dev(api.hip_fused_rotate_convrot_activation(xd, G)), rot)
+    ref, _, mag = orc.w4a16_matmul_codes(rot, "bfloat16", w_codes, wscales, bias, "float32")
+    tol = 2.0 ** -22 * K * mag * np.abs(wscales)[None, :] + np.abs(ref) * (2.0 ** -22 + 2.0 ** -8) + 1e-30
+    err = np.abs(got - ref)
+    assert (err <= tol).all(), f"max excess {np.max(err - tol)} (max err {err.max()})"
+
+
 @pytest.mark.parametrize("cfg", ["A", "B", "C", "F", "T"])
 @pytest.mark.parametrize("M,K,N", [(17, 96, 46), (37, 2688, 530), (1, 4000, 33), (5, 12288, 3072)])
-def test_w4a16_every_split(orc, dev, monkeypatch, cfg, M, K, N):
-    """Each W4A16 work split (forced through CONVROT_W4A16_CFG) on ragged M/N and on K that is
+def test_w4a16_every_split(orc, dev, tuning, cfg, M, K, N):
+    """Each W4A16 work split (forced through the w4a16_cfg tuning override) on ragged M/N and on K that is
     not a multiple of the 128-feature block (the tail features must read as zero)."""
-    monkeypatch.setenv("CONVROT_W4A16_CFG", cfg)
+    tuning.set("w4a16_cfg", cfg)
     rng = np.random.default_rng(M * 131 + K + N)
     w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
     ws = rng.uniform(0.001, 0.01, size=(N,)).astype(np.float32)
@@ -92,22 +120,22 @@ def _w4a16_tiled_case(orc, dev, act_dtype, out_dtype, M, K, N):
 
 @pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128"])
 @pytest.mark.parametrize("M,K,N", [(256, 128, 256), (300, 2688, 530), (1100, 4000, 2100), (129, 96, 8)])
-def test_w4a16_tiled(orc, dev, monkeypatch, tile, M, K, N):
-    """Every tile of the tiled kernel (M >= 128, forced through CONVROT_W4A16_TILE): partial
+def test_w4a16_tiled(orc, dev, tuning, tile, M, K, N):
+    """Every tile of the tiled kernel (M >= 128, forced through the w4a16_tile tuning override): partial
     tiles in M and N, K ending inside a 128-feature block, more tiles than the eight-way XCD
     interleave covers, and an incomplete group of four tile rows."""
-    monkeypatch.setenv("CONVROT_W4A16_CFG", "T")
-    monkeypatch.setenv("CONVROT_W4A16_TILE", tile)
+    tuning.set("w4a16_cfg", "T")
+    tuning.set("w4a16_tile", tile)
     _w4a16_tiled_case(orc, dev, "bfloat16", "bfloat16", M, K, N)
 
 
 @pytest.mark.parametrize("tile", ["256x256", "128x128"])
 @pytest.mark.parametrize("act_dtype,out_dtype", [("bfloat16", "float32"), ("float16", "float16"),
                                                   ("float16", "bfloat16"), ("float16", "float32")])
-def test_w4a16_tiled_dtypes(orc, dev, monkeypatch, tile, act_dtype, out_dtype):
+def test_w4a16_tiled_dtypes(orc, dev, tuning, tile, act_dtype, out_dtype):
     """Activation and output dtypes of the tiled kernel on a ragged shape."""
-    monkeypatch.setenv("CONVROT_W4A16_CFG", "T")
-    monkeypatch.setenv("CONVROT_W4A16_TILE", tile)
+    tuning.set("w4a16_cfg", "T")
+    tuning.set("w4a16_tile", tile)
     _w4a16_tiled_case(orc, dev, act_dtype, out_dtype, 300, 2688, 530)
 
 
@@ -245,15 +273,15 @@ def _many_tokens_case(orc, K, N):
 
 
 @pytest.mark.parametrize("cfg", [None, "T", "F"], ids=["auto", "tiled", "split"])
-def test_w4a16_layer_many_tokens(orc, dev, monkeypatch, cfg):
+def test_w4a16_layer_many_tokens(orc, dev, tuning, cfg):
     """ConvRotLinear (hip-w4a16) at 512 tokens, 1024 -> 3072, G=64: the automatic dispatch
     (the tiled kernel at this size) and each kernel forced, against the oracle."""
     api = _api()
     if cfg is None:
-        monkeypatch.delenv("CONVROT_W4A16_CFG", raising=False)
+        tuning.set("w4a16_cfg", None)
     else:
-        monkeypatch.setenv("CONVROT_W4A16_CFG", cfg)
-    monkeypatch.delenv("CONVROT_W4A16_TILE", raising=False)
+        tuning.set("w4a16_cfg", cfg)
+    tuning.set("w4a16_tile", None)
     K, N = 1024, 3072
     dense_w, dense_b, values, ws, ref, mag = _many_tokens_case(orc, K, N)
     qweight, wscales = api.quantize_convrot_weight(to_dev(dense_w, "bfloat16", dev), 64)

@@ -311,6 +311,32 @@ def test_w4a4_epilogue_order(orc):
     assert np.abs(out - fused).max() < 1e-5
 
 
+@pytest.mark.parametrize("out_dtype", ["float32", "bfloat16", "float16"])
+def test_w4a4_large_path_equals_int64_path(orc, out_dtype):
+    """The full-size checker (float32 BLAS dots + C epilogue) equals the int64 oracle bit for
+    bit, including extreme codes (-8 everywhere at K = 15360: |dot| = 64 K, the largest the
+    float32 argument allows) and a ragged slab boundary."""
+    rng = np.random.default_rng(29)
+    a = rng.integers(-8, 8, size=(67, 2688), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(53, 2688), dtype=np.int8)
+    xs = rng.uniform(0.001, 0.2, size=(67,)).astype(np.float32)
+    ws = rng.uniform(0.001, 0.2, size=(53,)).astype(np.float32)
+    b = rng.normal(size=(53,)).astype(np.float32)
+    want = orc.w4a4_matmul_codes(a, w, xs, ws, b, out_dtype)
+    got = orc.w4a4_matmul_codes_large(a, w, xs, ws, b, out_dtype)
+    assert np.array_equal(got.view(np.uint32) if out_dtype == "float32" else got,
+                          want.view(np.uint32) if out_dtype == "float32" else want)
+    K = 15360
+    a8 = np.full((3, K), -8, np.int8)
+    w8 = np.full((2, K), -8, np.int8)
+    w8[1, ::2] = 7
+    dots = orc.w4a4_dots_exact(a8, w8)
+    assert np.array_equal(dots, a8.astype(np.int64) @ w8.astype(np.int64).T)
+    # a dropped term (one code zeroed) must show in the dots
+    a8[0, 5] = 0
+    assert orc.w4a4_dots_exact(a8, w8)[0, 0] == 64 * K - 64
+
+
 def test_w4a4_bf16_output_is_rounded_float32(orc):
     rng = np.random.default_rng(27)
     a = rng.integers(-7, 8, size=(31, 1024), dtype=np.int8)
