@@ -235,7 +235,7 @@ def main() -> int:
             "pct_int8_peak": round(100.0 * tops / INT8_PEAK_TOPS, 2),
         },
         "roofline": {
-            "kernel": "W4A4 GEMM (w4a4_gemm_dma_kernel / w4a4_gemm_sk_kernel: INT8 MFMA + fused epilogue)",
+            "kernel": "W4A4 GEMM (w4a4_gemm_agpr_kernel, 288x192 and 256x256 tiles: INT8 MFMA + fused epilogue)",
             "bound": "mfma",
             "achieved": round(float(gemm_agg), 2),
             "peak": INT8_PEAK_TOPS,

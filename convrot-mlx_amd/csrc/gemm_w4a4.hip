@@ -327,15 +327,20 @@ __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], u
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    constexpr int CPR = TN / 8;        // 16-byte chunks per row
-    constexpr int RPI = 64 / CPR;      // rows per wave instruction
-    constexpr int NIT = TM / RPI;      // write-back iterations
-    const int cr = lane / CPR, cc = lane % CPR;
-    const int n = nw + cc * 8;
-    const bool vec = (N & 7) == 0 && n + 8 <= N;
+    // Write-back: the tile's TM x CPR 16-byte chunks, 64 per wave
+    // instruction; chunk c = 64 it + lane is row c / CPR, chunk c % CPR of it.
+    constexpr int CPR = TN / 8;                 // 16-byte chunks per row
+    constexpr int NIT = (TM * CPR + 63) / 64;   // write-back iterations
+    constexpr bool kWhole = (TM * CPR) % 64 == 0;
+    auto row_of = [&](int it) { return (it * 64 + lane) / CPR; };
+    auto col_of = [&](int it) { return nw + ((it * 64 + lane) % CPR) * 8; };
+    auto live = [&](int it) {
+      return (kWhole || it * 64 + lane < TM * CPR) && mw + row_of(it) < M && col_of(it) < N;
+    };
     auto store_row = [&](int it, uint4 v) {
-      uint16_t* dst = (uint16_t*)out + (int64_t)(mw + it * RPI + cr) * N + n;
-      if (vec) {
+      const int n = col_of(it);
+      uint16_t* dst = (uint16_t*)out + (int64_t)(mw + row_of(it)) * N + n;
+      if ((N & 7) == 0 && n + 8 <= N) {
         *(uint4*)dst = v;
       } else {
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -344,32 +349,33 @@ __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], u
           if (n + j < N) dst[j] = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
       }
     };
+    auto staged = [&](int it) {
+      return *(const uint4*)(region + row_of(it) * RS + ((it * 64 + lane) % CPR) * 16);
+    };
     if (!gr.residual) {
 #pragma unroll
-      for (int it = 0; it < NIT; ++it) {
-        const int rl = it * RPI + cr;
-        if (mw + rl >= M || n >= N) continue;
-        store_row(it, *(const uint4*)(region + rl * RS + cc * 16));
-      }
+      for (int it = 0; it < NIT; ++it)
+        if (live(it)) store_row(it, staged(it));
     } else {
       // Residual and gate loads of BATCH rows go out before their stores (a
       // load cannot be moved above a store that may alias it, so one row at a
       // time would wait a memory round trip per row).
       constexpr int BATCH = NIT < 8 ? NIT : 8;
-      static_assert(NIT % BATCH == 0, "write-back batches");
 #pragma unroll
       for (int b0 = 0; b0 < NIT; b0 += BATCH) {
         Gated8 ops[BATCH];
 #pragma unroll
         for (int i = 0; i < BATCH; ++i) {
-          const int m = mw + (b0 + i) * RPI + cr;
-          if (m < M && n < N) gate_load8<ODT>(gr, m, n, N, vec, ops[i]);
+          const int it = b0 + i;
+          if (it < NIT && live(it)) {
+            const int n = col_of(it);
+            gate_load8<ODT>(gr, mw + row_of(it), n, N, (N & 7) == 0 && n + 8 <= N, ops[i]);
+          }
         }
 #pragma unroll
         for (int i = 0; i < BATCH; ++i) {
-          const int rl = (b0 + i) * RPI + cr;
-          if (mw + rl >= M || n >= N) continue;
-          store_row(b0 + i, gate_apply8<ODT>(ops[i], *(const uint4*)(region + rl * RS + cc * 16)));
+          const int it = b0 + i;
+          if (it < NIT && live(it)) store_row(it, gate_apply8<ODT>(ops[i], staged(it)));
         }
       }
     }
@@ -418,12 +424,14 @@ __device__ __forceinline__ void mfma_agpr(i32x4& c, const i32x4& b, const i32x4&
   asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(b), "v"(a) : "memory");
 }
 
-// Two wait states after the VALU writes of the eight unpacked weight operands,
-// ordered before the MFMAs that read them.
-__device__ __forceinline__ void hazard_pad(const i32x4 (&w)[8]) {
-  asm volatile("s_nop 1" ::"v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]),
-               "v"(w[7])
-               : "memory");
+// Two wait states after the VALU writes of the unpacked weight operands,
+// ordered before the MFMAs that read them (the empty asms tie every operand
+// to the padding).
+template <int FN>
+__device__ __forceinline__ void hazard_pad(const i32x4 (&w)[FN]) {
+#pragma unroll
+  for (int i = 0; i < FN; ++i) asm volatile("" ::"v"(w[i]) : "memory");
+  asm volatile("s_nop 1" ::: "memory");
 }
 
 // Wait states between the last MFMA and any read of its accumulators (more
@@ -450,10 +458,13 @@ struct DmaEngine {
   static constexpr int LOADS = A_FRAGS + B_FRAGS;
   static constexpr int STAGE_BYTES = LOADS * 1024;
   // Epilogue operands of the tile, loaded into LDS with the first k-blocks:
-  // xs[m0 .. m0+255], ws[n0 .. n0+255], bias[n0 .. n0+255] (1 KB each).
+  // xs[m0 .. m0+BM), ws[n0 .. n0+BN), bias[n0 .. n0+BN), each in whole
+  // 256-byte dword DMAs (64 floats).
+  static constexpr int XS_DMAS = (BM * 4 + 255) / 256, WS_DMAS = (BN * 4 + 255) / 256;
+  static constexpr int EPI_DMAS = XS_DMAS + 2 * WS_DMAS;
   static constexpr int EPI_OFF = STAGES * STAGE_BYTES;
-  static constexpr int EPI_BYTES = 3 * 1024;
-  static constexpr int EPI_DMAS = 3 * 4;  // 256-byte dword DMAs
+  static constexpr int WS_OFF = EPI_OFF + XS_DMAS * 256, BIAS_OFF = WS_OFF + WS_DMAS * 256;
+  static constexpr int EPI_BYTES = EPI_DMAS * 256;
   static constexpr int SMEM_BYTES = EPI_OFF + EPI_BYTES;
   static constexpr int LPW = LOADS / NW;  // DMA instructions per wave per k-block
   static constexpr int APW = A_FRAGS / NW, BPW = B_FRAGS / NW;  // of which activation / weight
@@ -462,7 +473,7 @@ struct DmaEngine {
   static_assert(LOADS % NW == 0, "fragment loads must split evenly over waves");
   static_assert(A_FRAGS % NW == 0 && B_FRAGS % NW == 0, "each wave loads APW + BPW pieces");
   static_assert(NW * STAGING <= EPI_OFF, "epilogue staging exceeds the ring");
-  static_assert(BM <= 256 && BN <= 256, "one KB of LDS per epilogue operand");
+  static_assert(SMEM_BYTES <= 160 * 1024, "LDS of one CU");
   static_assert(STAGES >= 3 && (STAGES - 1) * LPW <= 63, "ring depth: vmcnt counts at most 63 DMAs");
 
   // Fragments of one k-block held in registers: packed weights (both k-steps)
@@ -496,23 +507,25 @@ struct DmaEngine {
 
   __device__ __forceinline__ uint8_t* staging() const { return smem + wave * STAGING; }
   __device__ __forceinline__ const float* epi_xs() const { return (const float*)(smem + EPI_OFF); }
-  __device__ __forceinline__ const float* epi_ws() const { return (const float*)(smem + EPI_OFF + 1024); }
-  __device__ __forceinline__ const float* epi_bias() const { return (const float*)(smem + EPI_OFF + 2048); }
+  __device__ __forceinline__ const float* epi_ws() const { return (const float*)(smem + WS_OFF); }
+  __device__ __forceinline__ const float* epi_bias() const { return (const float*)(smem + BIAS_OFF); }
 
-  // Load the tile's epilogue operands into LDS: 12 dword DMAs of 256 bytes,
-  // DMA d by wave d % NW.  Entries past M or N, and all of a missing
+  // Load the tile's epilogue operands into LDS: EPI_DMAS dword DMAs of 256
+  // bytes, DMA d by wave d % NW.  Entries past M or N, and all of a missing
   // bias, read as zero.  Issued before the run's prologue: vmcnt retires in
   // issue order, so the run's first DMA wait also retires these, and the
   // barrier after the run publishes them to every wave.  The area must not be
   // read by a previous epilogue when they are issued.
   __device__ __forceinline__ void issue_epi(const float* xscales, const float* wscales, const float* bias, int M,
                                             int N, int m0, int n0) {
-    for (int d = wave; d < EPI_DMAS; d += NW) {  // array d / 4, quarter d % 4
-      const int arr = d >> 2;
+    for (int d = wave; d < EPI_DMAS; d += NW) {  // array arr, 256-byte piece q of it
+      const int arr = d < XS_DMAS ? 0 : d < XS_DMAS + WS_DMAS ? 1 : 2;
+      const int q = d - (arr == 0 ? 0 : arr == 1 ? XS_DMAS : XS_DMAS + WS_DMAS);
+      const int off = arr == 0 ? EPI_OFF : arr == 1 ? WS_OFF : BIAS_OFF;
       const float* base = arr == 0 ? xscales + m0 : arr == 1 ? wscales + n0 : (bias ? bias + n0 : wscales);
       const int count = arr == 0 ? M - m0 : (arr == 1 || bias) ? N - n0 : 0;
       const i32x4_sgpr r = buffer_rsrc(base, (uint32_t)count * 4u);
-      dma4(r, (uint32_t)((d & 3) * 256 + lane * 4), smem_addr + (uint32_t)(EPI_OFF + arr * 1024 + (d & 3) * 256));
+      dma4(r, (uint32_t)(q * 256 + lane * 4), smem_addr + (uint32_t)(off + q * 256));
     }
   }
 
@@ -613,22 +626,24 @@ struct DmaEngine {
     else body(kb0, n, acc, flag, tag);
   }
 
-  // ---- kAgpr: the 4-wave 256x256 tile, 128x128 per wave (FN = FM = 8)
+  // ---- kAgpr: the 4-wave tiles, one wave per SIMD, FN x FM accumulator
+  //      fragments per wave in the AGPRs (256x256: 8 x 8; 288x192: 6 x 9)
   //
   // Per k-block i (two 64-feature k-steps):
-  //   k-step 0: 64 MFMAs on (w0, a0); between them the wave reads a1 (its
+  //   k-step 0: FM*FN MFMAs on (w0, a0); between them the wave reads a1 (its
   //             k-step-1 activation fragments) and unpacks w1 from bp;
   //   middle:   the wave's DMAs of block i+1 have landed and its a1 reads are
   //             done; a barrier publishes block i+1 to every wave and frees
   //             block i's ring stage, which the DMA of block i+STAGES refills;
-  //   k-step 1: 64 MFMAs on (w1, a1); between them the wave reads block i+1's
-  //             packed weights bp and k-step-0 fragments a0, and unpacks w0.
+  //   k-step 1: FM*FN MFMAs on (w1, a1); between them the wave reads block
+  //             i+1's packed weights bp and k-step-0 fragments a0, and unpacks
+  //             w0.
   // So the MFMA pipe never waits for a whole block's reads, and the only
   // workgroup barrier of a block sits between its two k-steps.
-  __device__ __forceinline__ void read_bp(int stage, uint4 (&bp)[8], int fn0, int cnt) const {
+  __device__ __forceinline__ void read_bp(int stage, uint4 (&bp)[FN]) const {
     const uint8_t* sb = smem + stage * STAGE_BYTES + (A_FRAGS + wn * FN) * 1024 + lane * 16;
 #pragma unroll
-    for (int fn = fn0; fn < fn0 + cnt; ++fn) bp[fn] = *(const uint4*)(sb + fn * 1024);
+    for (int fn = 0; fn < FN; ++fn) bp[fn] = *(const uint4*)(sb + fn * 1024);
   }
   __device__ __forceinline__ const uint8_t* a_base(int stage, int ks) const {
     const int r = lane & 15;
@@ -673,56 +688,58 @@ struct DmaEngine {
   // wave issues about one instruction per four cycles, so LDS reads, weight
   // unpacks and DMA issues placed one or two at a time between MFMAs (16
   // cycles each) run in the MFMA's shadow, where a burst of them would leave
-  // the MFMA pipe idle.  Slot t follows MFMA t = 8 * fm + fn.
-  //
-  // k-step 0 of the block in ring stage st: MFMAs on (w0, a0); reads of a1
-  // after slots 1, 5, .., 29 and the halves of the unpack of w1 after slots
-  // 3, 7, .., 63.
-  __device__ __forceinline__ void agpr_kstep0(int st, const uint4 (&bp)[8], const i32x4 (&a0)[8], i32x4 (&a1)[8],
-                                              const i32x4 (&w0)[8], i32x4 (&w1)[8], i32x4 (&acc)[FN][FM]) const {
+  // the MFMA pipe idle.  Slot t follows MFMA t = FN * fm + fn.
+  static constexpr int kSlots = FM * FN;
+
+  // k-step 0 of the block in ring stage st: MFMAs on (w0, a0); read of a1[i]
+  // after slot 4i + 1 and half j of the unpack of w1 after slot 4j + 3.
+  __device__ __forceinline__ void agpr_kstep0(int st, const uint4 (&bp)[FN], const i32x4 (&a0)[FM],
+                                              i32x4 (&a1)[FM], const i32x4 (&w0)[FN], i32x4 (&w1)[FN],
+                                              i32x4 (&acc)[FN][FM]) const {
     hazard_pad(w0);
     const uint8_t* sa = a_base(st, 1);
-    uint32_t u[8][4];
+    uint32_t u[FN][4];
 #pragma unroll
-    for (int t = 0; t < 64; ++t) {
-      const int fm = t / 8, fn = t % 8;
+    for (int t = 0; t < kSlots; ++t) {
+      const int fm = t / FN, fn = t % FN;
       mfma_agpr(acc[fn][fm], w0[fn], a0[fm]);
-      if (t % 4 == 1 && t < 32) a1[t / 4] = *(const i32x4*)(sa + (t / 4) * 2048);
-      if (t % 4 == 3) {
+      if (t % 4 == 1 && t / 4 < FM) a1[t / 4] = *(const i32x4*)(sa + (t / 4) * 2048);
+      if (t % 4 == 3 && t / 4 < 2 * FN) {
         const int j = t / 8, h = (t / 4) % 2;
         unpack_half(h ? bp[j].w : bp[j].z, u[j][2 * h], u[j][2 * h + 1]);
       }
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) w1[j] = (i32x4){(int)u[j][0], (int)u[j][1], (int)u[j][2], (int)u[j][3]};
+    for (int j = 0; j < FN; ++j) w1[j] = (i32x4){(int)u[j][0], (int)u[j][1], (int)u[j][2], (int)u[j][3]};
   }
 
-  // k-step 1: MFMAs on (w1, a1); reads of the next block's bp (after slots
-  // 0, 2, .., 14) and a0 (after slots 16, 18, .., 30) from ring stage nst, the
-  // 12 DMA pieces of k-block dma_kb into stage st (after slots 1, 5, .., 45),
-  // and the halves of the unpack of the next w0 (after slots 33, 35, .., 63).
-  __device__ __forceinline__ void agpr_kstep1(int st, int nst, int dma_kb, uint4 (&bp)[8], i32x4 (&a0)[8],
-                                              const i32x4 (&a1)[8], i32x4 (&w0)[8], const i32x4 (&w1)[8],
+  // k-step 1: MFMAs on (w1, a1); from ring stage nst, reads of the next
+  // block's bp[i] after slot 2i and a0[i] after slot 2 FN + 2i; the LPW DMA
+  // pieces of k-block dma_kb into stage st after slots 1, 5, 9, ..; half j of
+  // the unpack of the next w0 after slot 2 (FN + FM) + 1 + 2j.
+  __device__ __forceinline__ void agpr_kstep1(int st, int nst, int dma_kb, uint4 (&bp)[FN], i32x4 (&a0)[FM],
+                                              const i32x4 (&a1)[FM], i32x4 (&w0)[FN], const i32x4 (&w1)[FN],
                                               i32x4 (&acc)[FN][FM]) {
-    static_assert(LPW == 12, "12 DMA pieces per k-block");
+    constexpr int U0 = 2 * (FN + FM) + 1;
     hazard_pad(w1);
     const uint8_t* sa = a_base(nst, 0);
     const uint8_t* sb = smem + nst * STAGE_BYTES + (A_FRAGS + wn * FN) * 1024 + lane * 16;
-    uint32_t u[8][4];
+    uint32_t u[FN][4];
 #pragma unroll
-    for (int t = 0; t < 64; ++t) {
-      const int fm = t / 8, fn = t % 8;
+    for (int t = 0; t < kSlots; ++t) {
+      const int fm = t / FN, fn = t % FN;
       mfma_agpr(acc[fn][fm], w1[fn], a1[fm]);
-      if (t % 2 == 0 && t < 16) bp[t / 2] = *(const uint4*)(sb + (t / 2) * 1024);
-      if (t % 2 == 0 && t >= 16 && t < 32) a0[(t - 16) / 2] = *(const i32x4*)(sa + ((t - 16) / 2) * 2048);
-      if (t % 4 == 1 && t < 48) issue_piece(dma_kb, st, t / 4);
-      if (t % 2 == 1 && t >= 33) {
-        const int k = (t - 33) / 2, j = k / 2, h = k % 2;
+      if (t % 2 == 0 && t < 2 * FN) bp[t / 2] = *(const uint4*)(sb + (t / 2) * 1024);
+      if (t % 2 == 0 && t >= 2 * FN && t < 2 * (FN + FM))
+        a0[(t - 2 * FN) / 2] = *(const i32x4*)(sa + ((t - 2 * FN) / 2) * 2048);
+      if (t % 4 == 1 && t / 4 < LPW) issue_piece(dma_kb, st, t / 4);
+      if (t >= U0 && (t - U0) % 2 == 0 && (t - U0) / 2 < 2 * FN) {
+        const int k = (t - U0) / 2, j = k / 2, h = k % 2;
         unpack_half(h ? bp[j].y : bp[j].x, u[j][2 * h], u[j][2 * h + 1]);
       }
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) w0[j] = (i32x4){(int)u[j][0], (int)u[j][1], (int)u[j][2], (int)u[j][3]};
+    for (int j = 0; j < FN; ++j) w0[j] = (i32x4){(int)u[j][0], (int)u[j][1], (int)u[j][2], (int)u[j][3]};
   }
 
   // The k-loop runs one branch-free body per block, so the accumulators keep
@@ -731,20 +748,23 @@ struct DmaEngine {
   // last k-block re-fetch that last block (in range) into stages no later
   // block uses.  Two DMA groups are therefore in flight at every middle wait.
   __device__ __forceinline__ void body_agpr(int kb0, int n, i32x4 (&acc)[FN][FM], int* flag, int tag) {
-    static_assert(FN == 8 && FM == 8 && NW == 4 && STAGES == 3, "kAgpr is the 4-wave 256x256 tile, 3 stages");
-    uint4 bp[8];
-    i32x4 a0[8], a1[8], w0[8], w1[8];
+    static_assert(NW == 4 && STAGES == 3, "kAgpr: 4 waves, 3 stages");
+    static_assert(4 * (FM > 2 * FN ? FM : 2 * FN) <= kSlots, "k-step 0 fillers: one per four slots");
+    static_assert(2 * (FN + FM) + 2 * (2 * FN) - 1 <= kSlots && 4 * LPW - 3 <= kSlots,
+                  "k-step 1 fillers: reads, DMA pieces and unpacks");
+    uint4 bp[FN];
+    i32x4 a0[FM], a1[FM], w0[FN], w1[FN];
     wait_vmcnt<2 * LPW>();  // block 0 (and the epilogue operands) landed
     if (flag && lane == 0) __hip_atomic_store(flag, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_barrier();
-    read_bp(0, bp, 0, 8);
+    read_bp(0, bp);
     {
       const uint8_t* sa = a_base(0, 0);
 #pragma unroll
-      for (int fm = 0; fm < 8; ++fm) a0[fm] = *(const i32x4*)(sa + fm * 2048);
+      for (int fm = 0; fm < FM; ++fm) a0[fm] = *(const i32x4*)(sa + fm * 2048);
     }
 #pragma unroll
-    for (int fn = 0; fn < 8; ++fn) unpack(bp[fn], 0, w0[fn]);
+    for (int fn = 0; fn < FN; ++fn) unpack(bp[fn], 0, w0[fn]);
     const int last_kb = kb0 + n - 1;
     int st = 0;
     for (int i = 0; i < n; ++i) {
@@ -881,15 +901,15 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_dma_kernel(
                                               N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, gr, m0, n0);
 }
 
-// The kAgpr 4-wave 256x256 tile, one workgroup per output tile: one wave per
-// SIMD may use all 512 registers (256 VGPRs + the 256 AGPRs of the
-// accumulator).
-template <int STAGES, int ODT>
+// The kAgpr 4-wave tiles (256x256, 288x192), one workgroup per output tile:
+// one wave per SIMD may use all 512 registers (256 VGPRs + the 256 AGPRs of
+// the accumulator).
+template <int BM, int BN, int STAGES, int ODT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void w4a4_gemm_agpr_kernel(
     const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
     int K, int nblocks, int kblocks, int tiles_m, int tiles_n, GatedResidual gr) {
-  using E = DmaEngine<256, 256, 2, 2, kAgpr, STAGES>;
+  using E = DmaEngine<BM, BN, 2, 2, kAgpr, STAGES>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
   E e(smem);
 
@@ -898,7 +918,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int per_xcd = tiles / kXcds;
   if (logical < per_xcd * kXcds) logical = (logical % kXcds) * per_xcd + logical / kXcds;
   int m0, n0;
-  tile_origin(logical, tiles_m, tiles_n, 256, 256, m0, n0);
+  tile_origin(logical, tiles_m, tiles_n, BM, BN, m0, n0);
 
   e.set_tile(act, wq, M, K, nblocks, kblocks, m0, n0);
   e.issue_epi(xscales, wscales, bias, M, N, m0, n0);
@@ -1263,27 +1283,36 @@ namespace {
 // 8-wave 256x256 tile on every FLUX shape at M = 1536 and 4608.  The 8-wave
 // tile moves half the L2 bytes per MFMA of 128x128 but runs one workgroup per
 // CU; 128x128 fits two per CU.  `sk` marks the tiles the stream-K kernel runs
-// well: the 8-wave 256x256 one spills registers inside its k-loop there and
-// 128x128 pieces are too short.
+// well: the 8-wave 256x256 one spills registers inside its k-loop there,
+// 128x128 pieces are too short, and the 4-wave 256x256 stream-K kernel ran
+// 1.4-2.8x slower than the data-parallel one on every FLUX shape timed
+// (M = 1024 .. 4608), and 2x slower than 128x256 stream-K at 1536x12288->3072.
 //
 // The 192x128 tile moves more L2 bytes per MFMA than the 256x256 ones and
 // sustains 0.69 of the 4-wave tile's rate with every CU busy, but 0.77 when
 // its grid is a single round that leaves CUs idle (1536 tokens: 192 tiles at
 // N = 3072).
+//
+// The 4-wave 288x192 tile (6 x 9 fragments per wave, data-parallel only) moves
+// the same 48 KB per k-block as 256x256 for 0.84 of its MFMAs; at 4608 tokens
+// its grid is exactly one workgroup per CU for every N multiple of 3072/16,
+// where 256x256 leaves 40 CUs idle (N = 3072) or a 3/8-full last round.
 struct Cand {
   Tile t;
   int per_cu;
   double eff;
   double eff_partial;  // eff when the grid is one round of fewer tiles than CUs
   bool sk;
-  bool dma_only;  // no register-staged (packed-activation) variant
+  bool dma_only;   // no register-staged (packed-activation) variant
+  bool no_sk = false;  // no stream-K kernel
 };
-constexpr Cand kCands[6] = {{{256, 256, 2, 2, 3}, 1, 1.0, 1.0, true, true},
+constexpr Cand kCands[7] = {{{256, 256, 2, 2, 3}, 1, 1.0, 1.0, false, true},
                             {{256, 256, 2, 4, 3}, 1, 0.92, 0.92, false, false},
                             {{128, 256, 2, 4, 4}, 1, 0.79, 0.79, true, false},
                             {{256, 128, 4, 2, 3}, 1, 0.74, 0.74, true, false},
                             {{128, 128, 2, 2, 3}, 2, 0.74, 0.74, false, false},
-                            {{192, 128, 4, 2, 3}, 1, 0.69, 0.77, false, true}};
+                            {{192, 128, 4, 2, 3}, 1, 0.69, 0.77, false, true},
+                            {{288, 192, 2, 2, 3}, 1, 0.94, 0.94, false, true, true}};
 // Fixed cost of the stream-K fix-up (ticket, partial store and reload, the
 // extra pipeline ramp of each piece, the idle tail while owners wait), in
 // units of one 256x256 k-block; fitted to M = 512 .. 4608 FLUX shapes.
@@ -1354,7 +1383,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_dma, size_t ws_byte
     const double td = dp_time(c, tiles, kb, cus);
     const double ts = sk_time(c, tiles, kb, cus, min_iters);
     const int grid = std::min(kSkMaxGrid, cus * c.per_cu) / kXcds * kXcds;
-    const bool sk = grid >= kXcds && sk_bytes(c.t, grid) <= ws_bytes &&
+    const bool sk = !c.no_sk && grid >= kXcds && sk_bytes(c.t, grid) <= ws_bytes &&
                     (force_sk == 1 || (force_sk == -1 && c.sk && ts < td));
     const double tt = sk ? ts : td;
     if (tt < best_time * (1.0 - 1e-9)) {
@@ -1423,30 +1452,34 @@ hipError_t launch_dma(const Plan& plan, const void* act, const float* xs, const 
   const int spin = tuning(kTuneSkSpinLimit);
   const SkArgs ska{wsp.ptr, plan.min_iters, spin >= 0 ? spin : kSkSpinLimit};
   const bool sk = plan.sk && wsp.ptr && wsp.bytes >= sk_bytes(plan.t, plan.grid);
-  if constexpr (BM == 256 && BN == 256 && WM * WN == 4) {
-    if (sk)
-      hipLaunchKernelGGL((w4a4_gemm_agpr_sk_kernel<STAGES, ODT>), dim3((unsigned)plan.grid), dim3(256), 0, stream,
-                         (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, tm,
-                         tn, ska, gr);
-    else
-      hipLaunchKernelGGL((w4a4_gemm_agpr_kernel<STAGES, ODT>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream,
-                         (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, tm,
-                         tn, gr);
+  if constexpr (WM * WN == 4 && ((BM == 256 && BN == 256) || (BM == 288 && BN == 192))) {
+    if constexpr (BM == 256) {
+      if (sk) {
+        hipLaunchKernelGGL((w4a4_gemm_agpr_sk_kernel<STAGES, ODT>), dim3((unsigned)plan.grid), dim3(256), 0, stream,
+                           (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, tm,
+                           tn, ska, gr);
+        return hipGetLastError();
+      }
+    }
+    hipLaunchKernelGGL((w4a4_gemm_agpr_kernel<BM, BN, STAGES, ODT>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream,
+                       (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, tm, tn,
+                       gr);
     return hipGetLastError();
-  }
-  // Double-buffered fragments except on the 8-wave 256x256 tile, whose
-  // 128-register accumulator leaves no room for a second set.
-  constexpr int kPP = (BM == 256 && BN == 256) ? kSingle : kPingPong;
-  if (sk) {
-    hipLaunchKernelGGL((w4a4_gemm_sk_kernel<BM, BN, WM, WN, kPP, STAGES, ODT>), dim3((unsigned)plan.grid),
+  } else {
+    // Double-buffered fragments except on the 8-wave 256x256 tile, whose
+    // 128-register accumulator leaves no room for a second set.
+    constexpr int kPP = (BM == 256 && BN == 256) ? kSingle : kPingPong;
+    if (sk) {
+      hipLaunchKernelGGL((w4a4_gemm_sk_kernel<BM, BN, WM, WN, kPP, STAGES, ODT>), dim3((unsigned)plan.grid),
+                         dim3(WM * WN * 64), 0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N,
+                         (int)K, nblocks, kblocks, tm, tn, ska, gr);
+      return hipGetLastError();
+    }
+    hipLaunchKernelGGL((w4a4_gemm_dma_kernel<BM, BN, WM, WN, kPP, STAGES, ODT>), dim3((unsigned)(tm * tn)),
                        dim3(WM * WN * 64), 0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N,
-                       (int)K, nblocks, kblocks, tm, tn, ska, gr);
+                       (int)K, nblocks, kblocks, tm, tn, gr);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((w4a4_gemm_dma_kernel<BM, BN, WM, WN, kPP, STAGES, ODT>), dim3((unsigned)(tm * tn)), dim3(WM * WN * 64),
-                     0, stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks,
-                     tm, tn, gr);
-  return hipGetLastError();
 }
 
 template <bool APACK, int ODT>
@@ -1471,6 +1504,7 @@ hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const f
     CONVROT_DMA(128, 256, 2, 4, 4)
     CONVROT_DMA(128, 128, 2, 2, 3)
     CONVROT_DMA(192, 128, 4, 2, 3)
+    CONVROT_DMA(288, 192, 2, 2, 3)
 #undef CONVROT_DMA
   }
 #define CONVROT_TILE(BM_, BN_, WM_, WN_)                    \
@@ -1504,6 +1538,20 @@ constexpr int64_t kSmallMMax = 32;
 constexpr int64_t kSmallMMaxWide = 64;
 constexpr int64_t kSmallMWideElems = 40000000;  // N * K, i.e. 20 MB of int4 weights
 
+namespace {
+
+// Largest M the few-row weight-streaming kernel takes (same results bit for
+// bit).  It wins up to M = 32 everywhere measured, and up to 64 while the int4
+// weight is at most ~20 MB (beyond that the tiled kernel's 16-17 us floor is
+// lower).  The gemm_smallm_max tuning override sets it (0: never).
+int64_t smallm_limit(int64_t N, int64_t K) {
+  int64_t small_max = N * K <= kSmallMWideElems ? kSmallMMaxWide : kSmallMMax;
+  if (const int v = tuning(kTuneGemmSmallmMax); v >= 0) small_max = v;
+  return small_max;
+}
+
+}  // namespace
+
 hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
                             const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
                             void* out, int out_dtype, hipStream_t stream, const GatedResidual& gr,
@@ -1511,13 +1559,7 @@ hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscale
   if (M == 0 || N == 0) return hipSuccess;
   if (act_format == CONVROT_ACT_PACKED)
     return launch_odt<true>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, gr, src, stream);
-  // Few rows: the weight-streaming kernel (same results bit for bit).  It
-  // wins up to M = 32 everywhere measured, and up to 64 while the int4 weight
-  // is at most ~20 MB (beyond that the tiled kernel's 16-17 us floor is lower).
-  // The gemm_smallm_max tuning override sets the largest M it takes (0: never).
-  int64_t small_max = N * K <= kSmallMWideElems ? kSmallMMaxWide : kSmallMMax;
-  if (const int v = tuning(kTuneGemmSmallmMax); v >= 0) small_max = v;
-  if (M <= small_max)
+  if (M <= smallm_limit(N, K))
     return launch_w4a4_smallm((const int8_t*)act, xscales, qweight, wscales, bias, M, N, K, out, out_dtype, stream,
                               gr);
   return launch_odt<false>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, gr, src, stream);

@@ -122,7 +122,7 @@ def test_odd_shapes_bf16(orc, dev, seed, M, K, N):
 # Tiles the automatic choice picks (BMxBN, waves WMxWN), plus 2x2-wave register-staged
 # variants that are only reached through the override.
 _TILES = ["256x256w2x4", "256x128w4x2", "128x256w2x4", "128x128w2x2", "192x128w4x2", "256x256w2x2",
-          "256x128w2x2", "128x256w2x2", "256x256w4x2"]
+          "288x192w2x2", "256x128w2x2", "128x256w2x2", "256x256w4x2"]
 
 
 @pytest.mark.parametrize("no_dma", [False, True], ids=["dma", "regstaged"])
@@ -182,7 +182,7 @@ def test_stream_k(orc, dev, tuning, tile, seed, M, K, N, sk_min):
 
 @pytest.mark.parametrize("sk", [False, True], ids=["dp", "sk"])
 @pytest.mark.parametrize("tile", ["256x256w2x4", "256x256w2x2", "256x128w4x2", "128x256w2x4", "128x128w2x2",
-                                  "192x128w4x2"])
+                                  "192x128w4x2", "288x192w2x2"])
 @pytest.mark.parametrize("out_dtype", ["float32", "float16"])
 def test_epilogue_operands_without_bias(orc, dev, tuning, tile, sk, out_dtype):
     """The DMA kernels stage xs / ws / bias of each tile in LDS: ragged M and N that are not
@@ -287,12 +287,13 @@ def test_small_m_kernel(orc, dev, tuning, cfg, out_dtype, seed, M, K, N):
                   f"small-M cfg {cfg} without bias")
 
 
-@pytest.mark.parametrize("tile", ["256x256w2x4", "256x256w2x2"])
+@pytest.mark.parametrize("tile", ["256x256w2x4", "256x256w2x2", "288x192w2x2"])
 @pytest.mark.parametrize("M,K,N", [(4608, 3072, 3072), (1536, 12288, 3072), (520, 15360, 1000), (300, 128, 264)])
 def test_large_tiles_full_output(orc, dev, tuning, tile, M, K, N):
-    """The two 256x256 tiles (8 waves with the accumulator in VGPRs; 4 waves with it in the
-    AGPRs, software-pipelined k-steps) forced on full-size and ragged shapes, every output
-    compared bit for bit: one and many k-blocks, a ragged last tile row and column."""
+    """The large tiles (256x256 with 8 waves and the accumulator in VGPRs; 256x256 and 288x192
+    with 4 waves and the accumulator in the AGPRs, software-pipelined k-steps) forced on
+    full-size and ragged shapes, every output compared bit for bit: one and many k-blocks, a
+    ragged last tile row and column."""
     api = _api()
     tuning.set("gemm_tile", tile)
     tuning.set("gemm_sk", "0")
@@ -314,13 +315,17 @@ def test_stream_k_wait_timeout_is_reported(orc, dev, tuning, tile):
     with zero polls, so every kernel still runs to its end -- writes NaN over its tile instead
     of a silently wrong value and sets the workspace's error word: w4a4_status raises once and
     clears it.  The next launch (normal bounded wait) is exact again: flags left by the failed
-    launch carry an older generation and never match."""
+    launch carry an older generation and never match.
+
+    600x2688->600 has 21 k-blocks per tile; with stream-K ranges of at least 14 k-blocks, the
+    XCD groups that hold two tiles split them into three pieces (their owners wait), while
+    the groups that hold one tile run it as a single piece (no wait, never poisoned)."""
     api = _api()
     from convrot_mlx_amd import _native as nat
 
     tuning.set("gemm_tile", tile)
     tuning.set("gemm_sk", "1")
-    tuning.set("gemm_sk_min", "1")
+    tuning.set("gemm_sk_min", "14")
     M, K, N = 600, 2688, 600
     rng = np.random.default_rng(71)
     a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)

@@ -33,6 +33,10 @@ PATHS = {
                     3, 100, 384, 260, "int8"),
     "dma_192x128": ({"gemm_smallm_max": "0", "gemm_tile": "192x128w4x2", "gemm_sk": "0"},
                     2, 150, 256, 136, "int8"),
+    "dma_288x192": ({"gemm_smallm_max": "0", "gemm_tile": "288x192w2x2", "gemm_sk": "0"},
+                    2, 330, 512, 400, "int8"),
+    "dma_288x192_odd": ({"gemm_smallm_max": "0", "gemm_tile": "288x192w2x2", "gemm_sk": "0"},
+                        3, 101, 256, 202, "int8"),
     "stream_k": ({"gemm_smallm_max": "0", "gemm_tile": "128x256w2x4", "gemm_sk": "1",
                   "gemm_sk_min": "1"}, 2, 130, 1024, 270, "int8"),
     "register": ({"gemm_smallm_max": "0", "gemm_no_dma": "1"}, 2, 90, 256, 100, "int8"),
@@ -147,7 +151,7 @@ def test_every_kernel_path(orc, dev, tuning, path, dtype):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
 @pytest.mark.parametrize("form", ["chunk", "odd_stride", "vector", "full", "none"])
-@pytest.mark.parametrize("path", ["smallm_A", "dma_128x128", "register"])
+@pytest.mark.parametrize("path", ["smallm_A", "dma_128x128", "register", "dma_288x192"])
 def test_gate_forms(orc, dev, tuning, path, form, dtype):
     api = _api()
     env, B, L, K, N, fmt = PATHS[path]
