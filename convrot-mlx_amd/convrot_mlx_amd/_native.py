@@ -36,6 +36,8 @@ SIGNATURES = {
     "convrot_w4a4_gemm_ws": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp,
                                     _i64, _vp, _i32, _vp]),
     "convrot_w4a4_status": (_i32, [_vp, _vp]),
+    "convrot_w4a4_gemm_noalloc": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64,
+                                         _vp, _i32, _vp]),
     "convrot_w4a16_gemm": (_i32, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_w4a16_gemm_residual": (_i32, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp,
                                            _i32, _vp]),

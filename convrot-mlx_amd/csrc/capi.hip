@@ -346,6 +346,36 @@ int convrot_w4a4_gemm_ws(const void* act, int act_format, const float* xscales, 
                        "convrot_w4a4_gemm_ws");
 }
 
+int convrot_w4a4_gemm_noalloc(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
+                              const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
+                              const void* residual, const void* gate, int64_t gate_stride, int64_t rows_per_gate,
+                              void* out, int out_dtype, void* stream) {
+  if (int rc = check_w4a4(act, act_format, xscales, qweight, wscales, M, N, K, out, out_dtype)) return rc;
+  if (gate && !residual) return fail(CONVROT_ERR_INVALID, "a gate needs a residual");
+  if (gate && rows_per_gate <= 0)
+    return fail(CONVROT_ERR_INVALID, "rows_per_gate must be positive, got %lld", (long long)rows_per_gate);
+  if (M == 0 || N == 0) return ok();
+  convrot::GatedResidual gr{};
+  if (residual)
+    if (int rc = check_residual(residual, gate, gate_stride, rows_per_gate, M, N, &gr)) return rc;
+  // The same plan as convrot_w4a4_gemm; its workspace must fit the static scratch.
+  const size_t need = convrot::w4a4_plan_workspace_bytes(act_format, M, N, K);
+  if (need > convrot::kNoAllocScratchBytes)
+    return fail(CONVROT_ERR_INVALID,
+                "convrot_w4a4_gemm_noalloc: the plan for M=%lld N=%lld K=%lld needs %zu bytes of scratch, beyond "
+                "the static maximum of %zu",
+                (long long)M, (long long)N, (long long)K, need, convrot::kNoAllocScratchBytes);
+  convrot::WorkspaceSource src;
+  src.kind = convrot::WorkspaceSource::kGiven;
+  if (need > 0) {
+    if (const hipError_t e = convrot::noalloc_scratch((hipStream_t)stream, &src.given); e != hipSuccess)
+      return fail(CONVROT_ERR_LAUNCH, "convrot_w4a4_gemm_noalloc: scratch set-up failed: %s", hipGetErrorString(e));
+  }
+  return launch_status(convrot::launch_w4a4_gemm(act, act_format, xscales, qweight, wscales, bias, M, N, K, out,
+                                                 out_dtype, (hipStream_t)stream, gr, src),
+                       "convrot_w4a4_gemm_noalloc");
+}
+
 int convrot_w4a4_status(const void* workspace, void* stream) {
   const char* what = nullptr;
   const int rc = convrot::w4a4_workspace_status(workspace, (hipStream_t)stream, &what);

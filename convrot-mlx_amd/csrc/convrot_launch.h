@@ -76,6 +76,18 @@ hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscale
 // describes it) or -1 (a HIP call failed).
 int w4a4_workspace_status(const void* workspace, hipStream_t stream, const char** what);
 
+// Bytes of stream-K workspace the automatic W4A4 plan of this shape uses when
+// kSkWorkspaceBytes are available (0: a data-parallel plan, the few-row kernel
+// or the packed-activation kernel), under the current tuning overrides.
+size_t w4a4_plan_workspace_bytes(int act_format, int64_t M, int64_t N, int64_t K);
+
+// Static scratch of convrot_w4a4_gemm_noalloc (a file-scope device array, one
+// per GPU; no allocation): its size, and its device address on the current
+// device.  The first call on a device looks the address up and zero-fills the
+// control block with a kernel on `stream`.
+constexpr size_t kNoAllocScratchBytes = kSkWorkspaceBytes;
+hipError_t noalloc_scratch(hipStream_t stream, Workspace* out);
+
 // Few-row W4A4 kernel (int8 activation codes only); launch_w4a4_gemm routes
 // small M here.
 hipError_t launch_w4a4_smallm(const int8_t* act, const float* xscales, const uint8_t* qweight,

@@ -1432,6 +1432,34 @@ Workspace library_workspace(hipStream_t stream, bool create) {
   return {(uint8_t*)p, kSkWorkspaceBytes};
 }
 
+// Scratch of convrot_w4a4_gemm_noalloc: a stream-K workspace that is a
+// file-scope device array, so that entry point allocates nothing.  Every GPU
+// the library runs on holds its own copy (at its own device address) until
+// the process ends, and every no-alloc call on that GPU shares it.  Host code
+// never names the array itself (on the host it is a stand-in, not a device
+// address): it uses the address hipGetSymbolAddress returns for the current
+// device, kept in g_noalloc.
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+struct NoAllocState {
+  uint8_t* ptr = nullptr;  // device address of `scratch` on this device
+  bool cleared = false;    // its control block was zeroed by an eager launch
+};
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+NoAllocState g_noalloc[kMaxDevices];
+
+__global__ __launch_bounds__(256) void zero_words_kernel(int* __restrict__ p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+int current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
+  return dev;
+}
+
 template <int BM, int BN, int WM, int WN, bool APACK, int ODT>
 hipError_t launch_tile(const void* act, const float* xs, const uint8_t* wq, const float* ws, const float* bias,
                        int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
@@ -1565,11 +1593,52 @@ hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscale
   return launch_odt<false>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, gr, src, stream);
 }
 
+size_t w4a4_plan_workspace_bytes(int act_format, int64_t M, int64_t N, int64_t K) {
+  if (M == 0 || N == 0 || act_format == CONVROT_ACT_PACKED || M <= smallm_limit(N, K)) return 0;
+  const bool dma = tuning(kTuneGemmNoDma) != 1;
+  const Plan plan = choose_plan(M, N, K, dma, dma ? kSkWorkspaceBytes : 0);
+  return plan.sk ? sk_bytes(plan.t, plan.grid) : 0;
+}
+
+hipError_t noalloc_scratch(hipStream_t stream, Workspace* out) {
+  const int dev = current_device();
+  if (dev < 0) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  NoAllocState& s = g_noalloc[dev];
+  if (!s.ptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    s.ptr = (uint8_t*)p;
+  }
+  if (!s.cleared) {
+    // The stream-K control block (counters, generations, error word, flags)
+    // must start at zero; a fill kernel, stream-ordered before the call's GEMM.
+    // Under graph capture the fill becomes part of the graph (harmless: it
+    // runs before that graph's GEMM) and the next eager call clears again.
+    constexpr int kWords = (int)(kSkPartialOffset / 4);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((kWords + 255) / 256), dim3(256), 0, stream, (int*)s.ptr, kWords);
+    if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone) s.cleared = true;
+  }
+  *out = {s.ptr, kNoAllocScratchBytes};
+  return hipSuccess;
+}
+
 int w4a4_workspace_status(const void* workspace, hipStream_t stream, const char** what) {
   *what = nullptr;
   if (hipStreamSynchronize(stream) != hipSuccess) return -1;
   const uint8_t* bufs[2] = {(const uint8_t*)workspace, nullptr};
-  if (!workspace) bufs[0] = library_workspace(stream, false).ptr;
+  if (!workspace) {
+    bufs[0] = library_workspace(stream, false).ptr;
+    const int dev = current_device();
+    if (dev >= 0) {
+      std::lock_guard<std::mutex> lock(g_noalloc_mu);
+      bufs[1] = g_noalloc[dev].ptr;
+    }
+  }
   for (const uint8_t* b : bufs) {
     if (!b) continue;
     int err = 0;

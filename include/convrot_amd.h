@@ -24,11 +24,13 @@
  *    that needs it allocates it (hipMalloc + a stream-ordered zero fill, no
  *    host synchronization) and it is kept until the process ends; a launch
  *    under capture on a stream without one runs a data-parallel plan (same
- *    results bit for bit).  This is the library's only allocation and its only
- *    global state besides convrot_set_tuning's overrides.  Launches that use
- *    one workspace must not overlap in time: keep them on one stream, and do
- *    not replay a captured graph concurrently with other launches on its
- *    capture stream.
+ *    results bit for bit).  This is the library's only allocation.
+ *    convrot_w4a4_gemm_noalloc instead uses a static device array (one per
+ *    GPU, shared by all its calls) and allocates nothing.  Besides these
+ *    workspaces and convrot_set_tuning's overrides the library keeps no global
+ *    state.  Launches that use one workspace must not overlap in time: keep
+ *    them on one stream, and do not replay a captured graph concurrently with
+ *    other launches on its capture stream.
  *  - Otherwise calls are reentrant; concurrent calls on different streams are
  *    safe.
  */
@@ -194,11 +196,34 @@ int convrot_w4a4_gemm_ws(const void* act, int act_format, const float* xscales,
  * that never arrived; that owner wrote NaN over its output tile instead of a
  * silently wrong value) since the last call: synchronizes `stream`, reads and
  * clears the error word of `workspace` (NULL: the library's own workspace of
- * `stream`).  Returns CONVROT_ERR_LAUNCH with a message if so, else CONVROT_OK.
+ * `stream` and the static scratch of convrot_w4a4_gemm_noalloc on the current
+ * GPU).  Returns CONVROT_ERR_LAUNCH with a message if so, else CONVROT_OK.
  * Not callable under graph capture.  No counterpart in the reference (its
  * kernels have no error path, core.py:1106-1120).
  */
 int convrot_w4a4_status(const void* workspace, void* stream);
+
+/*
+ * convrot_w4a4_gemm_ws without a workspace argument and without any
+ * allocation: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference (MLX allocates every kernel output itself,
+ * core.py:1106-1113).  It runs the same plan as convrot_w4a4_gemm, bit for bit,
+ * taking the stream-K workspace from a static device array of
+ * 64 MiB + 32 KiB per GPU (kept until the process ends), which covers every
+ * plan on up to 256 CUs; a plan that would need more is rejected with
+ * CONVROT_ERR_INVALID.  The first call on a GPU looks up that array's address
+ * and zero-fills its control block with a kernel on `stream`; it calls no
+ * hipMalloc or hipFree.  Every call on one GPU shares the array: calls that
+ * overlap in time on one GPU (other streams, concurrent graph replays) race,
+ * so keep them on one stream.  convrot_w4a4_status(NULL, stream) reports a
+ * bounded-wait give-up of these calls too.
+ */
+int convrot_w4a4_gemm_noalloc(const void* act, int act_format, const float* xscales,
+                              const uint8_t* qweight, const float* wscales, const float* bias,
+                              int64_t M, int64_t N, int64_t K, const void* residual,
+                              const void* gate, int64_t gate_stride, int64_t rows_per_gate,
+                              void* out, int out_dtype, void* stream);
 
 /*
  * W4A16 GEMM: out[m, n] = out_dtype((dot_f32(act[m, :], w[n, :]) * wscales[n]) + bias[n]).

@@ -176,6 +176,24 @@ def test_gemm_residual_validation(lib):
     assert _err(lib) == "gate rows 16 elements apart overlap (N=32)"
 
 
+def test_gemm_noalloc_validation(lib):
+    """convrot_w4a4_gemm_noalloc (arguments of convrot_w4a4_gemm_residual; residual NULL: the
+    plain GEMM) rejects bad arguments before it touches its scratch or launches anything."""
+    g = lib.convrot_w4a4_gemm_noalloc
+    p = 0x10000
+    assert g(None, 1, None, None, None, None, 4, 32, 48, None, None, 0, 1, None, BF16, None) == 1
+    assert _err(lib) == "W4A4 GEMM requires K divisible by 32, got 48"
+    assert g(p, 1, p, p, p, None, 0, 32, 64, None, None, 0, 1, p, BF16, None) == 0  # no rows: nothing to do
+    assert g(p, 1, p, p, p, None, 4, 32, 64, None, p, 32, 1, p, BF16, None) == 1
+    assert _err(lib) == "a gate needs a residual"
+    assert g(p, 1, p, p, p, None, 4, 32, 64, p, p, 32, 0, p, BF16, None) == 1
+    assert _err(lib) == "rows_per_gate must be positive, got 0"
+    assert g(p, 1, p, p, p, None, 4, 32, 64, p + 8, None, 0, 1, p, BF16, None) == 1
+    assert _err(lib) == "residual and gate must be 16-byte aligned"
+    assert g(None, 1, p, p, p, None, 4, 32, 64, None, None, 0, 1, p, BF16, None) == 1
+    assert _err(lib) == "null pointer argument"
+
+
 def test_repack_validation(lib):
     assert lib.convrot_repack_weight(None, 0, None, 1, 33, 64, None) == 1
     assert _err(lib) == "MPP int4 packing requires even out_features, got 33"
