@@ -25,6 +25,7 @@ enum TuneKey : int {
   kTuneW4a16Tile,        // W4A16 tiled kernel tile: bm | bn << 10
   kTunePrepNi,           // prep kernel 1024-feature iterations per wave (1, 3 or 4)
   kTuneSkSpinLimit,      // stream-K bounded wait: polls before an owner gives up
+  kTuneGemmPersist,      // persistent 4-wave W4A4 kernel: 0 never, G > 0 always, on a grid of G workgroups
   kTuneCount
 };
 int tuning(TuneKey key);

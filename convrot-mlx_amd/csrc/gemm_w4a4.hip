@@ -466,6 +466,10 @@ struct DmaEngine {
   static constexpr int WS_OFF = EPI_OFF + XS_DMAS * 256, BIAS_OFF = WS_OFF + WS_DMAS * 256;
   static constexpr int EPI_BYTES = EPI_DMAS * 256;
   static constexpr int SMEM_BYTES = EPI_OFF + EPI_BYTES;
+  // The persistent kernel keeps two epilogue-operand buffers (the next tile's
+  // are fetched while the current tile's are still read).
+  static constexpr int SMEM_BYTES_2EPI = EPI_OFF + 2 * EPI_BYTES;
+
   static constexpr int LPW = LOADS / NW;  // DMA instructions per wave per k-block
   static constexpr int APW = A_FRAGS / NW, BPW = B_FRAGS / NW;  // of which activation / weight
   static constexpr int SHIFT = 4;         // weights unpacked x16: acc = 16 * dot
@@ -486,6 +490,7 @@ struct DmaEngine {
   uint8_t* smem;
   uint32_t smem_addr;
   int lane, wave, wm, wn;
+  int epi_buf = 0;  // epilogue-operand buffer in use (0 or 1; 1 only in the persistent kernel)
   // This wave's loads: activation pieces j = wave APW + i (rows 8j .. 8j+7)
   // and weight blocks j = wave BPW + i.  Per-lane byte offsets: va[i & 1]
   // for activations (the row swizzle flips with the parity of j; set_tile
@@ -506,9 +511,15 @@ struct DmaEngine {
   }
 
   __device__ __forceinline__ uint8_t* staging() const { return smem + wave * STAGING; }
-  __device__ __forceinline__ const float* epi_xs() const { return (const float*)(smem + EPI_OFF); }
-  __device__ __forceinline__ const float* epi_ws() const { return (const float*)(smem + WS_OFF); }
-  __device__ __forceinline__ const float* epi_bias() const { return (const float*)(smem + BIAS_OFF); }
+  __device__ __forceinline__ const float* epi_xs() const {
+    return (const float*)(smem + EPI_OFF + epi_buf * EPI_BYTES);
+  }
+  __device__ __forceinline__ const float* epi_ws() const {
+    return (const float*)(smem + WS_OFF + epi_buf * EPI_BYTES);
+  }
+  __device__ __forceinline__ const float* epi_bias() const {
+    return (const float*)(smem + BIAS_OFF + epi_buf * EPI_BYTES);
+  }
 
   // Load the tile's epilogue operands into LDS: EPI_DMAS dword DMAs of 256
   // bytes, DMA d by wave d % NW.  Entries past M or N, and all of a missing
@@ -521,7 +532,7 @@ struct DmaEngine {
     for (int d = wave; d < EPI_DMAS; d += NW) {  // array arr, 256-byte piece q of it
       const int arr = d < XS_DMAS ? 0 : d < XS_DMAS + WS_DMAS ? 1 : 2;
       const int q = d - (arr == 0 ? 0 : arr == 1 ? XS_DMAS : XS_DMAS + WS_DMAS);
-      const int off = arr == 0 ? EPI_OFF : arr == 1 ? WS_OFF : BIAS_OFF;
+      const int off = (arr == 0 ? EPI_OFF : arr == 1 ? WS_OFF : BIAS_OFF) + epi_buf * EPI_BYTES;
       const float* base = arr == 0 ? xscales + m0 : arr == 1 ? wscales + n0 : (bias ? bias + n0 : wscales);
       const int count = arr == 0 ? M - m0 : (arr == 1 || bias) ? N - n0 : 0;
       const i32x4_sgpr r = buffer_rsrc(base, (uint32_t)count * 4u);
@@ -931,6 +942,170 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __syncthreads();  // all waves done with the LDS ring before it is reused for output staging
   epilogue<ODT, E::TM, E::TN, E::SHIFT, true>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M,
                                               N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, gr, m0, n0);
+}
+
+// One pass of the 16-bit epilogue of the persistent 4-wave kernel: fragment
+// rows FM0 .. FM1-1 of the wave's TM x TN tile, ((float(acc) * xs) * ws) + bias
+// as in `epilogue`, staged through the wave's LDS region and written as 16-byte
+// buffer stores; a chunk outside the M x N output gets an offset past the
+// buffer's range, which the hardware drops.  Needs N % 8 == 0 and 2 M N < 2^31.
+template <int ODT, int TM, int TN, int SHIFT, int FM0, int FM1>
+__device__ __forceinline__ void epilogue_pass(const i32x4 (&acc)[TN / 16][TM / 16], uint8_t* region, int lane,
+                                              int mw, int nw, int M, int N, const float* xs_lds,
+                                              const float* ws_lds, const float* bias_lds,
+                                              __amdgpu_buffer_rsrc_t orsrc, int m0, int n0) {
+  static_assert(ODT == kBF16 || ODT == kF16, "16-bit outputs");
+  constexpr int FN = TN / 16, RS = TN * 2 + 16, CPR = TN / 8, ROWS = (FM1 - FM0) * 16;
+  constexpr int NIT = ROWS * CPR / 64;
+  static_assert(ROWS * CPR % 64 == 0, "whole store instructions per pass");
+  float xs[FM1 - FM0];
+#pragma unroll
+  for (int fm = FM0; fm < FM1; ++fm) xs[fm - FM0] = xs_lds[mw + fm * 16 + (lane & 15) - m0];
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) {
+    const int nl = fn * 16 + 4 * (lane >> 4);
+    const float4 w4 = *(const float4*)(ws_lds + (nw + nl - n0));
+    const float4 b4 = *(const float4*)(bias_lds + (nw + nl - n0));
+    const float wsv[4] = {w4.x, w4.y, w4.z, w4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+    for (int fm = FM0; fm < FM1; ++fm) {
+      float o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = (((float)(acc[fn][fm][r] >> SHIFT) * xs[fm - FM0]) * wsv[r]) + bv[r];
+      const uint2 w = ODT == kBF16 ? make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]))
+                                   : make_uint2(pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3]));
+      *(uint2*)(region + ((fm - FM0) * 16 + (lane & 15)) * RS + nl * 2) = w;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int c = it * 64 + lane, row = c / CPR, cc = c % CPR;
+    const int m = mw + FM0 * 16 + row, n = nw + cc * 8;
+    const uint4 v = *(const uint4*)(region + row * RS + cc * 16);
+    const uint32_t off = (m < M && n < N) ? (uint32_t)((m * N + n) * 2) : 0x80000000u;
+    __builtin_amdgcn_raw_buffer_store_b128((u32x4){v.x, v.y, v.z, v.w}, orsrc, (int)off, 0, 0);
+  }
+  // the region's next writes (the next pass) come after these reads
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Persistent form of the kAgpr data-parallel kernel for multi-round grids with
+// the plain 16-bit epilogue: workgroup g runs tiles g, g + G, g + 2G, ... (G =
+// gridDim.x, a multiple of the XCD count, so each tile keeps the XCD the
+// one-tile-per-workgroup kernel gives it).  At a tile boundary the workgroup
+// fetches the next tile's epilogue operands (into the other operand buffer)
+// and first k-block (ring stage 0) before the current tile's epilogue, which
+// stages its output through ring stages 1 and 2 in two passes; the next
+// tile's k-blocks 1 and 2 follow once every wave is done with the staging.  So
+// the first DMA's latency and the workgroup relaunch overlap the epilogue.
+// The next tile's first wait (at most 2 x LPW DMAs in flight) retires block 0
+// and everything issued before blocks 1 and 2, the output stores included.
+// Arguments of the persistent kernel.  The kernel parks them in LDS and reads
+// them back at each tile boundary, so they do not occupy scalar registers
+// across the k-loop (kept live there, they spilled).
+struct PersistArgs {
+  const int8_t* act;
+  const uint8_t* wq;
+  const float* xscales;
+  const float* wscales;
+  const float* bias;
+  void* out;
+  int M, N, K, nblocks, kblocks, tiles_m, tiles_n;
+};
+
+// A wave-uniform value read back from LDS into scalar registers.
+template <class T>
+__device__ __forceinline__ T lds_uniform(const T& v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "dword or qword");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+  } else {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t r = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u) |
+                       ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32)) << 32);
+    return __builtin_bit_cast(T, r);
+  }
+}
+
+template <int BM, int BN, int STAGES, int ODT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void w4a4_gemm_agpr_persist_kernel(
+    PersistArgs args) {
+  using E = DmaEngine<BM, BN, 2, 2, kAgpr, STAGES>;
+  constexpr int FM = E::FM, P1 = (FM + 1) / 2;  // fragment rows of the first pass
+  constexpr int RS = E::TN * 2 + 16;
+  static_assert(E::NW * P1 * 16 * RS <= 2 * E::STAGE_BYTES, "two-pass staging fits ring stages 1 and 2");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES_2EPI];
+  __shared__ PersistArgs la;
+  E e(smem);
+
+  const int tiles = args.tiles_m * args.tiles_n;
+  int t = blockIdx.x, m0, n0;
+  if (t >= tiles) return;  // the grid is rounded up to a multiple of the XCD count
+  auto origin = [](int t, int tiles_m, int tiles_n, int& m0, int& n0) {
+    const int tiles = tiles_m * tiles_n, per_xcd = tiles / kXcds;
+    int logical = t;
+    if (logical < per_xcd * kXcds) logical = (logical % kXcds) * per_xcd + logical / kXcds;
+    tile_origin(logical, tiles_m, tiles_n, BM, BN, m0, n0);
+  };
+  if (threadIdx.x == 0) la = args;  // published by the first k-block's barrier
+  origin(t, args.tiles_m, args.tiles_n, m0, n0);
+  e.set_tile(args.act, args.wq, args.M, args.K, args.nblocks, args.kblocks, m0, n0);
+  e.issue_epi(args.xscales, args.wscales, args.bias, args.M, args.N, m0, n0);
+  e.prologue(0, args.kblocks);
+  int kblocks = args.kblocks;
+  i32x4 acc[E::FN][FM];
+  while (true) {
+    // Opaque per tile: keeps the compiler from hoisting lane-derived addresses
+    // out of the tile loop, where they would stay live across the k-loop.
+    asm volatile("" : "+v"(e.lane), "+s"(kblocks));
+#pragma unroll
+    for (int a = 0; a < E::FN; ++a)
+#pragma unroll
+      for (int b = 0; b < FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
+    e.body_agpr(0, kblocks, acc, nullptr, 0);
+    // every wave is done with the ring and the DMAs of this tile have landed
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int M = lds_uniform(la.M), N = lds_uniform(la.N);
+    const int tiles_m = lds_uniform(la.tiles_m), tiles_n = lds_uniform(la.tiles_n);
+    const int nt = t + (int)gridDim.x;
+    const bool more = nt < tiles_m * tiles_n;
+    const int cur = e.epi_buf;
+    int nm0 = 0, nn0 = 0;
+    if (more) {
+      origin(nt, tiles_m, tiles_n, nm0, nn0);
+      e.set_tile(lds_uniform(la.act), lds_uniform(la.wq), M, lds_uniform(la.K), lds_uniform(la.nblocks), kblocks,
+                 nm0, nn0);
+      e.epi_buf = cur ^ 1;
+      e.issue_epi(lds_uniform(la.xscales), lds_uniform(la.wscales), lds_uniform(la.bias), M, N, nm0, nn0);
+      e.issue(0, 0);
+    }
+    const __amdgpu_buffer_rsrc_t orsrc =
+        __builtin_amdgcn_make_buffer_rsrc(lds_uniform(la.out), (short)0, (int)((int64_t)M * N * 2), 0x00020000);
+    const int mw = m0 + e.wm * E::TM, nw = n0 + e.wn * E::TN;
+    uint8_t* staging = smem + E::STAGE_BYTES + e.wave * (P1 * 16 * RS);
+    const uint8_t* epi = smem + E::EPI_OFF + cur * E::EPI_BYTES;
+    const float* xs_lds = (const float*)epi;
+    const float* ws_lds = (const float*)(epi + (E::WS_OFF - E::EPI_OFF));
+    const float* b_lds = (const float*)(epi + (E::BIAS_OFF - E::EPI_OFF));
+    epilogue_pass<ODT, E::TM, E::TN, E::SHIFT, 0, P1>(acc, staging, e.lane, mw, nw, M, N, xs_lds, ws_lds, b_lds,
+                                                      orsrc, m0, n0);
+    epilogue_pass<ODT, E::TM, E::TN, E::SHIFT, P1, FM>(acc, staging, e.lane, mw, nw, M, N, xs_lds, ws_lds, b_lds,
+                                                       orsrc, m0, n0);
+    if (!more) break;
+    // every wave is done with the staging area (ring stages 1 and 2)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    e.issue(min(1, kblocks - 1), 1);
+    e.issue(min(2, kblocks - 1), 2);
+    t = nt;
+    m0 = nm0;
+    n0 = nn0;
+  }
 }
 
 // ---- stream-K
@@ -1486,6 +1661,25 @@ hipError_t launch_dma(const Plan& plan, const void* act, const float* xs, const 
         hipLaunchKernelGGL((w4a4_gemm_agpr_sk_kernel<STAGES, ODT>), dim3((unsigned)plan.grid), dim3(256), 0, stream,
                            (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, tm,
                            tn, ska, gr);
+        return hipGetLastError();
+      }
+    }
+    if constexpr (ODT != kF32) {
+      // More tiles than one round: the persistent kernel (plain epilogue,
+      // whole 16-byte output chunks, 32-bit store offsets).  The gemm_persist
+      // tuning override turns it off (0) or forces it on a grid of G.
+      const int cus = device_cus();
+      const int force = tuning(kTuneGemmPersist);
+      const bool eligible = !gr.residual && N % 8 == 0 && M * N * 2 < ((int64_t)1 << 31);
+      const int64_t tiles = (int64_t)tm * tn;
+      int grid = force > 0 ? force : cus;
+      grid = std::max(kXcds, grid / kXcds * kXcds);
+      if (eligible && force != 0 && (force > 0 || tiles > cus)) {
+        grid = (int)std::min<int64_t>(grid, (tiles + kXcds - 1) / kXcds * kXcds);
+        const PersistArgs pa{(const int8_t*)act, wq, xs, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks,
+                             tm, tn};
+        hipLaunchKernelGGL((w4a4_gemm_agpr_persist_kernel<BM, BN, STAGES, ODT>), dim3((unsigned)grid), dim3(256), 0,
+                           stream, pa);
         return hipGetLastError();
       }
     }

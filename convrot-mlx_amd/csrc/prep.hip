@@ -564,6 +564,17 @@ bool prep_plan(int64_t rows, int64_t K, int* ni_out, int* waves_out) {
       best_w = (int)w;
     }
   }
+  // Three iterations on more than four waves lose to four iterations on at
+  // most four waves with one idle block: at 4608 rows, 15 blocks run 7 % faster
+  // as 4 waves x 4 than as 5 waves x 3 (12 blocks stay 4 x 3).
+  if (best_ni == 3 && best_w > 4) {
+    const int64_t w4 = (blocks + 3) / 4;
+    if (w4 <= 4 && w4 * 4 - blocks <= best_idle + 1) {
+      best_ni = 4;
+      best_w = (int)w4;
+      best_idle = w4 * 4 - blocks;
+    }
+  }
   if (best_idle < 0) return false;
   *ni_out = best_ni;
   *waves_out = best_w;

@@ -287,6 +287,8 @@ const char* convrot_last_error(void);
  *   w4a16_tile       "BMxBN"              W4A16 tiled-kernel tile
  *   prep_ni          "1" | "3" | "4"      prep kernel 1024-feature blocks per wave
  *   sk_spin_limit    polls                stream-K bounded wait before giving up
+ *   gemm_persist     "0" | workgroups     persistent 4-wave W4A4 kernel: never, or always
+ *                                         on a grid of that many workgroups
  * Returns CONVROT_ERR_INVALID for an unknown name or a malformed value.
  */
 int convrot_set_tuning(const char* name, const char* value);

@@ -356,3 +356,40 @@ def test_stream_k_wait_timeout_is_reported(orc, dev, tuning, tile):
     for _ in range(2):
         _assert_exact(run(), expected, f"tile {tile} after a failed launch")
     api.w4a4_status(dev)
+
+
+@pytest.mark.parametrize("tile", ["288x192w2x2", "256x256w2x2"])
+@pytest.mark.parametrize("out_dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("grid,M,K,N", [(8, 1000, 640, 1000),   # 4 x 6 / 4 x 4 tiles, ragged edges, 3 per workgroup
+                                        (16, 600, 384, 776),    # more workgroups than tiles
+                                        (8, 300, 128, 264),     # one k-block
+                                        (8, 2000, 1408, 1536)])  # 7 x 8 / 8 x 6 tiles, 11 k-blocks
+def test_persistent_kernel(orc, dev, tuning, tile, out_dtype, grid, M, K, N):
+    """The persistent 4-wave kernel (which the automatic plan runs when a 4-wave tile's grid
+    exceeds one round) forced on a small grid through the gemm_persist override, so every
+    workgroup runs several tiles: every output bit-exact against the oracle and equal to the
+    one-tile-per-workgroup kernel's."""
+    api = _api()
+    tuning.set("gemm_tile", tile)
+    tuning.set("gemm_sk", "0")
+    tuning.set("gemm_smallm_max", "0")
+    rng = np.random.default_rng(M + K + N + grid)
+    a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    b = rng.normal(size=(N,)).astype(np.float32)
+    want = orc.w4a4_matmul_codes_large(a, w, xs, ws, b, out_dtype)
+    args = (torch.from_numpy(a).to(dev), _dev_u8(orc.codes_to_cdna4(w), dev), torch.from_numpy(xs).to(dev),
+            torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev))
+    dt = {"bfloat16": torch.bfloat16, "float16": torch.float16}[out_dtype]
+    outs = {}
+    for mode in (str(grid), "0"):
+        tuning.set("gemm_persist", mode)
+        for call in range(2):
+            out = api.hip_w4a4_int8_matmul(*args, output_dtype=dt, out_features=N)
+            torch.cuda.synchronize()
+            got = from_dev(out)
+            _assert_exact(got, want, f"tile {tile} gemm_persist={mode} call {call}")
+        outs[mode] = got
+    assert np.array_equal(outs[str(grid)], outs["0"])
