@@ -26,6 +26,8 @@ there is no CPU path.  Outputs and receipts are never overwritten.
 
 from __future__ import annotations
 
+import os
+
 import hashlib
 import json
 import time
@@ -335,7 +337,7 @@ def load_convrot_checkpoint(
     model: nn.Module,
     path: str | Path,
     *,
-    backend: str = "hip-w4a4",
+    backend: str | None = None,
     preprocessor: str | None = None,
     group_size: int = CONVROT_GROUP_SIZE,
     expected_source_sha256: str | None = None,
@@ -348,6 +350,8 @@ def load_convrot_checkpoint(
     `hip-*` takes CONVROT_CDNA4_SCHEMA as stored, or the NK CONVROT_SCHEMA repacked to the
     CDNA4 layout on `device` while loading."""
     metadata = read_metadata(path)
+    # the same default as ConvRotLinear: $CONVROT_BACKEND, then the reference's variable
+    backend = backend or os.getenv("CONVROT_BACKEND") or os.getenv("CONVROT_MLX_BACKEND") or "hip-w4a4"
     uses_mpp = backend.startswith("mpp-")
     allowed = (CONVROT_MPP_SCHEMA,) if uses_mpp else (CONVROT_CDNA4_SCHEMA, CONVROT_SCHEMA)
     schema = metadata.get("schema")

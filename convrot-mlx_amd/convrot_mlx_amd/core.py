@@ -292,12 +292,21 @@ def regular_hadamard(x: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE) -> t
 
 
 def quantize_signed_int4_rowwise(x: torch.Tensor):
-    """Symmetric absmax/7 row quantization without rotation (core.py:149-158)."""
+    """Symmetric absmax/7 row quantization without rotation (core.py:149-158), for any even
+    number of features like the reference.  The kernel reads rows in 16-feature chunks, so a
+    row whose length is not a multiple of 16 is zero-padded on the device first: zeros change
+    neither the row absmax nor any code, and the padded codes fall in whole bytes past K/2."""
     if x.ndim != 2:
         raise ValueError(f"rowwise int4 quantization expects 2D input, got {tuple(x.shape)}")
-    if x.shape[-1] % 2:
-        raise ValueError(f"last dimension must be even, got {x.shape[-1]}")
-    return _prepare(x, 1, nat.PREP_PACKED | nat.PREP_NO_ROTATE)
+    features = x.shape[-1]
+    if features % 2:
+        raise ValueError(f"last dimension must be even, got {features}")
+    if features % 16 == 0 or x.shape[0] == 0:
+        return _prepare(x, 1, nat.PREP_PACKED | nat.PREP_NO_ROTATE)
+    nat.require_device(x)
+    padded = torch.nn.functional.pad(x, (0, -features % 16))
+    q, scales = _prepare(padded, 1, nat.PREP_PACKED | nat.PREP_NO_ROTATE)
+    return q[:, : features // 2].contiguous(), scales
 
 
 def prepare_convrot_activation(x: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE):

@@ -114,6 +114,23 @@ def test_quantize_without_rotation(orc, dev, dtype):
     assert np.array_equal(orc.unpack_signed_int4(from_dev(q)), codes)
 
 
+@pytest.mark.parametrize("features", [2, 6, 34, 250])
+def test_quantize_without_rotation_any_even_features(orc, dev, features):
+    """quantize_signed_int4_rowwise accepts any even row length, as the reference does
+    (core.py:97-100,149-158): rows not a multiple of 16 long are padded with zeros on the
+    device; codes and scales equal the oracle's bit for bit, with extreme rows (all zero, one
+    outlier) included."""
+    api = _api()
+    x = normal_input(29 + features, (7, features), "bfloat16", orc)
+    x[0] = 0
+    x[1, -1] = orc.from_f32(np.array([300.0], np.float32), "bfloat16")[0]
+    q, s = api.quantize_signed_int4_rowwise(to_dev(x, "bfloat16", dev))
+    codes, scales = orc.quantize_rowwise_codes(x, "bfloat16")
+    assert q.shape == (7, features // 2)
+    assert np.array_equal(from_dev(s), scales)
+    assert np.array_equal(orc.unpack_signed_int4(from_dev(q)), codes)
+
+
 def test_regular_hadamard_any_leading_shape(orc, dev):
     api = _api()
     x = normal_input(9, (2, 3, 7, 256), "bfloat16", orc)
