@@ -70,6 +70,9 @@ def parse():
     ap.add_argument("--no-config5", action="store_true", help="skip the FLUX DiT step (config 5)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run one 256 MiB device copy first (counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--workload", choices=("config3", "config2"), default="config3",
+                    help="the measured workload: configs[2] (the headline, M=4608 G=256) or configs[1] (M=1536 "
+                         "G=64, for profiling); the extras are the same either way")
     return ap.parse_args()
 
 
@@ -187,8 +190,11 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    M, G, shapes = CONFIG3["M"], CONFIG3["G"], CONFIG3["shapes"]
-    sets = make_layers(torch, core, dev, M, G, shapes, seed=20260823, sets=args.sets)
+    W = CONFIG3 if args.workload == "config3" else CONFIG2
+    M, G, shapes = W["M"], W["G"], W["shapes"]
+    # configs[1]'s four linears total ~315 MB: three buffer sets keep a step out of the Infinity Cache
+    sets = make_layers(torch, core, dev, M, G, shapes, seed=20260823,
+                       sets=args.sets if args.workload == "config3" else max(args.sets, 3))
     torch.cuda.synchronize()
     runner = PathRunner(nat, dev, M, G)
     ms_per_step, prep_ms, gemm_ms, ms_events, ev_steps = measure_path(
@@ -203,7 +209,7 @@ def main() -> int:
     prep_agg = prep_bytes.sum() / (prep_ms.sum() * 1e-3) / 1e9
 
     traffic, traffic_note = None, "no FETCH_SIZE/WRITE_SIZE profile for this workload"
-    if TRAFFIC_FILE.exists():
+    if TRAFFIC_FILE.exists() and args.workload == "config3":
         try:
             tj = json.loads(TRAFFIC_FILE.read_text())
             traffic = tj.get("hbm_bytes_per_launch_avg")
@@ -228,9 +234,13 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) activations with 0.5% x20 channels, N(0,0.02^2) weights with 1% x10 "
                 "input channels, N(0,0.02^2) bias; random init)",
         "config": {
-            "workload": "benchmark configs[2]: FLUX W4A4 linears at M=4608 (4096 image + 512 text tokens), group "
-                        "256, bf16, with bias: 3072->9216, 3072->3072, 3072->12288, 12288->3072, 3072->21504, "
-                        "15360->3072; complete path prep+GEMM+epilogue",
+            "workload": ("benchmark configs[2]: FLUX W4A4 linears at M=4608 (4096 image + 512 text tokens), "
+                         "group 256, bf16, with bias: 3072->9216, 3072->3072, 3072->12288, 12288->3072, "
+                         "3072->21504, 15360->3072; complete path prep+GEMM+epilogue"
+                         if args.workload == "config3" else
+                         "benchmark configs[1]: FLUX double-block W4A4 linears at M=1536 (1024 image + 512 "
+                         "text tokens), group 64, bf16, with bias: 3072->9216, 3072->3072, 3072->12288, "
+                         "12288->3072; complete path prep+GEMM+epilogue"),
             "M": M, "group_size": G, "shapes_KxN": shapes, "buffer_sets": args.sets,
             "pct_int8_peak": round(100.0 * tops / INT8_PEAK_TOPS, 2),
         },
@@ -460,7 +470,7 @@ def cpu_baseline(np, layers, M, G, rows_per_thread, shapes):
     except OSError:
         pass
     return {"value": round(ops / seconds / 1e12, 6), "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"the first {rows} of the {M} rows of each of the six config-3 linears, complete path "
+            "sample": f"the first {rows} of the {M} rows of each of the {len(shapes)} linears, complete path "
                       f"(prep + integer GEMM + epilogue), {threads} threads of {cpu} "
                       f"(os.cpu_count() = {os.cpu_count()}), median of 3 repetitions: "
                       f"{', '.join(f'{r:.2f}' for r in reps)} s"}
