@@ -92,7 +92,7 @@ int convrot_set_tuning(const char* name, const char* value) {
                 {"gemm_smallm_max", kTuneGemmSmallmMax}, {"w4a4_smallm_cfg", kTuneW4a4SmallmCfg},
                 {"w4a16_cfg", kTuneW4a16Cfg},         {"w4a16_tile", kTuneW4a16Tile},
                 {"prep_ni", kTunePrepNi},             {"sk_spin_limit", kTuneSkSpinLimit},
-                {"gemm_persist", kTuneGemmPersist}};
+                {"gemm_persist", kTuneGemmPersist},   {"gemm_mfma32", kTuneGemmMfma32}};
   int key = -1;
   for (const auto& n : kNames)
     if (strcmp(n.name, name) == 0) key = n.key;

@@ -448,6 +448,29 @@ __device__ __forceinline__ void mfma_drain(i32x4 (&acc)[FN][FM]) {
     for (int fm = 0; fm < FM; ++fm) asm volatile("" : "+a"(acc[fn][fm]));
 }
 
+// The 32 x 32 x 32 form: acc (16 AGPRs, a 32 x 32 int32 block) += b . a.  Lane
+// l supplies row l % 32 of each operand and 16 bytes of its k-group l / 32;
+// the result's register v of lane l is (n = 8 (v / 4) + 4 (l / 32) + v % 4,
+// m = l % 32) of the block.  Hazards as for mfma_agpr (the drain's 24 wait
+// states also cover this MFMA's longer result latency).
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ void mfma_agpr32(i32x16& c, const i32x4& b, const i32x4& a) {
+  asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+a"(c) : "v"(b), "v"(a) : "memory");
+}
+
+template <int FN, int FM>
+__device__ __forceinline__ void mfma_drain32(i32x16 (&acc)[FN][FM]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) asm volatile("" : "+a"(acc[fn][fm]));
+}
+
+// Global slot (0 .. 31) of the second half-block at which DMA piece p of the
+// 32 x 32 k-loop is issued: the 12 pieces spread evenly over its 32 MFMAs.
+__host__ __device__ constexpr int agpr32_dma_slot(int p) { return p * 8 / 3 + 1; }
+
 template <int BM, int BN, int WM, int WN, int PIPE, int STAGES = 3>
 struct DmaEngine {
   static constexpr int kBM = BM, kBN = BN;
@@ -793,6 +816,133 @@ struct DmaEngine {
     wait_vmcnt<0>();  // the DMAs past the last block have landed before the ring is reused
   }
 
+  // ---- kAgpr on v_mfma_i32_32x32x32_i8: the wave's TM x TN corner as
+  //      FN32 x FM32 blocks of 32 x 32, four 32-feature k-steps per k-block.
+  //
+  // Lane (g = lane / 32, r = lane % 32) feeds row r of a block and, in k-step
+  // s, the 16 features of 16-byte chunk c = 4 g + s of the k-block: activation
+  // chunk c of row r; weight row r (CDNA4 weight block 2 f + r / 16, row r % 16)
+  // holds chunks 2 q and 2 q + 1 in the 16 bytes of layout lane 16 q + r % 16,
+  // so the lane reads q = 2 g (chunks 4 g, 4 g + 1) and q = 2 g + 1 (4 g + 2,
+  // 4 g + 3).  Both operands pair chunk c byte for byte as the 16 x 16 x 64
+  // path does, so the integer dot products are the same.
+  //
+  // Per k-block: k-steps 0 and 1 read the block's activation chunks for
+  // k-steps 1 .. 3; a barrier publishes block i+1 and frees the block's ring
+  // stage; k-steps 2 and 3 read block i+1's packed weights and k-step-0
+  // activations and issue the 12 DMA pieces of block i+STAGES.
+  static constexpr int FN32 = TN / 32, FM32 = TM / 32, NS32 = FN32 * FM32;
+
+  __device__ __forceinline__ const uint8_t* a_base32(int stage, int s) const {
+    const int r = lane & 31;
+    return smem + stage * STAGE_BYTES + (wm * TM + r) * 128 + (((4 * (lane >> 5) + s) ^ a_swizzle(r)) * 16);
+  }
+  // Packed weights of block f, half q - 2 g of the lane: at + f * 2048 + i * 256.
+  __device__ __forceinline__ const uint8_t* b_base32(int stage) const {
+    return smem + stage * STAGE_BYTES + (A_FRAGS + wn * FN + ((lane >> 4) & 1)) * 1024 +
+           (32 * (lane >> 5) + (lane & 15)) * 16;
+  }
+  __device__ __forceinline__ void read_bq32(int stage, uint4 (&bq)[FN32][2]) const {
+    const uint8_t* sb = b_base32(stage);
+#pragma unroll
+    for (int f = 0; f < FN32; ++f)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) bq[f][i] = *(const uint4*)(sb + f * 2048 + i * 256);
+  }
+
+  // k-step S of the block in ring stage st: MFMAs on (w[S & 1], a[S]); the
+  // fillers between them prepare the following k-steps (see above).
+  template <int S>
+  __device__ __forceinline__ void agpr32_kstep(int st, int nst, int dma_kb, uint4 (&bq)[FN32][2],
+                                               i32x4 (&a)[4][FM32], i32x4 (&w)[2][FN32],
+                                               i32x16 (&acc)[FN32][FM32]) {
+    hazard_pad(w[S & 1]);
+    uint32_t u[FN32][4];
+    // source of the next k-step's weights: this block's bq, or (S == 3) the next block's
+    constexpr int NB = S == 3 ? 0 : (S + 1) >> 1, NH = (S + 1) & 1;
+    const uint8_t* sa1 = a_base32(S < 2 ? st : nst, S == 0 ? 1 : S == 1 ? 3 : 0);
+    const uint8_t* sa2 = a_base32(st, 2);
+    const uint8_t* sb = b_base32(nst);
+#pragma unroll
+    for (int t = 0; t < NS32; ++t) {
+      const int fm = t / FN32, fn = t % FN32;
+      mfma_agpr32(acc[fn][fm], w[S & 1][fn], a[S][fm]);
+      // activation chunks: S 0 -> a[1] at slots 1, 3, .. and a[2] after them;
+      // S 1 -> a[3]; S 3 -> next block's a[0] (ring stage nst)
+      if (S != 2 && t % 2 == 1 && t / 2 < FM32) {
+        if constexpr (S == 0) a[1][t / 2] = *(const i32x4*)(sa1 + (t / 2) * 4096);
+        if constexpr (S == 1) a[3][t / 2] = *(const i32x4*)(sa1 + (t / 2) * 4096);
+        if constexpr (S == 3) a[0][t / 2] = *(const i32x4*)(sa1 + (t / 2) * 4096);
+      }
+      if (S == 0 && t % 2 == 1 && t / 2 >= FM32 && t / 2 < 2 * FM32)
+        a[2][t / 2 - FM32] = *(const i32x4*)(sa2 + (t / 2 - FM32) * 4096);
+      // S 2: the next block's packed weights (ring stage nst) after this
+      // block's last unpack (slots 0 .. 2 FN32 - 1 below)
+      if (S == 2 && t >= 2 * FN32 && t < 4 * FN32) {
+        const int k = t - 2 * FN32;
+        bq[k / 2][k % 2] = *(const uint4*)(sb + (k / 2) * 2048 + (k % 2) * 256);
+      }
+      // DMA pieces of block dma_kb into the freed stage st
+      if (S >= 2) {
+#pragma unroll
+        for (int p = 0; p < LPW; ++p)
+          if (agpr32_dma_slot(p) == (S - 2) * NS32 + t) issue_piece(dma_kb, st, p);
+      }
+      // the next k-step's weight operand, half k of 2 FN32: S 0..2 at slots
+      // 0 .. 2 FN32 - 1 (S 0, 1 on even slots), S 3 once its bq has landed
+      {
+        int k = -1;
+        if (S == 0 || S == 1) k = t % 2 == 0 ? t / 2 : -1;
+        if (S == 2) k = t;
+        if (S == 3) k = t - (NS32 - 2 * FN32);
+        if (k >= 0 && k < 2 * FN32) {
+          const int j = k / 2, h = k % 2;
+          const uint4& b = bq[j][NB];
+          unpack_half(NH ? (h ? b.w : b.z) : (h ? b.y : b.x), u[j][2 * h], u[j][2 * h + 1]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < FN32; ++j)
+      w[(S + 1) & 1][j] = (i32x4){(int)u[j][0], (int)u[j][1], (int)u[j][2], (int)u[j][3]};
+  }
+
+  __device__ __forceinline__ void body_agpr32(int kb0, int n, i32x16 (&acc)[FN32][FM32]) {
+    static_assert(NW == 4 && STAGES == 3 && TM % 32 == 0 && TN % 32 == 0, "kAgpr 32x32: 4 waves, 3 stages");
+    static_assert(NS32 == 16 && FN32 == 4 && FM32 == 4, "filler schedule written for 4 x 4 blocks per wave");
+    static_assert(LPW == 12 && agpr32_dma_slot(LPW - 1) < 2 * NS32, "DMA pieces fit the second half-block");
+    uint4 bq[FN32][2];
+    i32x4 a[4][FM32], w[2][FN32];
+    wait_vmcnt<2 * LPW>();  // block 0 (and the epilogue operands) landed
+    __builtin_amdgcn_s_barrier();
+    read_bq32(0, bq);
+    {
+      const uint8_t* sa = a_base32(0, 0);
+#pragma unroll
+      for (int fm = 0; fm < FM32; ++fm) a[0][fm] = *(const i32x4*)(sa + fm * 4096);
+    }
+#pragma unroll
+    for (int f = 0; f < FN32; ++f) unpack(bq[f][0], 0, w[0][f]);
+    const int last_kb = kb0 + n - 1;
+    int st = 0;
+    for (int i = 0; i < n; ++i) {
+      const int nst = st + 1 == STAGES ? 0 : st + 1;
+      const int dma_kb = min(kb0 + i + STAGES, last_kb);
+      agpr32_kstep<0>(st, nst, dma_kb, bq, a, w, acc);
+      agpr32_kstep<1>(st, nst, dma_kb, bq, a, w, acc);
+      // middle: block i+1 landed and this block's activation reads are done;
+      // the barrier publishes block i+1 and frees stage st
+      wait_vmcnt<LPW>();
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      agpr32_kstep<2>(st, nst, dma_kb, bq, a, w, acc);
+      agpr32_kstep<3>(st, nst, dma_kb, bq, a, w, acc);
+      st = nst;
+    }
+    mfma_drain32(acc);
+    wait_vmcnt<0>();  // the DMAs past the last block have landed before the ring is reused
+  }
+
   // Wait until at most `ahead` k-blocks of this wave's DMAs (LPW each) are in
   // flight (`ahead` <= J; wave-uniform, so the branches are scalar).
   template <int J>
@@ -993,6 +1143,88 @@ __device__ __forceinline__ void epilogue_pass(const i32x4 (&acc)[TN / 16][TM / 1
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The 16-bit epilogue of a wave's TM x TN corner held as 32 x 32 blocks
+// (mfma_agpr32's layout): ((float(acc) * xs) * ws) + bias as in `epilogue`,
+// staged through the wave's LDS region (TM rows of TN * 2 + 16 bytes) and
+// written as range-checked 16-byte buffer stores.  Needs N % 8 == 0 and
+// 2 M N < 2^31.
+template <int ODT, int TM, int TN, int SHIFT>
+__device__ __forceinline__ void epilogue32(const i32x16 (&acc)[TN / 32][TM / 32], uint8_t* region, int lane, int mw,
+                                           int nw, int M, int N, const float* xs_lds, const float* ws_lds,
+                                           const float* bias_lds, __amdgpu_buffer_rsrc_t orsrc, int m0, int n0) {
+  static_assert(ODT == kBF16 || ODT == kF16, "16-bit outputs");
+  constexpr int FN = TN / 32, FM = TM / 32, RS = TN * 2 + 16, CPR = TN / 8;
+  constexpr int NIT = TM * CPR / 64;
+  static_assert(TM * CPR % 64 == 0, "whole store instructions");
+  float xs[FM];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) xs[fm] = xs_lds[mw + fm * 32 + (lane & 31) - m0];
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int nl = fn * 32 + 8 * q + 4 * (lane >> 5);
+      const float4 w4 = *(const float4*)(ws_lds + (nw + nl - n0));
+      const float4 b4 = *(const float4*)(bias_lds + (nw + nl - n0));
+      const float wsv[4] = {w4.x, w4.y, w4.z, w4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = (((float)(acc[fn][fm][4 * q + r] >> SHIFT) * xs[fm]) * wsv[r]) + bv[r];
+        const uint2 w = ODT == kBF16 ? make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]))
+                                     : make_uint2(pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3]));
+        *(uint2*)(region + (fm * 32 + (lane & 31)) * RS + nl * 2) = w;
+      }
+    }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int c = it * 64 + lane, row = c / CPR, cc = c % CPR;
+    const int m = mw + row, n = nw + cc * 8;
+    const uint4 v = *(const uint4*)(region + row * RS + cc * 16);
+    const uint32_t off = (m < M && n < N) ? (uint32_t)((m * N + n) * 2) : 0x80000000u;
+    __builtin_amdgcn_raw_buffer_store_b128((u32x4){v.x, v.y, v.z, v.w}, orsrc, (int)off, 0, 0);
+  }
+}
+
+// The 4-wave 256x256 kAgpr tile on v_mfma_i32_32x32x32_i8, one tile per
+// workgroup, plain 16-bit epilogue (N % 8 == 0, 2 M N < 2^31).
+template <int STAGES, int ODT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void w4a4_gemm_agpr32_kernel(
+    const int8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
+    const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
+    int K, int nblocks, int kblocks, int tiles_m, int tiles_n) {
+  using E = DmaEngine<256, 256, 2, 2, kAgpr, STAGES>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
+  E e(smem);
+
+  const int tiles = tiles_m * tiles_n;
+  int logical = blockIdx.x;
+  const int per_xcd = tiles / kXcds;
+  if (logical < per_xcd * kXcds) logical = (logical % kXcds) * per_xcd + logical / kXcds;
+  int m0, n0;
+  tile_origin(logical, tiles_m, tiles_n, 256, 256, m0, n0);
+
+  e.set_tile(act, wq, M, K, nblocks, kblocks, m0, n0);
+  e.issue_epi(xscales, wscales, bias, M, N, m0, n0);
+  i32x16 acc[E::FN32][E::FM32];
+#pragma unroll
+  for (int a = 0; a < E::FN32; ++a)
+#pragma unroll
+    for (int b = 0; b < E::FM32; ++b) acc[a][b] = (i32x16){};
+  e.prologue(0, kblocks);
+  e.body_agpr32(0, kblocks, acc);
+  __syncthreads();  // all waves done with the LDS ring before it is reused for output staging
+  const __amdgpu_buffer_rsrc_t orsrc =
+      __builtin_amdgcn_make_buffer_rsrc(out, (short)0, (int)((int64_t)M * N * 2), 0x00020000);
+  epilogue32<ODT, E::TM, E::TN, E::SHIFT>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M, N,
+                                          e.epi_xs(), e.epi_ws(), e.epi_bias(), orsrc, m0, n0);
 }
 
 // Persistent form of the kAgpr data-parallel kernel for multi-round grids with
@@ -1662,6 +1894,20 @@ hipError_t launch_dma(const Plan& plan, const void* act, const float* xs, const 
                            (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, tm,
                            tn, ska, gr);
         return hipGetLastError();
+      }
+      if constexpr (ODT != kF32) {
+        // 32x32x32 MFMAs where the grid leaves CUs idle (at most 7/8 of them
+        // busy): 5-14 % faster there, 4 % slower with every CU busy, where the
+        // shader clock drops further under its higher MFMA rate.  The
+        // gemm_mfma32 tuning override forces it off (0) or on (1).
+        const int m32 = tuning(kTuneGemmMfma32);
+        const bool partial = (int64_t)tm * tn * 8 <= (int64_t)device_cus() * 7;
+        if ((m32 == 1 || (m32 < 0 && partial)) && !gr.residual && N % 8 == 0 && M * N * 2 < ((int64_t)1 << 31)) {
+          hipLaunchKernelGGL((w4a4_gemm_agpr32_kernel<STAGES, ODT>), dim3((unsigned)(tm * tn)), dim3(256), 0,
+                             stream, (const int8_t*)act, xs, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks,
+                             kblocks, tm, tn);
+          return hipGetLastError();
+        }
       }
     }
     if constexpr (ODT != kF32) {

@@ -289,6 +289,8 @@ const char* convrot_last_error(void);
  *   sk_spin_limit    polls                stream-K bounded wait before giving up
  *   gemm_persist     "0" | workgroups     persistent 4-wave W4A4 kernel: never, or always
  *                                         on a grid of that many workgroups
+ *   gemm_mfma32      "0" | "1"            4-wave 256x256 W4A4 tile on 32x32x32 MFMAs: never,
+ *                                         or always (plain 16-bit outputs)
  * Returns CONVROT_ERR_INVALID for an unknown name or a malformed value.
  */
 int convrot_set_tuning(const char* name, const char* value);

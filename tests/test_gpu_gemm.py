@@ -393,3 +393,30 @@ def test_persistent_kernel(orc, dev, tuning, tile, out_dtype, grid, M, K, N):
             _assert_exact(got, want, f"tile {tile} gemm_persist={mode} call {call}")
         outs[mode] = got
     assert np.array_equal(outs[str(grid)], outs["0"])
+
+
+@pytest.mark.parametrize("out_dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("M,K,N", [(300, 128, 264), (1000, 640, 1000), (520, 15360, 1000), (4608, 3072, 3072)])
+def test_mfma32_tile(orc, dev, tuning, out_dtype, M, K, N):
+    """The 4-wave 256x256 tile on 32x32x32 MFMAs (which the automatic plan runs when the
+    tile's grid leaves CUs idle) forced on and off through gemm_mfma32: ragged edges, one and
+    many k-blocks, every output bit-exact against the oracle both ways."""
+    api = _api()
+    tuning.set("gemm_tile", "256x256w2x2")
+    tuning.set("gemm_sk", "0")
+    tuning.set("gemm_smallm_max", "0")
+    rng = np.random.default_rng(M + K + N + 32)
+    a = rng.integers(-8, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    b = rng.normal(size=(N,)).astype(np.float32)
+    want = orc.w4a4_matmul_codes_large(a, w, xs, ws, b, out_dtype)
+    args = (torch.from_numpy(a).to(dev), _dev_u8(orc.codes_to_cdna4(w), dev), torch.from_numpy(xs).to(dev),
+            torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev))
+    dt = {"bfloat16": torch.bfloat16, "float16": torch.float16}[out_dtype]
+    for mode in ("1", "0"):
+        tuning.set("gemm_mfma32", mode)
+        out = api.hip_w4a4_int8_matmul(*args, output_dtype=dt, out_features=N)
+        torch.cuda.synchronize()
+        _assert_exact(from_dev(out), want, f"gemm_mfma32={mode}")
