@@ -18,7 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 # include/convrot_amd.h
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
-PREP_PACKED, PREP_INT8, PREP_ROTATE, PREP_NO_ROTATE = 0, 1, 2, 0x10
+PREP_PACKED, PREP_INT8, PREP_ROTATE, PREP_FP6, PREP_NO_ROTATE = 0, 1, 2, 3, 0x10
 LAYOUT_NK, LAYOUT_KN, LAYOUT_CDNA4 = 0, 1, 2
 ACT_PACKED, ACT_INT8 = 0, 1
 
@@ -45,6 +45,9 @@ SIGNATURES = {
     "convrot_unpack_int4": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "convrot_repack_weight": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _vp]),
     "convrot_cdna4_bytes": (_i64, [_i64, _i64]),
+    "convrot_fp6_bytes": (_i64, [_i64, _i64]),
+    "convrot_weight_fp6": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "convrot_w4a4_gemm_fp6": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_last_error": (ctypes.c_char_p, []),
     "convrot_set_tuning": (_i32, [ctypes.c_char_p, ctypes.c_char_p]),
     "convrot_version": (ctypes.c_char_p, []),

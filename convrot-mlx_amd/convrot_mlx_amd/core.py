@@ -88,17 +88,30 @@ def cdna4_shape(out_features: int, in_features: int) -> tuple[int, int, int]:
 # ------------------------------------------------------------------ preparation
 
 
+def fp6_shape(rows: int, features: int) -> tuple[int, int, int]:
+    """Shape of the FP6 operand blocks of a [rows, features] operand (features % 128 == 0):
+    [features/128, ceil(rows/16), 1536] bytes (layout in include/convrot_amd.h)."""
+    return (features // 128, -(-rows // 16), 1536)
+
+
+def _prep_out(kind: int, rows: int, features: int, like: torch.Tensor) -> torch.Tensor:
+    """Output buffer of a preparation mode (FP6 blocks of a ragged last row block are
+    only partly written; their padding rows only reach GEMM rows that are never stored)."""
+    if kind == nat.PREP_PACKED:
+        return torch.empty((rows, features // 2), dtype=torch.uint8, device=like.device)
+    if kind == nat.PREP_INT8:
+        return torch.empty((rows, features), dtype=torch.int8, device=like.device)
+    if kind == nat.PREP_FP6:
+        return torch.empty(fp6_shape(rows, features), dtype=torch.uint8, device=like.device)
+    return torch.empty((rows, features), dtype=like.dtype, device=like.device)
+
+
 def _prepare(x: torch.Tensor, group_size: int, mode: int) -> tuple[torch.Tensor, torch.Tensor | None]:
     nat.require_device(x)
     x = x.contiguous()
     rows, features = x.shape
     kind = mode & ~nat.PREP_NO_ROTATE
-    if kind == nat.PREP_PACKED:
-        out = torch.empty((rows, features // 2), dtype=torch.uint8, device=x.device)
-    elif kind == nat.PREP_INT8:
-        out = torch.empty((rows, features), dtype=torch.int8, device=x.device)
-    else:
-        out = torch.empty_like(x)
+    out = _prep_out(kind, rows, features, x)
     scales = None if kind == nat.PREP_ROTATE else torch.empty((rows,), dtype=torch.float32, device=x.device)
     lib = nat.load()
     nat.check(
@@ -132,12 +145,7 @@ def _prepare_modulated(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor
     sh, sc, per_vector = _modulation_rows(rows, features, shift, scale)
     sh = sh.to(x.dtype).contiguous()
     sc = sc.to(x.dtype).contiguous()
-    if mode == nat.PREP_PACKED:
-        out = torch.empty((rows, features // 2), dtype=torch.uint8, device=x.device)
-    elif mode == nat.PREP_INT8:
-        out = torch.empty((rows, features), dtype=torch.int8, device=x.device)
-    else:
-        out = torch.empty_like(x)
+    out = _prep_out(mode, rows, features, x)
     scales = None if mode == nat.PREP_ROTATE else torch.empty((rows,), dtype=torch.float32, device=x.device)
     nat.check(
         nat.load().convrot_prepare_modulated(
@@ -203,12 +211,7 @@ def _prepare_gelu(x: torch.Tensor, head: torch.Tensor | None, group_size: int,
         head = _gelu_operand(head)
         head_features = head.shape[1]
     features = head_features + x_features
-    if mode == nat.PREP_PACKED:
-        out = torch.empty((rows, features // 2), dtype=torch.uint8, device=x.device)
-    elif mode == nat.PREP_INT8:
-        out = torch.empty((rows, features), dtype=torch.int8, device=x.device)
-    else:
-        out = torch.empty((rows, features), dtype=x.dtype, device=x.device)
+    out = _prep_out(mode, rows, features, x)
     scales = None if mode == nat.PREP_ROTATE else torch.empty((rows,), dtype=torch.float32, device=x.device)
     nat.check(
         nat.load().convrot_prepare_gelu(

@@ -143,12 +143,21 @@ int64_t convrot_cdna4_bytes(int64_t N, int64_t K) {
   return ((K + 127) / 128) * ((N + 15) / 16) * 1024;
 }
 
+int64_t convrot_fp6_bytes(int64_t R, int64_t K) {
+  if (R < 0 || K < 0 || K % 128) return -1;
+  return (K / 128) * ((R + 15) / 16) * 1536;
+}
+
 int convrot_prepare(const void* x, int dtype, int64_t rows, int64_t features, int group_size, int mode,
                     void* out, float* scales, void* stream) {
   const bool no_rotate = (mode & CONVROT_PREP_NO_ROTATE) != 0;
   const int kind = mode & ~CONVROT_PREP_NO_ROTATE;
-  if (kind != CONVROT_PREP_PACKED && kind != CONVROT_PREP_INT8 && kind != CONVROT_PREP_ROTATE)
+  if (kind != CONVROT_PREP_PACKED && kind != CONVROT_PREP_INT8 && kind != CONVROT_PREP_ROTATE &&
+      kind != CONVROT_PREP_FP6)
     return fail(CONVROT_ERR_INVALID, "unknown ConvRot preparation mode %d", mode);
+  if (kind == CONVROT_PREP_FP6 && features % 128)
+    return fail(CONVROT_ERR_UNSUPPORTED, "FP6 preparation requires features divisible by 128, got %lld",
+                (long long)features);
   if (no_rotate && kind == CONVROT_PREP_ROTATE)
     return fail(CONVROT_ERR_INVALID, "rotate mode cannot skip the rotation");
   if (!valid_dtype(dtype)) return fail(CONVROT_ERR_INVALID, "unsupported activation dtype code %d", dtype);
@@ -183,7 +192,8 @@ int convrot_prepare_modulated(const void* x, int dtype, int64_t rows, int64_t fe
                               float* scales, void* stream) {
   if (mode & CONVROT_PREP_NO_ROTATE)
     return fail(CONVROT_ERR_INVALID, "the modulated producer always rotates (no CONVROT_PREP_NO_ROTATE)");
-  if (mode != CONVROT_PREP_PACKED && mode != CONVROT_PREP_INT8 && mode != CONVROT_PREP_ROTATE)
+  if (mode != CONVROT_PREP_PACKED && mode != CONVROT_PREP_INT8 && mode != CONVROT_PREP_ROTATE &&
+      mode != CONVROT_PREP_FP6)
     return fail(CONVROT_ERR_INVALID, "unknown ConvRot preparation mode %d", mode);
   if (!valid_dtype(dtype)) return fail(CONVROT_ERR_INVALID, "unsupported activation dtype code %d", dtype);
   if (rows < 0 || features <= 0) return fail(CONVROT_ERR_INVALID, "invalid shape (%lld, %lld)", (long long)rows, (long long)features);
@@ -195,6 +205,9 @@ int convrot_prepare_modulated(const void* x, int dtype, int64_t rows, int64_t fe
   if (s > 5) return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot supports groups [4, 16, 64, 256, 1024], got %d", group_size);
   if (features % group_size)
     return fail(CONVROT_ERR_INVALID, "features %lld not divisible by ConvRot group size %d", (long long)features, group_size);
+  if (mode == CONVROT_PREP_FP6 && features % 128)
+    return fail(CONVROT_ERR_UNSUPPORTED, "FP6 preparation requires features divisible by 128, got %lld",
+                (long long)features);
   if (features % 16)
     return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot preparation requires features divisible by 16, got %lld",
                 (long long)features);
@@ -217,7 +230,8 @@ int convrot_prepare_gelu(const void* head, int64_t head_features, int64_t head_s
                          void* out, float* scales, void* stream) {
   if (mode & CONVROT_PREP_NO_ROTATE)
     return fail(CONVROT_ERR_INVALID, "the GELU producer always rotates (no CONVROT_PREP_NO_ROTATE)");
-  if (mode != CONVROT_PREP_PACKED && mode != CONVROT_PREP_INT8 && mode != CONVROT_PREP_ROTATE)
+  if (mode != CONVROT_PREP_PACKED && mode != CONVROT_PREP_INT8 && mode != CONVROT_PREP_ROTATE &&
+      mode != CONVROT_PREP_FP6)
     return fail(CONVROT_ERR_INVALID, "unknown ConvRot preparation mode %d", mode);
   if (!valid_dtype(dtype)) return fail(CONVROT_ERR_INVALID, "unsupported activation dtype code %d", dtype);
   if (rows < 0 || head_features < 0 || x_features <= 0)
@@ -232,6 +246,9 @@ int convrot_prepare_gelu(const void* head, int64_t head_features, int64_t head_s
   if (s > 5) return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot supports groups [4, 16, 64, 256, 1024], got %d", group_size);
   if (features % group_size)
     return fail(CONVROT_ERR_INVALID, "features %lld not divisible by ConvRot group size %d", (long long)features, group_size);
+  if (mode == CONVROT_PREP_FP6 && features % 128)
+    return fail(CONVROT_ERR_UNSUPPORTED, "FP6 preparation requires features divisible by 128, got %lld",
+                (long long)features);
   if (features > kMaxFeatures)
     return fail(CONVROT_ERR_UNSUPPORTED, "fused ConvRot preparation supports at most %lld features, got %lld",
                 (long long)kMaxFeatures, (long long)features);
@@ -285,6 +302,25 @@ int convrot_w4a4_gemm(const void* act, int act_format, const float* xscales, con
   return launch_status(convrot::launch_w4a4_gemm(act, act_format, xscales, qweight, wscales, bias, M, N, K, out,
                                                  out_dtype, (hipStream_t)stream),
                        "convrot_w4a4_gemm");
+}
+
+int convrot_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
+                          const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype, void* stream) {
+  if (M < 0 || N < 0 || K <= 0 || K % 128 || M > INT32_MAX || N > INT32_MAX || K > 300000)
+    return fail(CONVROT_ERR_INVALID, "FP6 W4A4 GEMM: bad shape M=%lld N=%lld K=%lld (K a multiple of 128)",
+                (long long)M, (long long)N, (long long)K);
+  if (out_dtype != CONVROT_DTYPE_BF16 && out_dtype != CONVROT_DTYPE_F16)
+    return fail(CONVROT_ERR_INVALID, "FP6 W4A4 GEMM: 16-bit outputs only");
+  if (N % 8 || M * N * 2 >= ((int64_t)1 << 31))
+    return fail(CONVROT_ERR_INVALID, "FP6 W4A4 GEMM: N must be a multiple of 8 and 2*M*N < 2^31");
+  if (M == 0 || N == 0) return ok();
+  if (!act6 || !xscales || !w6 || !wscales || !out) return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (!aligned(act6, 16) || !aligned(w6, 16) || !aligned(out, 16))
+    return fail(CONVROT_ERR_INVALID, "act6, w6 and out must be 16-byte aligned");
+  const int odt = out_dtype == CONVROT_DTYPE_BF16 ? convrot::kBF16 : convrot::kF16;
+  return launch_status(convrot::launch_w4a4_gemm_fp6(act6, xscales, w6, wscales, bias, M, N, K, out, odt,
+                                                     (hipStream_t)stream),
+                       "convrot_w4a4_gemm_fp6");
 }
 
 namespace {
@@ -470,6 +506,15 @@ int convrot_repack_weight(const uint8_t* in, int in_layout, uint8_t* out, int ou
   if (in == out) return fail(CONVROT_ERR_INVALID, "repack cannot run in place");
   return launch_status(convrot::launch_repack(in, in_layout, out, out_layout, N, K, (hipStream_t)stream),
                        "convrot_repack_weight");
+}
+
+int convrot_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, int32_t* minus8, void* stream) {
+  if (N < 0 || K < 0) return fail(CONVROT_ERR_INVALID, "invalid weight shape (%lld, %lld)", (long long)N, (long long)K);
+  if (N == 0 || K == 0) return ok();
+  if (!cdna4 || !fp6 || !minus8) return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (!aligned(cdna4, 16) || !aligned(fp6, 16)) return fail(CONVROT_ERR_INVALID, "cdna4 and fp6 must be 16-byte aligned");
+  return launch_status(convrot::launch_weight_fp6(cdna4, fp6, N, K, minus8, (hipStream_t)stream),
+                       "convrot_weight_fp6");
 }
 
 }  // extern "C"

@@ -90,6 +90,10 @@ size_t w4a4_plan_workspace_bytes(int act_format, int64_t M, int64_t N, int64_t K
 constexpr size_t kNoAllocScratchBytes = kSkWorkspaceBytes;
 hipError_t noalloc_scratch(hipStream_t stream, Workspace* out);
 
+hipError_t launch_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
+                                const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
+                                hipStream_t stream);
+
 // Few-row W4A4 kernel (int8 activation codes only); launch_w4a4_gemm routes
 // small M here.
 hipError_t launch_w4a4_smallm(const int8_t* act, const float* xscales, const uint8_t* qweight,
@@ -111,5 +115,8 @@ hipError_t launch_unpack_int4(const uint8_t* packed, int64_t rows, int64_t packe
 
 hipError_t launch_repack(const uint8_t* in, int in_layout, uint8_t* out, int out_layout, int64_t N, int64_t K,
                          hipStream_t stream);
+
+hipError_t launch_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, int* minus8,
+                             hipStream_t stream);
 
 }  // namespace convrot

@@ -1099,8 +1099,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // as in `epilogue`, staged through the wave's LDS region and written as 16-byte
 // buffer stores; a chunk outside the M x N output gets an offset past the
 // buffer's range, which the hardware drops.  Needs N % 8 == 0 and 2 M N < 2^31.
-template <int ODT, int TM, int TN, int SHIFT, int FM0, int FM1>
-__device__ __forceinline__ void epilogue_pass(const i32x4 (&acc)[TN / 16][TM / 16], uint8_t* region, int lane,
+// An accumulator element as the float the epilogue scales: int32 sums of
+// codes x 2^SHIFT, or (FP6 kernel) the exact float sum of code products.
+template <int SHIFT>
+__device__ __forceinline__ float acc_value(int v) {
+  return (float)(v >> SHIFT);
+}
+template <int SHIFT>
+__device__ __forceinline__ float acc_value(float v) {
+  return v;
+}
+
+template <int ODT, int TM, int TN, int SHIFT, int FM0, int FM1, class V = i32x4>
+__device__ __forceinline__ void epilogue_pass(const V (&acc)[TN / 16][TM / 16], uint8_t* region, int lane,
                                               int mw, int nw, int M, int N, const float* xs_lds,
                                               const float* ws_lds, const float* bias_lds,
                                               __amdgpu_buffer_rsrc_t orsrc, int m0, int n0) {
@@ -1121,7 +1132,7 @@ __device__ __forceinline__ void epilogue_pass(const i32x4 (&acc)[TN / 16][TM / 1
     for (int fm = FM0; fm < FM1; ++fm) {
       float o[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = (((float)(acc[fn][fm][r] >> SHIFT) * xs[fm - FM0]) * wsv[r]) + bv[r];
+      for (int r = 0; r < 4; ++r) o[r] = ((acc_value<SHIFT>(acc[fn][fm][r]) * xs[fm - FM0]) * wsv[r]) + bv[r];
       const uint2 w = ODT == kBF16 ? make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]))
                                    : make_uint2(pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3]));
       *(uint2*)(region + ((fm - FM0) * 16 + (lane & 15)) * RS + nl * 2) = w;
@@ -1338,6 +1349,236 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     m0 = nm0;
     n0 = nn0;
   }
+}
+
+// ---- FP6 operands
+//
+// Codes in [-7, 7] are exact FP6 (e2m3) values, and the FP6 form of
+// v_mfma_scale_f32_16x16x128_f8f6f4 (unit scales) accumulates their products
+// exactly in float32 while |sum| < 2^24 (K * 49 < 2^24 for every K below
+// 342,000): the sums equal the int32 dots, and the epilogue sees the same
+// values.  The instruction runs at twice the INT8 MFMA rate per cycle.
+//
+// Operand layout, the same for activations (rows) and weights (columns), K a
+// multiple of 128: a k-block is 128 features in four 32-feature groups; a
+// group's 32 six-bit codes (feature i at bits 6i..6i+5) form a 24-byte stream
+// split into a 16-byte head and an 8-byte tail.  [K/128][ceil(R/16)][1536]:
+// the 16 rows (columns) of a block, layout lane L = 16 g + r (row r, group g)
+// holding its head at 16 L and its tail at 1024 + 8 L, i.e. the 6 dwords lane
+// L of the MFMA operand takes.  A tile's k-block is one contiguous run of
+// blocks, moved by whole 1 KB DMAs.
+typedef int i32x6 __attribute__((ext_vector_type(6)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void mfma_fp6(f32x4& c, const i32x6& b, const i32x6& a, int scale) {
+  asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2"
+               : "+a"(c)
+               : "v"(b), "v"(a), "v"(scale)
+               : "memory");
+}
+
+template <int FN, int FM>
+__device__ __forceinline__ void mfma_drain_f(f32x4 (&acc)[FN][FM]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) asm volatile("" : "+a"(acc[fn][fm]));
+}
+
+__device__ __forceinline__ i32x6 fp6_operand(const uint8_t* head, const uint8_t* tail) {
+  const i32x4 h = *(const i32x4*)head;
+  const i32x2 t = *(const i32x2*)tail;
+  return (i32x6){h[0], h[1], h[2], h[3], t[0], t[1]};
+}
+
+// The 4-wave FP6 tile: BM x BN, waves 2 x 2, FN x FM 16 x 16 accumulator
+// blocks per wave in the AGPRs; a 3-stage LDS ring of k-blocks (the tile's
+// activation blocks, then its weight blocks).  Per k-block, one k-step of FN x
+// FM MFMAs in two halves: half 0 (fragment rows 0 .. FM/2-1) reads the
+// block's other activation fragments; a barrier publishes block i+1 and frees
+// the block's stage; half 1 reads block i+1's weights (into the spare set) and
+// first activation fragments, and issues the DMAs of block i+3.
+template <int BM, int BN>
+struct Fp6Engine {
+  static constexpr int NW = 4, STAGES = 3;
+  static constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 16, FN = TN / 16, HM = FM / 2;
+  static constexpr int A_BYTES = (BM / 16) * 1536, B_BYTES = (BN / 16) * 1536, STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int A_DMAS = A_BYTES / 1024, B_DMAS = B_BYTES / 1024, LOADS = A_DMAS + B_DMAS;
+  static constexpr int LPW = LOADS / NW, APW = A_DMAS / NW, BPW = B_DMAS / NW;
+  static constexpr int XS_DMAS = (BM * 4 + 255) / 256, WS_DMAS = (BN * 4 + 255) / 256;
+  static constexpr int EPI_DMAS = XS_DMAS + 2 * WS_DMAS;
+  static constexpr int EPI_OFF = STAGES * STAGE_BYTES;
+  static constexpr int WS_OFF = EPI_OFF + XS_DMAS * 256, BIAS_OFF = WS_OFF + WS_DMAS * 256;
+  static constexpr int SMEM_BYTES = EPI_OFF + EPI_DMAS * 256;
+  static constexpr int RS = TN * 2 + 16, STAGING = TM * RS;
+  static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0 && A_DMAS % NW == 0 && B_DMAS % NW == 0,
+                "whole DMA pieces per wave");
+  static_assert(FM % 2 == 0 && NW * STAGING <= EPI_OFF && SMEM_BYTES <= 160 * 1024, "LDS of one CU");
+  static_assert((STAGES - 1) * LPW <= 63, "vmcnt counts at most 63 DMAs");
+
+  uint8_t* smem;
+  uint32_t smem_addr;
+  int lane, wave, wm, wn;
+  i32x4_sgpr ra, rw;
+  uint32_t vl, a_kstride, w_kstride;
+
+  __device__ __forceinline__ explicit Fp6Engine(uint8_t* s) : smem(s) {
+    smem_addr = (uint32_t)(uintptr_t)s;
+    lane = threadIdx.x & 63;
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    wm = wave / 2;
+    wn = wave % 2;
+  }
+
+  __device__ __forceinline__ void issue_epi(const float* xscales, const float* wscales, const float* bias, int M,
+                                            int N, int m0, int n0) {
+    for (int d = wave; d < EPI_DMAS; d += NW) {
+      const int arr = d < XS_DMAS ? 0 : d < XS_DMAS + WS_DMAS ? 1 : 2;
+      const int q = d - (arr == 0 ? 0 : arr == 1 ? XS_DMAS : XS_DMAS + WS_DMAS);
+      const int off = arr == 0 ? EPI_OFF : arr == 1 ? WS_OFF : BIAS_OFF;
+      const float* base = arr == 0 ? xscales + m0 : arr == 1 ? wscales + n0 : (bias ? bias + n0 : wscales);
+      const int count = arr == 0 ? M - m0 : (arr == 1 || bias) ? N - n0 : 0;
+      const i32x4_sgpr r = buffer_rsrc(base, (uint32_t)count * 4u);
+      dma4(r, (uint32_t)(q * 256 + lane * 4), smem_addr + (uint32_t)(off + q * 256));
+    }
+  }
+
+  // Piece j of a k-block: bytes 1024 j .. of the tile's activation blocks
+  // (pieces 0 .. A_DMAS-1) or weight blocks.  Blocks past the last row
+  // (column) block of the last k-block read as zero; other blocks past the
+  // tile's edge read the next k-block's first blocks, which only reach
+  // accumulators of rows (columns) that are never stored.
+  __device__ __forceinline__ void set_tile(const uint8_t* act, const uint8_t* wq, int M, int K, int nblocks,
+                                           int m0, int n0) {
+    const int kblocks = K / 128, mblocks = (M + 15) / 16;
+    ra = buffer_rsrc(act + (int64_t)(m0 / 16) * 1536, (uint32_t)(((int64_t)kblocks * mblocks - m0 / 16) * 1536));
+    rw = buffer_rsrc(wq + (int64_t)(n0 / 16) * 1536, (uint32_t)(((int64_t)kblocks * nblocks - n0 / 16) * 1536));
+    vl = (uint32_t)lane * 16u;
+    a_kstride = (uint32_t)mblocks * 1536u;
+    w_kstride = (uint32_t)nblocks * 1536u;
+  }
+
+  __device__ __forceinline__ void issue_piece(int kb, int stage, int idx) {
+    const uint32_t base = smem_addr + (uint32_t)(stage * STAGE_BYTES);
+    if (idx < APW) {
+      const uint32_t j = (uint32_t)(wave * APW + idx);
+      uint32_t so = j * 1024u + (uint32_t)kb * a_kstride;
+      asm volatile("" : "+s"(so));
+      dma16(ra, vl + so, base + j * 1024u);
+    } else {
+      const uint32_t j = (uint32_t)(wave * BPW + idx - APW);
+      uint32_t so = j * 1024u + (uint32_t)kb * w_kstride;
+      asm volatile("" : "+s"(so));
+      dma16(rw, vl + so, base + (uint32_t)A_BYTES + j * 1024u);
+    }
+  }
+
+  __device__ __forceinline__ void prologue(int n) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s)
+#pragma unroll
+      for (int p = 0; p < LPW; ++p) issue_piece(min(s, n - 1), s, p);
+  }
+
+  __device__ __forceinline__ i32x6 read_a(int stage, int fm) const {
+    const uint8_t* blk = smem + stage * STAGE_BYTES + (wm * FM + fm) * 1536;
+    return fp6_operand(blk + 16 * lane, blk + 1024 + 8 * lane);
+  }
+  __device__ __forceinline__ i32x6 read_b(int stage, int fn) const {
+    const uint8_t* blk = smem + stage * STAGE_BYTES + A_BYTES + (wn * FN + fn) * 1536;
+    return fp6_operand(blk + 16 * lane, blk + 1024 + 8 * lane);
+  }
+
+  // k-block i (ring stage st) with weight fragments b; bn receives block i+1's.
+  __device__ __forceinline__ void block(int st, int nst, int dma_kb, const i32x6 (&b)[FN], i32x6 (&bn)[FN],
+                                        i32x6 (&a)[FM], f32x4 (&acc)[FN][FM], int scale) {
+    constexpr int NS = HM * FN;  // MFMAs per half
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      const int fm = t / FN, fn = t % FN;
+      mfma_fp6(acc[fn][fm], b[fn], a[fm], scale);
+      if (t % 2 == 1 && t / 2 < HM) a[HM + t / 2] = read_a(st, HM + t / 2);
+    }
+    // the half's fragments stay live to its end, so no read of this half lands
+    // in the registers of an MFMA issued just before it
+#pragma unroll
+    for (int i = 0; i < HM; ++i) asm volatile("" ::"v"(a[i]));
+    wait_vmcnt<LPW>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      const int fm = HM + t / FN, fn = t % FN;
+      mfma_fp6(acc[fn][fm], b[fn], a[fm], scale);
+      if (t < FN) bn[t] = read_b(nst, t);
+      if (t >= FN && t < FN + HM) a[t - FN] = read_a(nst, t - FN);
+#pragma unroll
+      for (int p = 0; p < LPW; ++p)
+        if (t == (p * NS) / LPW) issue_piece(dma_kb, st, p);
+    }
+#pragma unroll
+    for (int i = HM; i < FM; ++i) asm volatile("" ::"v"(a[i]));
+  }
+
+  __device__ __forceinline__ void run(int n, f32x4 (&acc)[FN][FM]) {
+    static_assert(LPW <= 2 * FN * HM, "DMA pieces fit the half");
+    const int scale = 0x7f7f7f7f;  // four E8M0 scales of 1.0
+    i32x6 a[FM], b0[FN], b1[FN];
+    wait_vmcnt<2 * LPW>();  // block 0 (and the epilogue operands) landed
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) b0[fn] = read_b(0, fn);
+#pragma unroll
+    for (int fm = 0; fm < HM; ++fm) a[fm] = read_a(0, fm);
+    const int last = n - 1;
+    int st = 0, i = 0;
+    auto nxt = [](int s) { return s + 1 == STAGES ? 0 : s + 1; };
+    for (; i + 1 < n; i += 2) {
+      block(st, nxt(st), min(i + STAGES, last), b0, b1, a, acc, scale);
+      st = nxt(st);
+      block(st, nxt(st), min(i + 1 + STAGES, last), b1, b0, a, acc, scale);
+      st = nxt(st);
+    }
+    if (i < n) block(st, nxt(st), min(i + STAGES, last), b0, b1, a, acc, scale);
+    mfma_drain_f(acc);
+    wait_vmcnt<0>();
+  }
+};
+
+// The 4-wave FP6 GEMM, one BM x BN tile per workgroup, plain 16-bit epilogue
+// (N % 8 == 0, 2 M N < 2^31).
+template <int BM, int BN, int ODT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void w4a4_gemm_fp6_kernel(
+    const uint8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
+    const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
+    int K, int nblocks, int tiles_m, int tiles_n) {
+  using E = Fp6Engine<BM, BN>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
+  E e(smem);
+  const int tiles = tiles_m * tiles_n;
+  int logical = blockIdx.x;
+  const int per_xcd = tiles / kXcds;
+  if (logical < per_xcd * kXcds) logical = (logical % kXcds) * per_xcd + logical / kXcds;
+  int m0, n0;
+  tile_origin(logical, tiles_m, tiles_n, BM, BN, m0, n0);
+  const int kblocks = K / 128;
+  e.set_tile(act, wq, M, K, nblocks, m0, n0);
+  e.issue_epi(xscales, wscales, bias, M, N, m0, n0);
+  f32x4 acc[E::FN][E::FM];
+#pragma unroll
+  for (int a = 0; a < E::FN; ++a)
+#pragma unroll
+    for (int b = 0; b < E::FM; ++b) acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  e.prologue(kblocks);
+  e.run(kblocks, acc);
+  __syncthreads();  // ring -> output staging
+  const __amdgpu_buffer_rsrc_t orsrc =
+      __builtin_amdgcn_make_buffer_rsrc(out, (short)0, (int)((int64_t)M * N * 2), 0x00020000);
+  epilogue_pass<ODT, E::TM, E::TN, 0, 0, E::FM, f32x4>(
+      acc, smem + e.wave * E::STAGING, e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M, N,
+      (const float*)(smem + E::EPI_OFF), (const float*)(smem + E::WS_OFF), (const float*)(smem + E::BIAS_OFF), orsrc,
+      m0, n0);
 }
 
 // ---- stream-K
@@ -2091,6 +2332,22 @@ int w4a4_workspace_status(const void* workspace, hipStream_t stream, const char*
     }
   }
   return 0;
+}
+
+// FP6-operand W4A4 GEMM (activation and weight layouts above; K % 128 == 0,
+// N % 8 == 0, 16-bit output, 2 M N < 2^31).
+hipError_t launch_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
+                                const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
+                                hipStream_t stream) {
+  const int nblocks = (int)((N + 15) / 16);
+  const int tm = (int)((M + 255) / 256), tn = (int)((N + 255) / 256);
+  if (out_dtype == kBF16)
+    hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<256, 256, kBF16>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, act6,
+                       xscales, w6, wscales, bias, out, (int)M, (int)N, (int)K, nblocks, tm, tn);
+  else
+    hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<256, 256, kF16>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, act6,
+                       xscales, w6, wscales, bias, out, (int)M, (int)N, (int)K, nblocks, tm, tn);
+  return hipGetLastError();
 }
 
 }  // namespace convrot

@@ -217,6 +217,23 @@ __device__ __forceinline__ uint32_t gather_nibbles(uint32_t b0, uint32_t b1, uin
   return __builtin_amdgcn_perm(0u, pairs, 0x0c0c0200u);
 }
 
+// Four A4 codes as their FP6 (e2m3) encodings, packed as a 24-bit field (code
+// j at bits 6j..6j+5).  m0..m3 are code_bits of the ratios' magnitudes (low
+// byte |q| in 0..7) and r0..r3 the ratios, whose signs pick the negative
+// codes; a zero code stays +0 (no e2m3 -0 enters the GEMM's sums).
+__device__ __forceinline__ uint32_t fp6_piece(uint32_t m0, uint32_t m1, uint32_t m2, uint32_t m3, float r0, float r1,
+                                              float r2, float r3) {
+  const uint32_t mag = gather_bytes(m0, m1, m2, m3);
+  const uint32_t pos = __builtin_amdgcn_perm(0x1e1c1a18u, 0x14100800u, mag);  // e2m3 of 0 .. 7
+  const uint32_t neg = __builtin_amdgcn_perm(0x3e3c3a38u, 0x34302800u, mag);  // e2m3 of 0, -1 .. -7
+  // selector 9 / 11: the sign bit of the second / first operand, over the byte
+  const uint32_t sm = __builtin_amdgcn_perm(__float_as_uint(r1), __float_as_uint(r0), 0x0c0c0b09u) |
+                      __builtin_amdgcn_perm(__float_as_uint(r3), __float_as_uint(r2), 0x0b090c0cu);
+  const uint32_t codes = (neg & sm) | (pos & ~sm);
+  const uint32_t y = (codes & 0x003f003fu) | ((codes >> 2) & 0x0fc00fc0u);  // 12-bit pairs at bits 0, 16
+  return (y & 0xfffu) | ((y >> 4) & 0xfff000u);
+}
+
 // Sum of a float64 over the wave (butterfly: every lane ends with the total,
 // added in the same order in every lane).
 __device__ __forceinline__ double wave_sum_f64(double v) {
@@ -442,14 +459,54 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
     const int64_t gbase = row * K + (int64_t)block * 1024 + (lane / LG) * GS;
     const float (&v)[16] = keep[it];
     uint32_t q[16];
+    float rt[16];
     if constexpr (MODE != CONVROT_PREP_ROTATE) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         float ratio;
         if constexpr (DT == kBF16) ratio = round_bf16(v[j] * inv);
         else ratio = scale > 0.0f ? rnd<DT>(v[j] / scale) : 0.0f;  // 0/0 on an all-zero f16 row
-        q[j] = code_bits(ratio);
+        // FP6 keeps |q| and the ratio's sign (rint is symmetric: |rint(c)| = rint(|c|))
+        q[j] = code_bits(MODE == CONVROT_PREP_FP6 ? fabsf(ratio) : ratio);
+        rt[j] = ratio;
       }
+    }
+    if constexpr (MODE == CONVROT_PREP_FP6) {
+      // Each run's four codes are a 24-bit field; 16 consecutive features (a
+      // group's half stream, 12 bytes) are 4 runs: the lane's own 4 runs for
+      // groups up to 16, else run r of the 4 lanes of a quad (lane k holding
+      // features 4k .. 4k+3 of it), which lane r of the quad gathers through
+      // the wave's LDS region.
+      uint32_t pc[4];
+#pragma unroll
+      for (int run = 0; run < 4; ++run)
+        pc[run] = fp6_piece(q[4 * run], q[4 * run + 1], q[4 * run + 2], q[4 * run + 3], rt[4 * run],
+                            rt[4 * run + 1], rt[4 * run + 2], rt[4 * run + 3]);
+      int fh;  // first feature (in the row) of the half this lane writes
+      if constexpr (S >= 3) {
+        uint32_t* xr = (uint32_t*)(lds + wave * kRegionFloats);
+        const int qb = lane & ~3, k = lane & 3;
+        wave_lds_fence();
+#pragma unroll
+        for (int run = 0; run < 4; ++run) xr[(qb + run) * 4 + k] = pc[run];
+        wave_lds_fence();
+        const uint4 g = *(const uint4*)(xr + (qb + k) * 4);
+        pc[0] = g.x, pc[1] = g.y, pc[2] = g.z, pc[3] = g.w;
+        fh = block * 1024 + (lane / LG) * GS + run_index<S, PHF>(p & ~3, k);
+      } else {
+        fh = block * 1024 + lane * 16;
+      }
+      const uint32_t d0 = pc[0] | (pc[1] << 24), d1 = (pc[1] >> 8) | (pc[2] << 16), d2 = (pc[2] >> 16) | (pc[3] << 8);
+      const int64_t mblocks = ((int64_t)gridDim.x + 15) >> 4;
+      uint8_t* blk = (uint8_t*)out + ((int64_t)(fh >> 7) * mblocks + (row >> 4)) * 1536;
+      const int L = ((fh >> 5) & 3) * 16 + (int)(row & 15);
+      if ((fh & 16) == 0) {
+        *(uint3*)(blk + 16 * L) = make_uint3(d0, d1, d2);
+      } else {
+        *(uint32_t*)(blk + 16 * L + 12) = d0;
+        *(uint2*)(blk + 1024 + 8 * L) = make_uint2(d1, d2);
+      }
+      continue;
     }
 #pragma unroll
     for (int run = 0; run < 4; ++run) {
@@ -497,6 +554,8 @@ hipError_t launch_prep_mode(int mode, const void* x, void* out, float* scales, i
   switch (mode) {
     case CONVROT_PREP_PACKED:
       return launch_prep_t<DT, S, NI, CONVROT_PREP_PACKED>(x, out, scales, rows, K, waves, mod, stream);
+    case CONVROT_PREP_FP6:
+      return launch_prep_t<DT, S, NI, CONVROT_PREP_FP6>(x, out, scales, rows, K, waves, mod, stream);
     case CONVROT_PREP_INT8:
       return launch_prep_t<DT, S, NI, CONVROT_PREP_INT8>(x, out, scales, rows, K, waves, mod, stream);
     default: return launch_prep_t<DT, S, NI, CONVROT_PREP_ROTATE>(x, out, scales, rows, K, waves, mod, stream);

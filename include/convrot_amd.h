@@ -58,6 +58,8 @@ extern "C" {
 #define CONVROT_PREP_PACKED 0 /* out: uint8 [rows, features/2] packed A4, + scales */
 #define CONVROT_PREP_INT8 1   /* out: int8  [rows, features] A4 codes,   + scales */
 #define CONVROT_PREP_ROTATE 2 /* out: dtype [rows, features] rotated values (scales unused) */
+#define CONVROT_PREP_FP6 3    /* out: FP6 operand blocks of the A4 codes, + scales; features % 128 == 0
+                               * (layout: convrot_w4a4_gemm_fp6; convrot_fp6_bytes(rows, features)) */
 /* OR-able flag: skip the rotation (quantize_signed_int4_rowwise semantics) */
 #define CONVROT_PREP_NO_ROTATE 0x10
 
@@ -267,6 +269,45 @@ int convrot_repack_weight(const uint8_t* in, int in_layout, uint8_t* out, int ou
 
 /* Size in bytes of a CDNA4-layout weight for an (N, K) weight. */
 int64_t convrot_cdna4_bytes(int64_t N, int64_t K);
+
+/*
+ * FP6 operand path.  An A4 code v in [-7, 7] is exactly representable as an
+ * FP6 (OCP MX e2m3) value, and gfx950's FP6 matrix instruction
+ * (v_mfma_scale_f32_16x16x128_f8f6f4, unit scales) sums products of such codes
+ * exactly in float32 for K < 342,000 (|sum| <= 49 K < 2^24) at twice the INT8
+ * instruction's rate.  So the same GEMM, with the same outputs bit for bit,
+ * runs on operands re-encoded as FP6: no counterpart in the reference, whose
+ * TensorOp multiplies the int4 codes as int8 (core.py:839-874).
+ *
+ * Operand layout (activations by row, weights by output column): blocks of 16
+ * rows x 128 features, 1536 bytes each, ordered [K/128][ceil(R/16)]; lane
+ * L = 16 q + r of a block holds row r's features 32 q + i (i = 0 .. 31) as a
+ * 24-byte stream (feature i at bits 6i .. 6i+5, little-endian), stream bytes
+ * 0 .. 15 at byte 16 L and 16 .. 23 at byte 1024 + 8 L.  K % 128 == 0.
+ */
+
+/* Bytes of the FP6 operand blocks of an (R, K) operand (R rows or columns). */
+int64_t convrot_fp6_bytes(int64_t R, int64_t K);
+
+/*
+ * CDNA4-layout weight -> FP6 operand blocks (an offline conversion, like
+ * convrot_repack_weight).  Adds to *minus8 (a device int32 the caller
+ * zero-fills) the number of -8 codes, which have no FP6 encoding: a weight
+ * with any must stay on the INT8 kernels (the reference's quantizers emit
+ * codes in [-7, 7], core.py:157).
+ */
+int convrot_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, int32_t* minus8,
+                       void* stream);
+
+/*
+ * convrot_w4a4_gemm on FP6 operands: act6 from convrot_prepare(..., CONVROT_PREP_FP6,
+ * ...), w6 from convrot_weight_fp6.  Same epilogue and outputs as
+ * convrot_w4a4_gemm with act_format CONVROT_ACT_INT8.  out_dtype f16 or bf16,
+ * K % 128 == 0, N % 8 == 0, 2 M N < 2^31.
+ */
+int convrot_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6,
+                          const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
+                          void* out, int out_dtype, void* stream);
 
 /* Thread-local message of the last failed call on this thread ("" if none). */
 const char* convrot_last_error(void);

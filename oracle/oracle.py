@@ -414,5 +414,69 @@ def cdna4_to_nk(blocks: np.ndarray, n: int, k: int) -> np.ndarray:
     return pack_signed_int4(cdna4_to_codes(blocks, n, k))
 
 
+# FP6 operand layout (no reference counterpart; defined by this build), for
+# activations (rows) and weights (columns) alike.  A code v in [-7, 7] is
+# stored as its OCP MX e2m3 encoding (sign bit 5, exponent bits 4..3 with bias
+# 1, mantissa bits 2..0), which represents every such integer exactly.  Blocks
+# of 16 rows x 128 features, 1536 bytes each, ordered [K/128][R_pad/16]; lane
+# L = 16*q + r of a block holds row r's features 32*q + i (i = 0..31), feature
+# i at bits 6i..6i+5 of a 192-bit little-endian stream whose bytes 0..15 sit
+# at 16*L and bytes 16..23 at 1024 + 8*L.  Rows are zero-padded to a multiple
+# of 16; K must be a multiple of 128.
+FP6_BLOCK_BYTES = 1536
+E2M3_MAG = np.array([0, 8, 16, 20, 24, 26, 28, 30], np.uint64)  # e2m3 code of |v|, v = 0..7
+
+
+def e2m3_value(code) -> np.ndarray:
+    """Value of an e2m3 code by the format's definition: (-1)^s * 2^(e-1) * (1 + m/8)
+    for e > 0, (-1)^s * m/8 for e = 0."""
+    c = np.asarray(code, dtype=np.int64)
+    s, e, m = (c >> 5) & 1, (c >> 3) & 3, c & 7
+    mag = np.where(e > 0, np.ldexp(1.0 + m / 8.0, (e - 1).astype(np.int32)), m / 8.0)
+    return np.where(s == 1, -mag, mag)
+
+
+def e2m3_code(v) -> np.ndarray:
+    """e2m3 code of integers in [-7, 7]."""
+    v = np.asarray(v, dtype=np.int64)
+    if v.size and (v.min() < -7 or v.max() > 7):
+        raise ValueError("e2m3 holds the integers -7 .. 7 only")
+    return E2M3_MAG[np.abs(v)] | np.where(v < 0, 32, 0).astype(np.uint64)
+
+
+def codes_to_fp6(codes: np.ndarray) -> np.ndarray:
+    """Row-major int8 codes [R, K] (K % 128 == 0) -> FP6 blocks [K/128, R_pad/16, 1536]."""
+    R, K = codes.shape
+    if K % 128:
+        raise ValueError(f"FP6 layout requires K divisible by 128, got {K}")
+    rb, kb = -(-R // 16), K // 128
+    full = np.zeros((rb * 16, K), np.int8)
+    full[:R] = codes
+    c = e2m3_code(full).reshape(rb, 16, kb, 4, 4, 8)  # rblk, r, kblk, q, chunk of 8 fields, field
+    words = (c << (6 * np.arange(8, dtype=np.uint64))).sum(-1)  # 48-bit chunks (disjoint bit fields)
+    stream = ((words[..., None] >> (8 * np.arange(6, dtype=np.uint64))) & 0xFF).astype(np.uint8)
+    stream = stream.reshape(rb, 16, kb, 4, 24).transpose(2, 0, 3, 1, 4)  # kblk, rblk, q, r, 24
+    head = stream[..., :16].reshape(kb, rb, 1024)
+    tail = stream[..., 16:].reshape(kb, rb, 512)
+    return np.ascontiguousarray(np.concatenate([head, tail], axis=-1))
+
+
+def fp6_to_codes(blocks: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """Exact inverse of codes_to_fp6, dropping the padding (every code must be an integer)."""
+    kb, rb, _ = blocks.shape
+    head = blocks[..., :1024].reshape(kb, rb, 4, 16, 16)
+    tail = blocks[..., 1024:].reshape(kb, rb, 4, 16, 8)
+    stream = np.concatenate([head, tail], axis=-1).astype(np.uint64)  # kblk, rblk, q, r, 24
+    bits = np.zeros(stream.shape[:-1], dtype=object)
+    for j in range(24):
+        bits = bits + (stream[..., j].astype(object) << (8 * j))
+    fields = np.stack([(bits >> (6 * i)) & 63 for i in range(32)], axis=-1).astype(np.int64)
+    vals = e2m3_value(fields)
+    if not np.array_equal(vals, np.round(vals)):
+        raise ValueError("FP6 blocks hold a code that is not an integer")
+    full = vals.astype(np.int64).transpose(1, 3, 0, 2, 4).reshape(rb * 16, kb * 128)
+    return full[:rows, :k].astype(np.int8)
+
+
 def cpu_threads() -> int:
     return len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)

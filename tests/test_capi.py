@@ -63,8 +63,8 @@ def test_constants_match_binding():
 
     c = header_constants()
     assert (c["CONVROT_DTYPE_F32"], c["CONVROT_DTYPE_F16"], c["CONVROT_DTYPE_BF16"]) == (n.DTYPE_F32, n.DTYPE_F16, n.DTYPE_BF16)
-    assert (c["CONVROT_PREP_PACKED"], c["CONVROT_PREP_INT8"], c["CONVROT_PREP_ROTATE"], c["CONVROT_PREP_NO_ROTATE"]) == (
-        n.PREP_PACKED, n.PREP_INT8, n.PREP_ROTATE, n.PREP_NO_ROTATE)
+    assert (c["CONVROT_PREP_PACKED"], c["CONVROT_PREP_INT8"], c["CONVROT_PREP_ROTATE"], c["CONVROT_PREP_FP6"],
+            c["CONVROT_PREP_NO_ROTATE"]) == (n.PREP_PACKED, n.PREP_INT8, n.PREP_ROTATE, n.PREP_FP6, n.PREP_NO_ROTATE)
     assert (c["CONVROT_LAYOUT_NK"], c["CONVROT_LAYOUT_KN"], c["CONVROT_LAYOUT_CDNA4"]) == (n.LAYOUT_NK, n.LAYOUT_KN, n.LAYOUT_CDNA4)
     assert (c["CONVROT_ACT_PACKED"], c["CONVROT_ACT_INT8"]) == (n.ACT_PACKED, n.ACT_INT8)
     assert (c["CONVROT_OK"], c["CONVROT_ERR_INVALID"], c["CONVROT_ERR_UNSUPPORTED"], c["CONVROT_ERR_LAUNCH"]) == (

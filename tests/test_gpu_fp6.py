@@ -1,0 +1,218 @@
+"""GPU parity of the FP6 operand path: the CDNA4 -> FP6 weight conversion, the preparation
+kernel's FP6 output and the FP6-operand W4A4 GEMM, each bit for bit against the CPU oracle
+(oracle.codes_to_fp6 for the layouts, w4a4_matmul_codes_large for the products), and the
+complete FP6 path against the INT8 path.
+
+The FP6 layout and e2m3 encoding are this build's own (no reference counterpart); the codes
+they carry are the reference's A4 / W4 codes (core.py:149-167, 514-527), and the products
+follow reference_w4a4_matmul (core.py:1155-1171) as the INT8 kernels do.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _util import from_dev, normal_input, outlier_input, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _nat():
+    from convrot_mlx_amd import _native as nat
+
+    return nat
+
+
+def _u8(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _weight_fp6(nat, wq_dev, N, K, dev):
+    out = torch.zeros(int(nat.load().convrot_fp6_bytes(N, K)), dtype=torch.uint8, device=dev)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    nat.check(nat.load().convrot_weight_fp6(nat.ptr(wq_dev), nat.ptr(out), N, K, nat.ptr(bad), nat.stream_of(dev)))
+    torch.cuda.synchronize()
+    return out, int(bad.item())
+
+
+def _prep_fp6(nat, xd, G, mode, dev):
+    rows, K = xd.shape
+    out = torch.zeros(int(nat.load().convrot_fp6_bytes(rows, K)), dtype=torch.uint8, device=dev)
+    scales = torch.empty(rows, dtype=torch.float32, device=dev)
+    nat.check(nat.load().convrot_prepare(nat.ptr(xd), nat.dtype_code(xd.dtype), rows, K, G, mode, nat.ptr(out),
+                                         nat.ptr(scales), nat.stream_of(dev)))
+    torch.cuda.synchronize()
+    return out, scales
+
+
+def _gemm_fp6(nat, a6, xs, w6, ws, b, M, N, K, dtype, dev):
+    out = torch.empty((M, N), dtype=dtype, device=dev)
+    nat.check(nat.load().convrot_w4a4_gemm_fp6(nat.ptr(a6), nat.ptr(xs), nat.ptr(w6), nat.ptr(ws), nat.ptr(b), M, N, K,
+                                               nat.ptr(out), nat.dtype_code(dtype), nat.stream_of(dev)))
+    torch.cuda.synchronize()
+    return out
+
+
+def _assert_exact(got, want, label):
+    bad = int((got != want).sum())
+    assert bad == 0, f"{label}: {bad} of {want.size} differ"
+
+
+@pytest.mark.parametrize("N,K", [(46, 128), (264, 384), (3072, 3072), (1000, 15360)])
+def test_weight_fp6_matches_oracle(orc, dev, N, K):
+    """CDNA4 weight -> FP6 blocks: every byte as the oracle's layout of the same codes
+    (padding columns included), and no -8 reported."""
+    nat = _nat()
+    rng = np.random.default_rng(N + K)
+    w = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
+    got, bad = _weight_fp6(nat, _u8(orc.codes_to_cdna4(w), dev), N, K, dev)
+    assert bad == 0
+    want = orc.codes_to_fp6(w).reshape(-1)
+    _assert_exact(from_dev(got), want, f"weight {N}x{K}")
+    assert np.array_equal(orc.fp6_to_codes(from_dev(got).reshape(K // 128, -1, 1536), N, K), w)
+
+
+def test_weight_fp6_counts_minus8(orc, dev):
+    """-8 codes (outside e2m3) are counted, so the caller keeps such a weight on the INT8 path."""
+    nat = _nat()
+    rng = np.random.default_rng(8)
+    w = rng.integers(-7, 8, size=(64, 256), dtype=np.int8)
+    w[3, 17] = -8
+    w[60, 255] = -8
+    w[0, 0] = -8
+    _, bad = _weight_fp6(nat, _u8(orc.codes_to_cdna4(w), dev), 64, 256, dev)
+    assert bad == 3
+
+
+@pytest.mark.parametrize("dtype,G,rows,K", [
+    ("bfloat16", 256, 37, 3072),     # config-3 group, ragged rows
+    ("bfloat16", 64, 300, 2688),     # config-2 group, K = 21 k-blocks
+    ("float16", 16, 19, 512),
+    ("float32", 4, 17, 256),
+    ("bfloat16", 1024, 33, 2048),
+    ("bfloat16", 256, 1536, 3072),   # the reference tests' route shape (test_core.py:128-137)
+    ("bfloat16", 256, 20, 15360),
+])
+def test_prepare_fp6_matches_oracle(orc, dev, dtype, G, rows, K):
+    """Fused preparation with FP6 output: the oracle's A4 codes in the FP6 layout, byte for
+    byte (rows padded with zero blocks), and the oracle's row scales."""
+    nat = _nat()
+    x = outlier_input(rows * 7 + K, (rows, K), dtype, orc)
+    codes, scales = orc.prepare_codes(x, dtype, G)
+    got, s = _prep_fp6(nat, to_dev(x, dtype, dev), G, nat.PREP_FP6, dev)
+    assert np.array_equal(from_dev(s), scales), "scales differ"
+    _assert_exact(from_dev(got), orc.codes_to_fp6(codes).reshape(-1), f"{dtype} G={G} {rows}x{K}")
+
+
+def test_prepare_fp6_without_rotation(orc, dev):
+    """CONVROT_PREP_FP6 | NO_ROTATE: quantize_signed_int4_rowwise codes in the FP6 layout."""
+    nat = _nat()
+    x = normal_input(1234, (21, 384), "bfloat16", orc)
+    codes, scales = orc.quantize_rowwise_codes(x, "bfloat16")
+    got, s = _prep_fp6(nat, to_dev(x, "bfloat16", dev), 256, nat.PREP_FP6 | nat.PREP_NO_ROTATE, dev)
+    assert np.array_equal(from_dev(s), scales)
+    _assert_exact(from_dev(got), orc.codes_to_fp6(codes).reshape(-1), "no-rotate")
+
+
+def test_prepare_fp6_zero_and_tiny_rows(orc, dev):
+    """An all-zero row and rows of tiny values: every code 0 is +0 in e2m3 (no -0 code)."""
+    nat = _nat()
+    x = normal_input(77, (18, 1024), "bfloat16", orc)
+    x[0] = 0
+    x[5] = orc.from_f32(np.full(1024, -1e-30, np.float32), "bfloat16")
+    codes, scales = orc.prepare_codes(x, "bfloat16", 256)
+    got, s = _prep_fp6(nat, to_dev(x, "bfloat16", dev), 256, nat.PREP_FP6, dev)
+    assert np.array_equal(from_dev(s), scales)
+    _assert_exact(from_dev(got), orc.codes_to_fp6(codes).reshape(-1), "zero rows")
+
+
+def test_modulated_and_gelu_producers_fp6(orc, dev):
+    """The fused producers' FP6 output equals their INT8 output in the FP6 layout."""
+    nat = _nat()
+    from convrot_mlx_amd import core
+
+    rows, K = 48, 3072  # whole 16-row blocks: the library leaves padding rows of a ragged last block unwritten
+    x = to_dev(outlier_input(5, (rows, K), "bfloat16", orc), "bfloat16", dev)
+    shift = torch.randn(K, device=dev).to(torch.bfloat16)
+    scale = torch.randn(K, device=dev).to(torch.bfloat16)
+    q8, s8 = core._prepare_modulated(x, shift, scale, 256, nat.PREP_INT8, 1e-6)
+    q6, s6 = core._prepare_modulated(x, shift, scale, 256, nat.PREP_FP6, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(s8, s6)
+    want = orc.codes_to_fp6(from_dev(q8)).reshape(-1)
+    _assert_exact(from_dev(q6).reshape(-1)[: want.size], want, "modulated")
+    head = to_dev(outlier_input(6, (rows, 3072), "bfloat16", orc), "bfloat16", dev)
+    g8, t8 = core._prepare_gelu(x, head, 256, nat.PREP_INT8)
+    g6, t6 = core._prepare_gelu(x, head, 256, nat.PREP_FP6)
+    torch.cuda.synchronize()
+    assert torch.equal(t8, t6)
+    want = orc.codes_to_fp6(from_dev(g8)).reshape(-1)
+    _assert_exact(from_dev(g6).reshape(-1)[: want.size], want, "gelu")
+
+
+@pytest.mark.parametrize("out_dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("M,K,N", [(300, 128, 264), (37, 384, 48), (1000, 640, 1000), (520, 1536, 1000),
+                                   (4608, 3072, 3072)])
+def test_fp6_gemm_matches_oracle(orc, dev, out_dtype, M, K, N):
+    """FP6-operand GEMM, every output bit-exact against the oracle: ragged tiles, one and many
+    k-blocks, all-zero activation rows (+0 sums) and a row of extreme codes."""
+    nat = _nat()
+    rng = np.random.default_rng(M + K + N)
+    a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
+    a[1] = 0
+    a[2] = 7
+    w[3] = -7
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    b = rng.normal(size=(N,)).astype(np.float32)
+    b[:4] = 0.0
+    dt = {"bfloat16": torch.bfloat16, "float16": torch.float16}[out_dtype]
+    out = _gemm_fp6(nat, _u8(orc.codes_to_fp6(a), dev), _u8(xs, dev), _u8(orc.codes_to_fp6(w), dev), _u8(ws, dev),
+                    _u8(b, dev), M, N, K, dt, dev)
+    _assert_exact(from_dev(out), orc.w4a4_matmul_codes_large(a, w, xs, ws, b, out_dtype), f"{M}x{K}x{N}")
+
+
+def test_fp6_gemm_largest_sums(orc, dev):
+    """K = 15360 with runs of +-7 * +-7: sums of +-752640 (the largest at config 3) stay exact."""
+    nat = _nat()
+    M, K, N = 64, 15360, 64
+    rng = np.random.default_rng(15360)
+    a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
+    a[:8] = 7
+    a[8:16] = -7
+    w[:8] = 7
+    w[8:16] = -7
+    xs = np.ones(M, np.float32)
+    ws = np.ones(N, np.float32)
+    b = np.zeros(N, np.float32)
+    out = _gemm_fp6(nat, _u8(orc.codes_to_fp6(a), dev), _u8(xs, dev), _u8(orc.codes_to_fp6(w), dev), _u8(ws, dev),
+                    _u8(b, dev), M, N, K, torch.bfloat16, dev)
+    _assert_exact(from_dev(out), orc.w4a4_matmul_codes_large(a, w, xs, ws, b, "bfloat16"), "largest sums")
+
+
+@pytest.mark.parametrize("M,G,K,N", [(1536, 256, 3072, 9216), (4608, 256, 12288, 3072), (1000, 64, 3072, 1000)])
+def test_fp6_complete_path_equals_int8_path(orc, dev, M, G, K, N):
+    """prep(FP6) -> FP6 GEMM on the FP6 conversion of a quantized weight gives the INT8 path's
+    output (prep(INT8) -> convrot_w4a4_gemm) bit for bit."""
+    nat = _nat()
+    from convrot_mlx_amd import core
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(M + K + N)
+    w = torch.randn((N, K), generator=gen, device=dev) * 0.02
+    qw, ws = core.quantize_convrot_weight(w, G)
+    wq = core.repack_nk_weight_for_cdna4(qw)
+    x = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+    bias = torch.randn(N, generator=gen, device=dev) * 0.02
+    q8, xs8 = core._prepare(x, G, nat.PREP_INT8)
+    want = core.hip_w4a4_int8_matmul(q8, wq, xs8, ws, bias, output_dtype=torch.bfloat16, out_features=N)
+    w6, bad = _weight_fp6(nat, wq, N, K, dev)
+    assert bad == 0
+    a6, xs6 = _prep_fp6(nat, x, G, nat.PREP_FP6, dev)
+    got = _gemm_fp6(nat, a6, xs6, w6, ws.float().contiguous(), bias.float().contiguous(), M, N, K, torch.bfloat16, dev)
+    assert torch.equal(xs6, xs8)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))

@@ -277,6 +277,48 @@ def test_cdna4_layout_brute_force(orc):
     assert np.array_equal(orc.cdna4_to_codes(blocks, N, K), v)
 
 
+def test_e2m3_codes_are_the_integers(orc):
+    """The e2m3 codes of -7 .. 7, decoded by the format's definition (bias 1, 3 mantissa
+    bits), are the integers themselves; no two share a code; 0 has no sign bit; and the
+    decoder agrees with a scan of all 64 codes for the integer-valued ones."""
+    v = np.arange(-7, 8)
+    c = orc.e2m3_code(v)
+    assert np.array_equal(orc.e2m3_value(c), v.astype(np.float64))
+    assert len(set(c.tolist())) == 15 and int(c[7]) == 0
+    all_codes = np.arange(64)
+    vals = orc.e2m3_value(all_codes)
+    ints = {int(x): int(k) for k, x in zip(all_codes, vals) if x == np.round(x) and not (x == 0 and k)}
+    assert ints == {int(x): int(k) for x, k in zip(v, c)}
+    with pytest.raises(ValueError):
+        orc.e2m3_code(np.array([-8]))
+
+
+def test_fp6_layout_brute_force(orc):
+    """Every (r, k) lands in block [k//128][r//16], lane L = 16*(k%128//32) + r%16, as the
+    6 bits at 6*(k%32) of the lane's 24-byte stream (bytes 0..15 at 16*L, 16..23 at
+    1024 + 8*L), built bit by bit here; the lanes hold the same features as the CDNA4
+    layout's lanes."""
+    rng = np.random.default_rng(6)
+    R, K = 37, 256
+    v = rng.integers(-7, 8, size=(R, K), dtype=np.int8)
+    blocks = orc.codes_to_fp6(v)
+    assert blocks.shape == (2, 3, 1536)
+    want = np.zeros_like(blocks)
+    for r in range(R):
+        for k in range(K):
+            kb, kk = divmod(k, 128)
+            L = 16 * (kk // 32) + r % 16
+            code = int(orc.e2m3_code(np.array([v[r, k]]))[0])
+            for b in range(6):
+                bit = 6 * (kk % 32) + b
+                byte = 16 * L + bit // 8 if bit < 128 else 1024 + 8 * L + (bit - 128) // 8
+                want[kb, r // 16, byte] |= ((code >> b) & 1) << (bit % 8)
+    assert np.array_equal(blocks, want)
+    assert np.array_equal(orc.fp6_to_codes(blocks, R, K), v)
+    cd = orc.cdna4_to_codes(orc.codes_to_cdna4(v), R, K)
+    assert np.array_equal(cd, v)  # same (row, feature) -> lane assignment: lane 16*(k%128//32) + r%16
+
+
 # ------------------------------------------------------------------ matmuls
 
 
