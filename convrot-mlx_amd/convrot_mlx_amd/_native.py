@@ -46,7 +46,7 @@ SIGNATURES = {
     "convrot_repack_weight": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _vp]),
     "convrot_cdna4_bytes": (_i64, [_i64, _i64]),
     "convrot_fp6_bytes": (_i64, [_i64, _i64]),
-    "convrot_weight_fp6": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "convrot_weight_fp6": (_i32, [_vp, _vp, _i64, _i64, _vp]),
     "convrot_w4a4_gemm_fp6": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_last_error": (ctypes.c_char_p, []),
     "convrot_set_tuning": (_i32, [ctypes.c_char_p, ctypes.c_char_p]),

@@ -508,12 +508,12 @@ int convrot_repack_weight(const uint8_t* in, int in_layout, uint8_t* out, int ou
                        "convrot_repack_weight");
 }
 
-int convrot_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, int32_t* minus8, void* stream) {
+int convrot_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, void* stream) {
   if (N < 0 || K < 0) return fail(CONVROT_ERR_INVALID, "invalid weight shape (%lld, %lld)", (long long)N, (long long)K);
   if (N == 0 || K == 0) return ok();
-  if (!cdna4 || !fp6 || !minus8) return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (!cdna4 || !fp6) return fail(CONVROT_ERR_INVALID, "null pointer argument");
   if (!aligned(cdna4, 16) || !aligned(fp6, 16)) return fail(CONVROT_ERR_INVALID, "cdna4 and fp6 must be 16-byte aligned");
-  return launch_status(convrot::launch_weight_fp6(cdna4, fp6, N, K, minus8, (hipStream_t)stream),
+  return launch_status(convrot::launch_weight_fp6(cdna4, fp6, N, K, (hipStream_t)stream),
                        "convrot_weight_fp6");
 }
 

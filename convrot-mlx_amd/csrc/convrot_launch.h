@@ -116,7 +116,6 @@ hipError_t launch_unpack_int4(const uint8_t* packed, int64_t rows, int64_t packe
 hipError_t launch_repack(const uint8_t* in, int in_layout, uint8_t* out, int out_layout, int64_t N, int64_t K,
                          hipStream_t stream);
 
-hipError_t launch_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, int* minus8,
-                             hipStream_t stream);
+hipError_t launch_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, hipStream_t stream);
 
 }  // namespace convrot

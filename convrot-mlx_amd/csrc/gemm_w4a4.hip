@@ -1353,10 +1353,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
 // ---- FP6 operands
 //
-// Codes in [-7, 7] are exact FP6 (e2m3) values, and the FP6 form of
-// v_mfma_scale_f32_16x16x128_f8f6f4 (unit scales) accumulates their products
-// exactly in float32 while |sum| < 2^24 (K * 49 < 2^24 for every K below
-// 342,000): the sums equal the int32 dots, and the epilogue sees the same
+// A code v in [-8, 7] is stored as the FP6 (e2m3) encoding of v/8: the
+// subnormal with mantissa |v| for |v| <= 7 (a sign-magnitude field), -1.0 for
+// -8.  The FP6 form of v_mfma_scale_f32_16x16x128_f8f6f4 with both operand
+// scales 2^3 multiplies (v/8 * 8) (w/8 * 8) = v w exactly and accumulates in
+// float32, exact while |sum| < 2^24 (K * 64 < 2^24 for every K below
+// 262,144): the sums equal the int32 dots, and the epilogue sees the same
 // values.  The instruction runs at twice the INT8 MFMA rate per cycle.
 //
 // Operand layout, the same for activations (rows) and weights (columns), K a
@@ -1523,7 +1525,7 @@ struct Fp6Engine {
 
   __device__ __forceinline__ void run(int n, f32x4 (&acc)[FN][FM]) {
     static_assert(LPW <= 2 * FN * HM, "DMA pieces fit the half");
-    const int scale = 0x7f7f7f7f;  // four E8M0 scales of 1.0
+    const int scale = (int)0x82828282u;  // E8M0 scales of 2^3 (one byte per 32-feature group)
     i32x6 a[FM], b0[FN], b1[FN];
     wait_vmcnt<2 * LPW>();  // block 0 (and the epilogue operands) landed
     __builtin_amdgcn_s_barrier();

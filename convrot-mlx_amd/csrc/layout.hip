@@ -107,24 +107,23 @@ __global__ void repack_kernel(const uint8_t* __restrict__ in, int in_layout, uin
   out[i] = (uint8_t)(lo | (hi << 4));
 }
 
-// e2m3 codes of two's-complement nibbles, one byte per nibble value: 0 .. 7
-// and (indexed by n & 7) 8 .. 15, i.e. -8 .. -1.  -8 has no e2m3 code (entry 0;
-// the kernel counts it).
-constexpr uint64_t kE2m3Pos = 0x1e1c1a1814100800ull;  // 0, 1 .. 7
-constexpr uint64_t kE2m3Neg = 0x283034383a3c3e00ull;  // -8 (none), -7 .. -1
+// FP6 fields of two's-complement nibbles, one byte per nibble value: 0 .. 7
+// and (indexed by n & 7) 8 .. 15, i.e. -8 .. -1.  A code v is the e2m3
+// encoding of v/8: the sign-magnitude subnormal for |v| <= 7, and -1.0
+// (0x28) for -8.
+constexpr uint64_t kFp6Pos = 0x0706050403020100ull;  // 0, 1 .. 7
+constexpr uint64_t kFp6Neg = 0x2122232425262728ull;  // -8, -7 .. -1
 
 // CDNA4 int4 weight -> FP6 operand blocks, one thread per 16-byte lane L of a
 // 1024-byte CDNA4 block: its 32 nibbles (features 32 q + 8 c + j + 4 h at
-// dword c, byte j, half h) become the lane's 24-byte e2m3 stream (feature i at
+// dword c, byte j, half h) become the lane's 24-byte FP6 stream (feature i at
 // bits 6 i), head at 16 L and tail at 1024 + 8 L of the 1536-byte FP6 block.
-__global__ void fp6_weight_kernel(const uint4* __restrict__ in, uint8_t* __restrict__ out, int64_t lanes,
-                                  int* __restrict__ minus8) {
+__global__ void fp6_weight_kernel(const uint4* __restrict__ in, uint8_t* __restrict__ out, int64_t lanes) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= lanes) return;
   const uint4 v = in[t];
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
   uint64_t s[3] = {0, 0, 0};
-  int bad = 0;
 #pragma unroll
   for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -132,8 +131,7 @@ __global__ void fp6_weight_kernel(const uint4* __restrict__ in, uint8_t* __restr
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t n = (w[c] >> (8 * j + 4 * h)) & 15u;
-        bad += n == 8u;
-        const uint64_t code = (((n & 8u) ? kE2m3Neg : kE2m3Pos) >> (8 * (n & 7u))) & 0x3fu;
+        const uint64_t code = (((n & 8u) ? kFp6Neg : kFp6Pos) >> (8 * (n & 7u))) & 0x3fu;
         const int bit = 6 * (8 * c + 4 * h + j);
         s[bit >> 6] |= code << (bit & 63);
         if ((bit & 63) > 58) s[(bit >> 6) + 1] |= code >> (64 - (bit & 63));
@@ -142,7 +140,6 @@ __global__ void fp6_weight_kernel(const uint4* __restrict__ in, uint8_t* __restr
   const int L = (int)(t & 63);
   *(uint4*)(o + 16 * L) = make_uint4((uint32_t)s[0], (uint32_t)(s[0] >> 32), (uint32_t)s[1], (uint32_t)(s[1] >> 32));
   *(uint2*)(o + 1024 + 8 * L) = make_uint2((uint32_t)s[2], (uint32_t)(s[2] >> 32));
-  if (bad) atomicAdd(minus8, bad);
 }
 
 inline unsigned grid_for(int64_t total, int block) { return (unsigned)((total + block - 1) / block); }
@@ -184,12 +181,11 @@ hipError_t launch_repack(const uint8_t* in, int in_layout, uint8_t* out, int out
   return hipGetLastError();
 }
 
-hipError_t launch_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, int* minus8,
-                             hipStream_t stream) {
+hipError_t launch_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, hipStream_t stream) {
   const int64_t lanes = ((K + 127) / 128) * ((N + 15) / 16) * 64;
   if (lanes == 0) return hipSuccess;
   hipLaunchKernelGGL(fp6_weight_kernel, dim3(grid_for(lanes, 256)), dim3(256), 0, stream, (const uint4*)cdna4, fp6,
-                     lanes, minus8);
+                     lanes);
   return hipGetLastError();
 }
 

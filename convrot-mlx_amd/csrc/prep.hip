@@ -217,21 +217,55 @@ __device__ __forceinline__ uint32_t gather_nibbles(uint32_t b0, uint32_t b1, uin
   return __builtin_amdgcn_perm(0u, pairs, 0x0c0c0200u);
 }
 
-// Four A4 codes as their FP6 (e2m3) encodings, packed as a 24-bit field (code
-// j at bits 6j..6j+5).  m0..m3 are code_bits of the ratios' magnitudes (low
-// byte |q| in 0..7) and r0..r3 the ratios, whose signs pick the negative
-// codes; a zero code stays +0 (no e2m3 -0 enters the GEMM's sums).
+// FP6 operand codes.  A code v is stored as the e2m3 encoding of v/8: for
+// |v| <= 7 that is the subnormal with mantissa |v| (sign bit 5, exponent bits
+// 4..3 zero), so the field is the sign-magnitude form of v; the GEMM's MFMA
+// scales both operands by 2^3 and sums the exact products v*w.  Zero codes
+// are +0.
+//
+// Four A4 codes as FP6 fields, packed as a 24-bit field (code j at bits
+// 6j..6j+5).  m0..m3 are code_bits of the ratios' magnitudes (low byte |q| in
+// 0..7) and r0..r3 the ratios, whose signs pick the negative codes.
 __device__ __forceinline__ uint32_t fp6_piece(uint32_t m0, uint32_t m1, uint32_t m2, uint32_t m3, float r0, float r1,
                                               float r2, float r3) {
   const uint32_t mag = gather_bytes(m0, m1, m2, m3);
-  const uint32_t pos = __builtin_amdgcn_perm(0x1e1c1a18u, 0x14100800u, mag);  // e2m3 of 0 .. 7
-  const uint32_t neg = __builtin_amdgcn_perm(0x3e3c3a38u, 0x34302800u, mag);  // e2m3 of 0, -1 .. -7
+  const uint32_t pos = mag;                                                    // 0 .. 7
+  const uint32_t neg = __builtin_amdgcn_perm(0x27262524u, 0x23222100u, mag);  // 0, -1 .. -7
   // selector 9 / 11: the sign bit of the second / first operand, over the byte
   const uint32_t sm = __builtin_amdgcn_perm(__float_as_uint(r1), __float_as_uint(r0), 0x0c0c0b09u) |
                       __builtin_amdgcn_perm(__float_as_uint(r3), __float_as_uint(r2), 0x0b090c0cu);
   const uint32_t codes = (neg & sm) | (pos & ~sm);
   const uint32_t y = (codes & 0x003f003fu) | ((codes >> 2) & 0x0fc00fc0u);  // 12-bit pairs at bits 0, 16
   return (y & 0xfffu) | ((y >> 4) & 0xfff000u);
+}
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x32 __attribute__((ext_vector_type(32)));
+typedef int i32x6 __attribute__((ext_vector_type(6)));
+
+// A pair of bf16 ratios with the sign cleared on each negative one of
+// magnitude at most 0.5 (bits 0x3f00), i.e. on each ratio whose code
+// rint(ratio) is 0: bit 15 of h + 0x40ff (per half, mod 2^16) is set for
+// exactly those negative halves (and for positive halves above 0.5, whose
+// sign bit is already clear).
+__device__ __forceinline__ uint32_t zero_code_sign_fix(uint32_t h) {
+  const u16x2 s = __builtin_bit_cast(u16x2, h) + (u16x2){0x40ff, 0x40ff};
+  return h & ~(__builtin_bit_cast(uint32_t, s) & 0x80008000u);
+}
+
+// FP6 fields of 16 bf16 ratios (8 packed pairs, lowest feature first), whose
+// magnitudes are at most 7.04 (as every bf16 ratio is, the scale being
+// bf16(absmax / 7)): v_cvt_scalef32_pk32_fp6_bf16 divides by the scale 8 and
+// rounds to the e2m3 grid of eighths with ties to even, so field i is
+// rint(ratio_i) / 8 -- the code with its sign -- and fields 0..15 fill the
+// first 96 bits (the other 16 inputs are zero).
+__device__ __forceinline__ void fp6_fields16(const uint32_t (&hp)[8], uint32_t& d0, uint32_t& d1, uint32_t& d2) {
+  const u32x16 in = {hp[0], hp[1], hp[2], hp[3], hp[4], hp[5], hp[6], hp[7], 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  const i32x6 f = __builtin_amdgcn_cvt_scalef32_pk32_fp6_bf16(__builtin_bit_cast(bf16x32, in), 8.0f);
+  d0 = (uint32_t)f[0];
+  d1 = (uint32_t)f[1];
+  d2 = (uint32_t)f[2];
 }
 
 // Sum of a float64 over the wave (butterfly: every lane ends with the total,
@@ -322,7 +356,14 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nwaves = blockDim.x >> 6;
-  const int64_t row = blockIdx.x;
+  int64_t row = blockIdx.x;
+  if constexpr (MODE == CONVROT_PREP_FP6) {
+    // Workgroups go round-robin to the 8 XCDs.  The 16 rows of an FP6 block
+    // share its cache lines, so each XCD takes runs of consecutive rows (a
+    // multiple of 16 each) and its L2 merges the rows' pieces of a line.
+    const int64_t run = ((int64_t)gridDim.x / (8 * 16)) * 16;
+    if (row < 8 * run) row = (row & 7) * run + (row >> 3);
+  }
   const int chunks = K >> 4;
   constexpr int kEsize = DT == kF32 ? 4 : 2;
   const __amdgpu_buffer_rsrc_t xrow = __builtin_amdgcn_make_buffer_rsrc(
@@ -460,7 +501,8 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
     const float (&v)[16] = keep[it];
     uint32_t q[16];
     float rt[16];
-    if constexpr (MODE != CONVROT_PREP_ROTATE) {
+    constexpr bool kFp6Cvt = MODE == CONVROT_PREP_FP6 && DT == kBF16;  // FP6 by the conversion instruction
+    if constexpr (MODE != CONVROT_PREP_ROTATE && !kFp6Cvt) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         float ratio;
@@ -472,31 +514,52 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
       }
     }
     if constexpr (MODE == CONVROT_PREP_FP6) {
-      // Each run's four codes are a 24-bit field; 16 consecutive features (a
-      // group's half stream, 12 bytes) are 4 runs: the lane's own 4 runs for
-      // groups up to 16, else run r of the 4 lanes of a quad (lane k holding
-      // features 4k .. 4k+3 of it), which lane r of the quad gathers through
-      // the wave's LDS region.
-      uint32_t pc[4];
-#pragma unroll
-      for (int run = 0; run < 4; ++run)
-        pc[run] = fp6_piece(q[4 * run], q[4 * run + 1], q[4 * run + 2], q[4 * run + 3], rt[4 * run],
-                            rt[4 * run + 1], rt[4 * run + 2], rt[4 * run + 3]);
+      // 16 consecutive features (a group's half stream, 12 bytes) are 4 runs
+      // of 4: the lane's own 4 runs for groups up to 16, else run r of the 4
+      // lanes of a quad (lane k holding features 4k .. 4k+3 of it), which
+      // lane r of the quad gathers through the wave's LDS region.
+      uint32_t d0, d1, d2;
       int fh;  // first feature (in the row) of the half this lane writes
-      if constexpr (S >= 3) {
-        uint32_t* xr = (uint32_t*)(lds + wave * kRegionFloats);
-        const int qb = lane & ~3, k = lane & 3;
-        wave_lds_fence();
+      const int qb = lane & ~3, k = lane & 3;
+      uint32_t* xr = (uint32_t*)(lds + wave * kRegionFloats);
+      if constexpr (kFp6Cvt) {
+        // bf16 ratios, two to a register (run r in hp[2r], hp[2r+1]), then one
+        // conversion instruction for the lane's 16 features
+        uint32_t hp[8];
 #pragma unroll
-        for (int run = 0; run < 4; ++run) xr[(qb + run) * 4 + k] = pc[run];
-        wave_lds_fence();
-        const uint4 g = *(const uint4*)(xr + (qb + k) * 4);
-        pc[0] = g.x, pc[1] = g.y, pc[2] = g.z, pc[3] = g.w;
-        fh = block * 1024 + (lane / LG) * GS + run_index<S, PHF>(p & ~3, k);
+        for (int i = 0; i < 8; ++i) hp[i] = zero_code_sign_fix(pack_bf16x2(v[2 * i] * inv, v[2 * i + 1] * inv));
+        if constexpr (S >= 3) {
+          wave_lds_fence();
+#pragma unroll
+          for (int run = 0; run < 4; ++run)
+            *(uint2*)(xr + (qb + run) * 8 + 2 * k) = make_uint2(hp[2 * run], hp[2 * run + 1]);
+          wave_lds_fence();
+          const uint4 g0 = *(const uint4*)(xr + (qb + k) * 8), g1 = *(const uint4*)(xr + (qb + k) * 8 + 4);
+          hp[0] = g0.x, hp[1] = g0.y, hp[2] = g0.z, hp[3] = g0.w;
+          hp[4] = g1.x, hp[5] = g1.y, hp[6] = g1.z, hp[7] = g1.w;
+        }
+        fp6_fields16(hp, d0, d1, d2);
       } else {
-        fh = block * 1024 + lane * 16;
+        // each run's four codes as a 24-bit field
+        uint32_t pc[4];
+#pragma unroll
+        for (int run = 0; run < 4; ++run)
+          pc[run] = fp6_piece(q[4 * run], q[4 * run + 1], q[4 * run + 2], q[4 * run + 3], rt[4 * run],
+                              rt[4 * run + 1], rt[4 * run + 2], rt[4 * run + 3]);
+        if constexpr (S >= 3) {
+          wave_lds_fence();
+#pragma unroll
+          for (int run = 0; run < 4; ++run) xr[(qb + run) * 4 + k] = pc[run];
+          wave_lds_fence();
+          const uint4 g = *(const uint4*)(xr + (qb + k) * 4);
+          pc[0] = g.x, pc[1] = g.y, pc[2] = g.z, pc[3] = g.w;
+        }
+        d0 = pc[0] | (pc[1] << 24);
+        d1 = (pc[1] >> 8) | (pc[2] << 16);
+        d2 = (pc[2] >> 16) | (pc[3] << 8);
       }
-      const uint32_t d0 = pc[0] | (pc[1] << 24), d1 = (pc[1] >> 8) | (pc[2] << 16), d2 = (pc[2] >> 16) | (pc[3] << 8);
+      if constexpr (S >= 3) fh = block * 1024 + (lane / LG) * GS + run_index<S, PHF>(p & ~3, k);
+      else fh = block * 1024 + lane * 16;
       const int64_t mblocks = ((int64_t)gridDim.x + 15) >> 4;
       uint8_t* blk = (uint8_t*)out + ((int64_t)(fh >> 7) * mblocks + (row >> 4)) * 1536;
       const int L = ((fh >> 5) & 3) * 16 + (int)(row & 15);

@@ -271,13 +271,15 @@ int convrot_repack_weight(const uint8_t* in, int in_layout, uint8_t* out, int ou
 int64_t convrot_cdna4_bytes(int64_t N, int64_t K);
 
 /*
- * FP6 operand path.  An A4 code v in [-7, 7] is exactly representable as an
- * FP6 (OCP MX e2m3) value, and gfx950's FP6 matrix instruction
- * (v_mfma_scale_f32_16x16x128_f8f6f4, unit scales) sums products of such codes
- * exactly in float32 for K < 342,000 (|sum| <= 49 K < 2^24) at twice the INT8
- * instruction's rate.  So the same GEMM, with the same outputs bit for bit,
- * runs on operands re-encoded as FP6: no counterpart in the reference, whose
- * TensorOp multiplies the int4 codes as int8 (core.py:839-874).
+ * FP6 operand path.  A code v in [-8, 7] is stored as the FP6 (OCP MX e2m3)
+ * encoding of v/8: for |v| <= 7 the subnormal with mantissa |v| (a
+ * sign-magnitude field, zero as +0), and -1.0 for -8.  gfx950's FP6 matrix
+ * instruction (v_mfma_scale_f32_16x16x128_f8f6f4, both operand scales 2^3)
+ * then sums the exact products v*w in float32, exactly for K < 262,144
+ * (|sum| <= 64 K < 2^24), at twice the INT8 instruction's rate.  So the same
+ * GEMM, with the same outputs bit for bit, runs on operands re-encoded as
+ * FP6: no counterpart in the reference, whose TensorOp multiplies the int4
+ * codes as int8 (core.py:839-874).
  *
  * Operand layout (activations by row, weights by output column): blocks of 16
  * rows x 128 features, 1536 bytes each, ordered [K/128][ceil(R/16)]; lane
@@ -291,13 +293,9 @@ int64_t convrot_fp6_bytes(int64_t R, int64_t K);
 
 /*
  * CDNA4-layout weight -> FP6 operand blocks (an offline conversion, like
- * convrot_repack_weight).  Adds to *minus8 (a device int32 the caller
- * zero-fills) the number of -8 codes, which have no FP6 encoding: a weight
- * with any must stay on the INT8 kernels (the reference's quantizers emit
- * codes in [-7, 7], core.py:157).
+ * convrot_repack_weight); every int4 code, -8 included, has an FP6 field.
  */
-int convrot_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, int32_t* minus8,
-                       void* stream);
+int convrot_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, void* stream);
 
 /*
  * convrot_w4a4_gemm on FP6 operands: act6 from convrot_prepare(..., CONVROT_PREP_FP6,

@@ -415,16 +415,17 @@ def cdna4_to_nk(blocks: np.ndarray, n: int, k: int) -> np.ndarray:
 
 
 # FP6 operand layout (no reference counterpart; defined by this build), for
-# activations (rows) and weights (columns) alike.  A code v in [-7, 7] is
-# stored as its OCP MX e2m3 encoding (sign bit 5, exponent bits 4..3 with bias
-# 1, mantissa bits 2..0), which represents every such integer exactly.  Blocks
-# of 16 rows x 128 features, 1536 bytes each, ordered [K/128][R_pad/16]; lane
+# activations (rows) and weights (columns) alike.  A code v in [-8, 7] is
+# stored as the OCP MX e2m3 encoding (sign bit 5, exponent bits 4..3 with bias
+# 1, mantissa bits 2..0) of v/8: for |v| <= 7 the subnormal with mantissa |v|,
+# for -8 the normal -1.0; zero is +0.  The GEMM multiplies both operands by
+# 2^3 (the MFMA's block scales), so products are v*w exactly.  Blocks of 16
+# rows x 128 features, 1536 bytes each, ordered [K/128][R_pad/16]; lane
 # L = 16*q + r of a block holds row r's features 32*q + i (i = 0..31), feature
 # i at bits 6i..6i+5 of a 192-bit little-endian stream whose bytes 0..15 sit
 # at 16*L and bytes 16..23 at 1024 + 8*L.  Rows are zero-padded to a multiple
 # of 16; K must be a multiple of 128.
 FP6_BLOCK_BYTES = 1536
-E2M3_MAG = np.array([0, 8, 16, 20, 24, 26, 28, 30], np.uint64)  # e2m3 code of |v|, v = 0..7
 
 
 def e2m3_value(code) -> np.ndarray:
@@ -436,12 +437,18 @@ def e2m3_value(code) -> np.ndarray:
     return np.where(s == 1, -mag, mag)
 
 
-def e2m3_code(v) -> np.ndarray:
-    """e2m3 code of integers in [-7, 7]."""
+def fp6_code(v) -> np.ndarray:
+    """FP6 field of integer codes in [-8, 7]: the e2m3 encoding of v/8 (zero as +0)."""
     v = np.asarray(v, dtype=np.int64)
-    if v.size and (v.min() < -7 or v.max() > 7):
-        raise ValueError("e2m3 holds the integers -7 .. 7 only")
-    return E2M3_MAG[np.abs(v)] | np.where(v < 0, 32, 0).astype(np.uint64)
+    if v.size and (v.min() < -8 or v.max() > 7):
+        raise ValueError("FP6 codes hold the integers -8 .. 7 only")
+    mag = np.where(v == -8, 8, np.abs(v)).astype(np.uint64)  # -8/8 = -1.0 is e=1, m=0: bits 0b001000
+    return mag | np.where(v < 0, 32, 0).astype(np.uint64)
+
+
+def fp6_value(code) -> np.ndarray:
+    """Integer code of an FP6 field (8 times its e2m3 value)."""
+    return e2m3_value(code) * 8.0
 
 
 def codes_to_fp6(codes: np.ndarray) -> np.ndarray:
@@ -452,7 +459,7 @@ def codes_to_fp6(codes: np.ndarray) -> np.ndarray:
     rb, kb = -(-R // 16), K // 128
     full = np.zeros((rb * 16, K), np.int8)
     full[:R] = codes
-    c = e2m3_code(full).reshape(rb, 16, kb, 4, 4, 8)  # rblk, r, kblk, q, chunk of 8 fields, field
+    c = fp6_code(full).reshape(rb, 16, kb, 4, 4, 8)  # rblk, r, kblk, q, chunk of 8 fields, field
     words = (c << (6 * np.arange(8, dtype=np.uint64))).sum(-1)  # 48-bit chunks (disjoint bit fields)
     stream = ((words[..., None] >> (8 * np.arange(6, dtype=np.uint64))) & 0xFF).astype(np.uint8)
     stream = stream.reshape(rb, 16, kb, 4, 24).transpose(2, 0, 3, 1, 4)  # kblk, rblk, q, r, 24
@@ -471,7 +478,7 @@ def fp6_to_codes(blocks: np.ndarray, rows: int, k: int) -> np.ndarray:
     for j in range(24):
         bits = bits + (stream[..., j].astype(object) << (8 * j))
     fields = np.stack([(bits >> (6 * i)) & 63 for i in range(32)], axis=-1).astype(np.int64)
-    vals = e2m3_value(fields)
+    vals = fp6_value(fields)
     if not np.array_equal(vals, np.round(vals)):
         raise ValueError("FP6 blocks hold a code that is not an integer")
     full = vals.astype(np.int64).transpose(1, 3, 0, 2, 4).reshape(rb * 16, kb * 128)

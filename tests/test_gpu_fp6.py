@@ -3,7 +3,7 @@ kernel's FP6 output and the FP6-operand W4A4 GEMM, each bit for bit against the 
 (oracle.codes_to_fp6 for the layouts, w4a4_matmul_codes_large for the products), and the
 complete FP6 path against the INT8 path.
 
-The FP6 layout and e2m3 encoding are this build's own (no reference counterpart); the codes
+The FP6 layout and encoding (a code v as the e2m3 value v/8) are this build's own (no reference counterpart); the codes
 they carry are the reference's A4 / W4 codes (core.py:149-167, 514-527), and the products
 follow reference_w4a4_matmul (core.py:1155-1171) as the INT8 kernels do.
 """
@@ -31,10 +31,9 @@ def _u8(a, dev):
 
 def _weight_fp6(nat, wq_dev, N, K, dev):
     out = torch.zeros(int(nat.load().convrot_fp6_bytes(N, K)), dtype=torch.uint8, device=dev)
-    bad = torch.zeros(1, dtype=torch.int32, device=dev)
-    nat.check(nat.load().convrot_weight_fp6(nat.ptr(wq_dev), nat.ptr(out), N, K, nat.ptr(bad), nat.stream_of(dev)))
+    nat.check(nat.load().convrot_weight_fp6(nat.ptr(wq_dev), nat.ptr(out), N, K, nat.stream_of(dev)))
     torch.cuda.synchronize()
-    return out, int(bad.item())
+    return out
 
 
 def _prep_fp6(nat, xd, G, mode, dev):
@@ -63,27 +62,36 @@ def _assert_exact(got, want, label):
 @pytest.mark.parametrize("N,K", [(46, 128), (264, 384), (3072, 3072), (1000, 15360)])
 def test_weight_fp6_matches_oracle(orc, dev, N, K):
     """CDNA4 weight -> FP6 blocks: every byte as the oracle's layout of the same codes
-    (padding columns included), and no -8 reported."""
+    (padding columns included), -8 codes included."""
     nat = _nat()
     rng = np.random.default_rng(N + K)
-    w = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
-    got, bad = _weight_fp6(nat, _u8(orc.codes_to_cdna4(w), dev), N, K, dev)
-    assert bad == 0
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    got = _weight_fp6(nat, _u8(orc.codes_to_cdna4(w), dev), N, K, dev)
     want = orc.codes_to_fp6(w).reshape(-1)
     _assert_exact(from_dev(got), want, f"weight {N}x{K}")
     assert np.array_equal(orc.fp6_to_codes(from_dev(got).reshape(K // 128, -1, 1536), N, K), w)
 
 
-def test_weight_fp6_counts_minus8(orc, dev):
-    """-8 codes (outside e2m3) are counted, so the caller keeps such a weight on the INT8 path."""
+def test_weight_fp6_minus8_codes(orc, dev):
+    """-8 weight codes (the int4 range's end, never emitted by the quantizers) encode as -1.0
+    (v/8) and multiply exactly: the FP6 GEMM on a weight of -8 runs equals the oracle."""
     nat = _nat()
     rng = np.random.default_rng(8)
-    w = rng.integers(-7, 8, size=(64, 256), dtype=np.int8)
-    w[3, 17] = -8
+    M, N, K = 64, 64, 512
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    w[3] = -8
     w[60, 255] = -8
-    w[0, 0] = -8
-    _, bad = _weight_fp6(nat, _u8(orc.codes_to_cdna4(w), dev), 64, 256, dev)
-    assert bad == 3
+    a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
+    a[5] = -7
+    got = _weight_fp6(nat, _u8(orc.codes_to_cdna4(w), dev), N, K, dev)
+    _assert_exact(from_dev(got), orc.codes_to_fp6(w).reshape(-1), "weight with -8")
+    assert int(orc.codes_to_fp6(np.full((1, 128), -8, np.int8))[0, 0, 0]) & 63 == 0x28
+    xs = np.ones(M, np.float32)
+    ws = np.ones(N, np.float32)
+    b = np.zeros(N, np.float32)
+    out = _gemm_fp6(nat, _u8(orc.codes_to_fp6(a), dev), _u8(xs, dev), got, _u8(ws, dev), _u8(b, dev), M, N, K,
+                    torch.float16, dev)
+    _assert_exact(from_dev(out), orc.w4a4_matmul_codes_large(a, w, xs, ws, b, "float16"), "-8 products")
 
 
 @pytest.mark.parametrize("dtype,G,rows,K", [
@@ -117,11 +125,18 @@ def test_prepare_fp6_without_rotation(orc, dev):
 
 
 def test_prepare_fp6_zero_and_tiny_rows(orc, dev):
-    """An all-zero row and rows of tiny values: every code 0 is +0 in e2m3 (no -0 code)."""
+    """An all-zero row, a row of tiny negative values, and rows whose negative ratios round to
+    code 0 next to one large value: every code 0 is +0 (no -0 field)."""
     nat = _nat()
     x = normal_input(77, (18, 1024), "bfloat16", orc)
     x[0] = 0
     x[5] = orc.from_f32(np.full(1024, -1e-30, np.float32), "bfloat16")
+    small = -np.abs(np.random.default_rng(5).normal(size=1024)).astype(np.float32) * 0.04
+    small[::97] = 0.0
+    for r, big in ((7, 40.0), (8, -40.0)):
+        row = small.copy()
+        row[3] = big
+        x[r] = orc.from_f32(row, "bfloat16")
     codes, scales = orc.prepare_codes(x, "bfloat16", 256)
     got, s = _prep_fp6(nat, to_dev(x, "bfloat16", dev), 256, nat.PREP_FP6, dev)
     assert np.array_equal(from_dev(s), scales)
@@ -161,10 +176,10 @@ def test_fp6_gemm_matches_oracle(orc, dev, out_dtype, M, K, N):
     nat = _nat()
     rng = np.random.default_rng(M + K + N)
     a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
-    w = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
     a[1] = 0
     a[2] = 7
-    w[3] = -7
+    w[3] = -8
     xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
     ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
     b = rng.normal(size=(N,)).astype(np.float32)
@@ -176,7 +191,8 @@ def test_fp6_gemm_matches_oracle(orc, dev, out_dtype, M, K, N):
 
 
 def test_fp6_gemm_largest_sums(orc, dev):
-    """K = 15360 with runs of +-7 * +-7: sums of +-752640 (the largest at config 3) stay exact."""
+    """K = 15360 with runs of +-7 * +-7 and -7 * -8: sums up to 860160 (beyond the largest at
+    config 3) stay exact."""
     nat = _nat()
     M, K, N = 64, 15360, 64
     rng = np.random.default_rng(15360)
@@ -186,6 +202,7 @@ def test_fp6_gemm_largest_sums(orc, dev):
     a[8:16] = -7
     w[:8] = 7
     w[8:16] = -7
+    w[16:24] = -8
     xs = np.ones(M, np.float32)
     ws = np.ones(N, np.float32)
     b = np.zeros(N, np.float32)
@@ -210,8 +227,7 @@ def test_fp6_complete_path_equals_int8_path(orc, dev, M, G, K, N):
     bias = torch.randn(N, generator=gen, device=dev) * 0.02
     q8, xs8 = core._prepare(x, G, nat.PREP_INT8)
     want = core.hip_w4a4_int8_matmul(q8, wq, xs8, ws, bias, output_dtype=torch.bfloat16, out_features=N)
-    w6, bad = _weight_fp6(nat, wq, N, K, dev)
-    assert bad == 0
+    w6 = _weight_fp6(nat, wq, N, K, dev)
     a6, xs6 = _prep_fp6(nat, x, G, nat.PREP_FP6, dev)
     got = _gemm_fp6(nat, a6, xs6, w6, ws.float().contiguous(), bias.float().contiguous(), M, N, K, torch.bfloat16, dev)
     assert torch.equal(xs6, xs8)

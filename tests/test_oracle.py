@@ -277,20 +277,59 @@ def test_cdna4_layout_brute_force(orc):
     assert np.array_equal(orc.cdna4_to_codes(blocks, N, K), v)
 
 
-def test_e2m3_codes_are_the_integers(orc):
-    """The e2m3 codes of -7 .. 7, decoded by the format's definition (bias 1, 3 mantissa
-    bits), are the integers themselves; no two share a code; 0 has no sign bit; and the
-    decoder agrees with a scan of all 64 codes for the integer-valued ones."""
-    v = np.arange(-7, 8)
-    c = orc.e2m3_code(v)
-    assert np.array_equal(orc.e2m3_value(c), v.astype(np.float64))
-    assert len(set(c.tolist())) == 15 and int(c[7]) == 0
+def test_fp6_codes_are_the_integers_over_8(orc):
+    """The FP6 fields of -8 .. 7, decoded by the e2m3 definition (bias 1, 3 mantissa bits),
+    are the codes divided by 8: no two share a field, 0 has no sign bit, |v| <= 7 are
+    subnormals (exponent bits zero, mantissa |v|), and a scan of all 64 fields finds
+    exactly these among the fields whose value times 8 is an integer of [-8, 7] (0 aside)."""
+    v = np.arange(-8, 8)
+    c = orc.fp6_code(v)
+    assert np.array_equal(orc.e2m3_value(c) * 8.0, v.astype(np.float64))
+    assert np.array_equal(orc.fp6_value(c), v.astype(np.float64))
+    assert len(set(c.tolist())) == 16 and int(c[8]) == 0
+    small = np.abs(v) <= 7
+    assert not ((c[small] >> 3) & 3).any() and np.array_equal(c[small] & 7, np.abs(v[small]))
+    assert int(c[0]) == 0b101000  # -8/8 = -1.0: sign, exponent 1 (bias 1), mantissa 0
     all_codes = np.arange(64)
-    vals = orc.e2m3_value(all_codes)
-    ints = {int(x): int(k) for k, x in zip(all_codes, vals) if x == np.round(x) and not (x == 0 and k)}
+    vals = orc.e2m3_value(all_codes) * 8.0
+    ints = {int(x): int(k) for k, x in zip(all_codes, vals)
+            if x == np.round(x) and -8 <= x <= 7 and not (x == 0 and k)}
     assert ints == {int(x): int(k) for x, k in zip(v, c)}
-    with pytest.raises(ValueError):
-        orc.e2m3_code(np.array([-8]))
+    for bad in (-9, 8):
+        with pytest.raises(ValueError):
+            orc.fp6_code(np.array([bad]))
+
+
+def test_bf16_ratios_stay_below_7_5(orc):
+    """Every bf16 ratio is at most 7.03125 in magnitude, so rint(ratio) never leaves [-7, 7]
+    and the clamp (core.py:157) never binds: for every positive finite bf16 row maximum m,
+    scale = bf16(max(m, bf16(1e-10)) / 7), and the largest ratio bf16(m * RN(1/scale)) and
+    bf16(m / scale) (the division the reference runs) are at most 7.03125."""
+    bits = np.arange(0x0001, 0x7F80, dtype=np.uint32)  # positive finite bf16 (subnormals included)
+    m = (bits << 16).view(np.float32)
+    floor = orc.to_f32(orc.from_f32(np.array([1e-10], np.float32), "bfloat16"), "bfloat16")[0]
+    scale = orc.to_f32(orc.from_f32((np.maximum(m, floor) / np.float32(7)).astype(np.float32), "bfloat16"),
+                       "bfloat16")
+    inv = (np.float32(1) / scale).astype(np.float32)
+    by_rcp = orc.to_f32(orc.from_f32((m * inv).astype(np.float32), "bfloat16"), "bfloat16")
+    by_div = orc.to_f32(orc.from_f32((m / scale).astype(np.float32), "bfloat16"), "bfloat16")
+    assert by_rcp.max() <= 7.03125 and by_div.max() <= 7.03125
+    assert by_rcp.max() > 7.0  # the bound is reached, not loose
+
+
+def test_fp6_zero_code_sign_fix_over_all_bf16_pairs():
+    """The preparation kernel's zero_code_sign_fix (prep.hip), restated on every bf16 half:
+    h & ~((h + 0x40ff mod 2^16) & 0x8000) clears the sign of exactly the negative values of
+    magnitude <= 0.5 (whose code rint(x) is 0) and leaves every other value unchanged."""
+    h = np.arange(65536, dtype=np.uint32)
+    fixed = h & ~(((h + 0x40FF) & 0xFFFF) & 0x8000)
+    x = (h << 16).view(np.float32)
+    finite = np.isfinite(x)
+    zero_code = finite & (np.abs(x) <= 0.5)
+    assert np.array_equal(fixed[zero_code], h[zero_code] & 0x7FFF)
+    assert np.array_equal(fixed[~zero_code & finite], h[~zero_code & finite])
+    assert np.array_equal(np.rint(x[zero_code]), np.zeros(int(zero_code.sum())))  # code 0 indeed
+    assert not np.any(np.rint(np.abs(x[finite & ~zero_code])) == 0)
 
 
 def test_fp6_layout_brute_force(orc):
@@ -300,7 +339,7 @@ def test_fp6_layout_brute_force(orc):
     layout's lanes."""
     rng = np.random.default_rng(6)
     R, K = 37, 256
-    v = rng.integers(-7, 8, size=(R, K), dtype=np.int8)
+    v = rng.integers(-8, 8, size=(R, K), dtype=np.int8)
     blocks = orc.codes_to_fp6(v)
     assert blocks.shape == (2, 3, 1536)
     want = np.zeros_like(blocks)
@@ -308,7 +347,7 @@ def test_fp6_layout_brute_force(orc):
         for k in range(K):
             kb, kk = divmod(k, 128)
             L = 16 * (kk // 32) + r % 16
-            code = int(orc.e2m3_code(np.array([v[r, k]]))[0])
+            code = int(orc.fp6_code(np.array([v[r, k]]))[0])
             for b in range(6):
                 bit = 6 * (kk % 32) + b
                 byte = 16 * L + bit // 8 if bit < 128 else 1024 + 8 * L + (bit - 128) // 8
