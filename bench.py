@@ -7,8 +7,10 @@ QKV 3072->9216, attention out 3072->3072, MLP 3072->12288 and 12288->3072, and
 the fused single-block linears 3072->21504 and 15360->3072.  Weights
 ~N(0, 0.02^2) with 1% of input channels x10, activations ~N(0, 1) with 0.5% of
 channels x20, bias ~N(0, 0.02^2) (synthetic, seeded).  One step = the complete
-path (fused prep kernel -> INT8-MFMA GEMM with the fused scale/bias epilogue)
-over all six linears, inputs and weights already resident in HBM.  A step
+path ConvRotLinear runs at these sizes (fused prep kernel writing FP6 operands
+-> FP6-MFMA GEMM with the fused scale/bias epilogue; the A4/W4 codes as FP6
+values give the INT8 path's outputs bit for bit) over all six linears, inputs
+and weights already resident in HBM.  A step
 touches ~1.2 GB of distinct buffers, over four times the 256 MB Infinity
 Cache, so no linear finds its operands cached from its previous step.
 
@@ -18,7 +20,9 @@ around every launch, over a pass of max(K, 30) steps run between the warm-up
 and the timed region.
 
 Prints ONE JSON line (the driver's contract).  Extra keys:
-  roofline        the W4A4 GEMM (dominant kernel) vs the INT8 MFMA peak, per shape too
+  roofline        the W4A4 GEMM (dominant kernel) vs the FP6 MFMA peak it runs on (and the
+                  INT8 peak the metric is quoted against), per shape too
+  int8_operands   the same step on INT8 operands (prep int8 codes -> INT8-MFMA GEMM)
   prep_roofline   the prep kernel vs the HBM peak, per shape too
   per_shape       complete-path latency and TOPS of each linear
   dense_bf16_control  torch bf16 linear (hipBLASLt) on the same six shapes
@@ -46,6 +50,7 @@ for _p in (str(ROOT / "convrot-mlx_amd"), str(ROOT)):
         sys.path.insert(0, _p)
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense INT8 MFMA (TOPS)
+FP6_PEAK_TOPS = 10100.0  # MI355X dense FP6 MFMA
 BF16_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBPS = 8000.0
 
@@ -53,7 +58,7 @@ CONFIG3 = {"M": 4608, "G": 256,
            "shapes": [(3072, 9216), (3072, 3072), (3072, 12288), (12288, 3072), (3072, 21504), (15360, 3072)]}
 CONFIG2 = {"M": 1536, "G": 64, "shapes": [(3072, 9216), (3072, 3072), (3072, 12288), (12288, 3072)]}
 CONFIG4 = {"G": 256, "Ms": (1, 8, 32), "shapes": [(3072, 12288), (12288, 3072)]}
-TRAFFIC_FILE = ROOT / "profiles" / "gemm_w4a4_flux_m4608_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "gemm_w4a4_fp6_flux_m4608_traffic.json"
 
 
 def parse():
@@ -70,6 +75,8 @@ def parse():
     ap.add_argument("--no-config5", action="store_true", help="skip the FLUX DiT step (config 5)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run one 256 MiB device copy first (counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--operands", choices=("fp6", "int8"), default="fp6",
+                    help="operands of the measured path: FP6 (what ConvRotLinear runs at these sizes) or INT8")
     ap.add_argument("--workload", choices=("config3", "config2"), default="config3",
                     help="the measured workload: configs[2] (the headline, M=4608 G=256) or configs[1] (M=1536 "
                          "G=64, for profiling); the extras are the same either way")
@@ -84,7 +91,7 @@ def outliers(torch, gen, dev, shape, std, frac, factor):
     return x.to(torch.bfloat16)
 
 
-def make_layers(torch, core, dev, M, G, shapes, seed, sets=1):
+def make_layers(torch, core, dev, M, G, shapes, seed, sets=1, fp6=True):
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     out = []
@@ -93,8 +100,11 @@ def make_layers(torch, core, dev, M, G, shapes, seed, sets=1):
         for K, N in shapes:
             w = outliers(torch, gen, dev, (N, K), 0.02, 0.01, 10.0)
             qw, ws = core.quantize_convrot_weight(w, G)
+            wq = core.repack_nk_weight_for_cdna4(qw)
             layers.append(dict(
-                K=K, N=N, w=w, qw=qw, wq=core.repack_nk_weight_for_cdna4(qw), ws=ws,
+                K=K, N=N, w=w, qw=qw, wq=wq, ws=ws,
+                w6=core.fp6_weight(wq, N, K) if fp6 else None,
+                a6=torch.empty(core.fp6_shape(M, K), dtype=torch.uint8, device=dev) if fp6 else None,
                 bias=(torch.randn(N, generator=gen, device=dev) * 0.02).float(),
                 x=outliers(torch, gen, dev, (M, K), 1.0, 0.005, 20.0),
                 out=torch.empty((M, N), dtype=torch.bfloat16, device=dev),
@@ -106,21 +116,28 @@ def make_layers(torch, core, dev, M, G, shapes, seed, sets=1):
 
 class PathRunner:
     """Launches of the complete path (prep -> GEMM) of one set of linears on one stream,
-    with optional HIP events around every launch."""
+    on FP6 or INT8 operands, with optional HIP events around every launch."""
 
-    def __init__(self, nat, dev, M, G):
+    def __init__(self, nat, dev, M, G, fp6=True):
         self.nat, self.lib, self.stream, self.M, self.G = nat, nat.load(), nat.stream_of(dev), M, G
+        self.fp6 = fp6
 
     def prep(self, L):
         nat = self.nat
-        nat.check(self.lib.convrot_prepare(nat.ptr(L["x"]), nat.DTYPE_BF16, self.M, L["K"], self.G, nat.PREP_INT8,
-                                           nat.ptr(L["qact"]), nat.ptr(L["xs"]), self.stream))
+        mode, out = (nat.PREP_FP6, L["a6"]) if self.fp6 else (nat.PREP_INT8, L["qact"])
+        nat.check(self.lib.convrot_prepare(nat.ptr(L["x"]), nat.DTYPE_BF16, self.M, L["K"], self.G, mode,
+                                           nat.ptr(out), nat.ptr(L["xs"]), self.stream))
 
     def gemm(self, L):
         nat = self.nat
-        nat.check(self.lib.convrot_w4a4_gemm(nat.ptr(L["qact"]), nat.ACT_INT8, nat.ptr(L["xs"]), nat.ptr(L["wq"]),
-                                             nat.ptr(L["ws"]), nat.ptr(L["bias"]), self.M, L["N"], L["K"],
-                                             nat.ptr(L["out"]), nat.DTYPE_BF16, self.stream))
+        if self.fp6:
+            nat.check(self.lib.convrot_w4a4_gemm_fp6(nat.ptr(L["a6"]), nat.ptr(L["xs"]), nat.ptr(L["w6"]),
+                                                     nat.ptr(L["ws"]), nat.ptr(L["bias"]), self.M, L["N"], L["K"],
+                                                     nat.ptr(L["out"]), nat.DTYPE_BF16, self.stream))
+        else:
+            nat.check(self.lib.convrot_w4a4_gemm(nat.ptr(L["qact"]), nat.ACT_INT8, nat.ptr(L["xs"]),
+                                                 nat.ptr(L["wq"]), nat.ptr(L["ws"]), nat.ptr(L["bias"]), self.M,
+                                                 L["N"], L["K"], nat.ptr(L["out"]), nat.DTYPE_BF16, self.stream))
 
     def step(self, layers, events=None):
         for j, L in enumerate(layers):
@@ -192,11 +209,12 @@ def main() -> int:
 
     W = CONFIG3 if args.workload == "config3" else CONFIG2
     M, G, shapes = W["M"], W["G"], W["shapes"]
+    fp6 = args.operands == "fp6"
     # configs[1]'s four linears total ~315 MB: three buffer sets keep a step out of the Infinity Cache
     sets = make_layers(torch, core, dev, M, G, shapes, seed=20260823,
-                       sets=args.sets if args.workload == "config3" else max(args.sets, 3))
+                       sets=args.sets if args.workload == "config3" else max(args.sets, 3), fp6=True)
     torch.cuda.synchronize()
-    runner = PathRunner(nat, dev, M, G)
+    runner = PathRunner(nat, dev, M, G, fp6=fp6)
     ms_per_step, prep_ms, gemm_ms, ms_events, ev_steps = measure_path(
         torch, np, runner, sets, shapes, M, args.steps, args.warmup)
 
@@ -204,12 +222,14 @@ def main() -> int:
     tops = ops.sum() / (ms_per_step * 1e-3) / 1e12
     gemm_tops = ops / (gemm_ms * 1e-3) / 1e12
     gemm_agg = ops.sum() / (gemm_ms.sum() * 1e-3) / 1e12
-    prep_bytes = np.array([3.0 * M * K + 4 * M for K, _ in shapes])  # bf16 in, int8 out, f32 scales
+    out_bytes = 0.75 if fp6 else 1.0  # FP6 (6 bits) or int8 codes per feature
+    prep_bytes = np.array([(2.0 + out_bytes) * M * K + 4 * M for K, _ in shapes])  # bf16 in, codes out, f32 scales
     prep_gbps = prep_bytes / (prep_ms * 1e-3) / 1e9
     prep_agg = prep_bytes.sum() / (prep_ms.sum() * 1e-3) / 1e9
+    peak = FP6_PEAK_TOPS if fp6 else INT8_PEAK_TOPS
 
     traffic, traffic_note = None, "no FETCH_SIZE/WRITE_SIZE profile for this workload"
-    if TRAFFIC_FILE.exists() and args.workload == "config3":
+    if TRAFFIC_FILE.exists() and args.workload == "config3" and fp6:
         try:
             tj = json.loads(TRAFFIC_FILE.read_text())
             traffic = tj.get("hbm_bytes_per_launch_avg")
@@ -230,7 +250,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        "dtype": "fp6" if fp6 else "int8",
         "data": "synthetic (seeded N(0,1) activations with 0.5% x20 channels, N(0,0.02^2) weights with 1% x10 "
                 "input channels, N(0,0.02^2) bias; random init)",
         "config": {
@@ -242,26 +262,33 @@ def main() -> int:
                          "text tokens), group 64, bf16, with bias: 3072->9216, 3072->3072, 3072->12288, "
                          "12288->3072; complete path prep+GEMM+epilogue"),
             "M": M, "group_size": G, "shapes_KxN": shapes, "buffer_sets": args.sets,
+            "operands": ("FP6: the A4/W4 codes v as e2m3 values v/8, multiplied by the FP6 MFMA with block "
+                         "scales 2^3 (exact integer products, float32 sums exact below 2^24): the INT8 path's "
+                         "outputs bit for bit" if fp6 else "INT8: A4 codes as int8, W4 nibbles unpacked to int8"),
             "pct_int8_peak": round(100.0 * tops / INT8_PEAK_TOPS, 2),
         },
         "roofline": {
-            "kernel": "W4A4 GEMM (w4a4_gemm_agpr_kernel, 288x192 and 256x256 tiles: INT8 MFMA + fused epilogue)",
+            "kernel": ("W4A4 GEMM on FP6 operands (w4a4_gemm_fp6_kernel: v_mfma_scale_f32_16x16x128_f8f6f4 + "
+                       "fused epilogue)" if fp6 else
+                       "W4A4 GEMM (w4a4_gemm_agpr_kernel, 288x192 and 256x256 tiles: INT8 MFMA + fused epilogue)"),
             "bound": "mfma",
             "achieved": round(float(gemm_agg), 2),
-            "peak": INT8_PEAK_TOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": round(float(gemm_agg) / INT8_PEAK_TOPS, 4),
+            "frac": round(float(gemm_agg) / peak, 4),
+            "frac_of_int8_peak": round(float(gemm_agg) / INT8_PEAK_TOPS, 4),
             "traffic": traffic,
             "traffic_source": traffic_note,
             "per_shape_us": [round(t * 1e3, 2) for t in gemm_ms],
             "per_shape_tops": [round(float(t), 1) for t in gemm_tops],
-            "per_shape_frac": [round(float(t) / INT8_PEAK_TOPS, 4) for t in gemm_tops],
-            "algorithmic": "2*M*N*K int ops per launch; achieved = sum of ops / sum of launch durations",
+            "per_shape_frac": [round(float(t) / peak, 4) for t in gemm_tops],
+            "algorithmic": "2*M*N*K int ops per launch; achieved = sum of ops / sum of launch durations; peak = "
+                           + ("the dense FP6 MFMA peak the kernel runs on" if fp6 else "the dense INT8 MFMA peak"),
             "timing": f"HIP events on the launch stream around each launch, over a pass of {ev_steps} steps run "
                       f"just before the timed region (that pass: {ms_events:.4f} ms per step with the markers)",
         },
         "prep_roofline": {
-            "kernel": "prep_kernel (rotate + absmax + A4 quantize, int8 codes out)",
+            "kernel": "prep_kernel (rotate + absmax + A4 quantize, " + ("FP6 codes out)" if fp6 else "int8 codes out)"),
             "bound": "hbm",
             "achieved": round(float(prep_agg), 1),
             "peak": HBM_PEAK_GBPS,
@@ -269,7 +296,8 @@ def main() -> int:
             "frac": round(float(prep_agg) / HBM_PEAK_GBPS, 4),
             "per_shape_us": [round(t * 1e3, 2) for t in prep_ms],
             "per_shape_GBps": [round(float(g), 1) for g in prep_gbps],
-            "algorithmic": "2*M*K (bf16 in) + M*K (int8 out) + 4*M bytes per launch",
+            "algorithmic": ("2*M*K (bf16 in) + 0.75*M*K (FP6 out)" if fp6 else "2*M*K (bf16 in) + M*K (int8 out)")
+                           + " + 4*M bytes per launch",
         },
         "per_shape": [{"K": K, "N": N, "path_us": round((p + g) * 1e3, 2),
                        "path_tops": round(float(o / ((p + g) * 1e-3) / 1e12), 1)}
@@ -277,11 +305,20 @@ def main() -> int:
     }
 
     if not args.no_extras:
+        other = PathRunner(nat, dev, M, G, fp6=not fp6)
+        o_ms, o_prep, o_gemm, _, _ = measure_path(torch, np, other, sets, shapes, M, args.steps, 3)
+        result["int8_operands" if fp6 else "fp6_operands"] = {
+            "what": "the same step and buffers on " + ("INT8" if fp6 else "FP6") + " operands",
+            "ms_per_step": round(o_ms, 4), "tops": round(float(ops.sum() / (o_ms * 1e-3) / 1e12), 1),
+            "pct_int8_peak": round(100.0 * ops.sum() / (o_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 2),
+            "gemm_per_shape_us": [round(t * 1e3, 2) for t in o_gemm],
+            "prep_per_shape_us": [round(t * 1e3, 2) for t in o_prep]}
+    if not args.no_extras:
         dense = dense_control(torch, sets[0], M, shapes)
         dense["convrot_speedup"] = round(dense["ms_per_step"] / ms_per_step, 3)
         result["dense_bf16_control"] = dense
-        result["config2_m1536"] = config2_figure(torch, np, core, nat, dev)
-        result["flux_m4608_column_shard_8"] = shard_figure(torch, np, core, nat, dev)
+        result["config2_m1536"] = config2_figure(torch, np, core, nat, dev, fp6)
+        result["flux_m4608_column_shard_8"] = shard_figure(torch, np, core, nat, dev, fp6)
         result["w4a16_config4"] = w4a16_figure(torch, core, nat, dev)
         if not args.no_config5:
             from examples.flux1_dev.dit import config5_figure
@@ -326,34 +363,36 @@ def dense_control(torch, layers, M, shapes):
             "per_shape_us": [round(t * 1e3, 2) for t in per]}
 
 
-def config2_figure(torch, np, core, nat, dev):
+def config2_figure(torch, np, core, nat, dev, fp6):
     """the four double-block linears at M=1536, G=64, complete path; three buffer
     sets (~630 MB) cycled so the Infinity Cache cannot hold a step's data."""
     M, G, shapes = CONFIG2["M"], CONFIG2["G"], CONFIG2["shapes"]
-    sets = make_layers(torch, core, dev, M, G, shapes, seed=1536, sets=3)
-    runner = PathRunner(nat, dev, M, G)
+    sets = make_layers(torch, core, dev, M, G, shapes, seed=1536, sets=3, fp6=fp6)
+    runner = PathRunner(nat, dev, M, G, fp6=fp6)
     ms, prep_ms, gemm_ms, _, _ = measure_path(torch, np, runner, sets, shapes, M, 50, 5)
     ops = np.array([2.0 * M * K * N for K, N in shapes])
     del sets
     torch.cuda.empty_cache()
-    return {"shapes_KxN": shapes, "M": M, "group_size": G, "ms_per_step": round(ms, 4),
+    return {"shapes_KxN": shapes, "M": M, "group_size": G, "operands": "fp6" if fp6 else "int8",
+            "ms_per_step": round(ms, 4),
             "tops": round(float(ops.sum() / (ms * 1e-3) / 1e12), 1),
             "gemm_tops": round(float(ops.sum() / (gemm_ms.sum() * 1e-3) / 1e12), 1),
             "gemm_per_shape_us": [round(t * 1e3, 2) for t in gemm_ms],
             "prep_per_shape_us": [round(t * 1e3, 2) for t in prep_ms]}
 
 
-def shard_figure(torch, np, core, nat, dev):
+def shard_figure(torch, np, core, nat, dev, fp6):
     """4608x3072->1536, G=256: one GPU's share of an 8-way column split of the MLP-up linear
     (no collective runs; three buffer sets)."""
     M, G, shapes = CONFIG3["M"], CONFIG3["G"], [(3072, 12288 // 8)]
-    sets = make_layers(torch, core, dev, M, G, shapes, seed=3, sets=3)
-    runner = PathRunner(nat, dev, M, G)
+    sets = make_layers(torch, core, dev, M, G, shapes, seed=3, sets=3, fp6=fp6)
+    runner = PathRunner(nat, dev, M, G, fp6=fp6)
     ms, prep_ms, gemm_ms, _, _ = measure_path(torch, np, runner, sets, shapes, M, 50, 5)
     ops = 2.0 * M * 3072 * 1536
     del sets
     torch.cuda.empty_cache()
-    return {"shape": f"{M}x3072->1536 G={G}", "us_per_linear": round(ms * 1e3, 2),
+    return {"shape": f"{M}x3072->1536 G={G}", "operands": "fp6" if fp6 else "int8",
+            "us_per_linear": round(ms * 1e3, 2),
             "tops": round(ops / (ms * 1e-3) / 1e12, 1), "gemm_us": round(float(gemm_ms[0]) * 1e3, 2),
             "pct_int8_peak": round(100 * ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 2)}
 

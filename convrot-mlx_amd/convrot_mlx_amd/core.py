@@ -658,6 +658,80 @@ def hip_w4a4_int8_matmul(activations, qweight, xscales, wscales, bias, *, output
                  out_features, gr)
 
 
+# ------------------------------------------------------------------ FP6 operands
+#
+# A code v is stored as the FP6 (e2m3) encoding of v/8, and gfx950's FP6 matrix
+# instruction, with both operand scales 2^3, sums the exact products v*w at
+# twice the INT8 instruction's rate: the same GEMM with the same outputs bit
+# for bit (layout and encoding in include/convrot_amd.h).  ConvRotLinear
+# takes this path for the plain epilogue at FP6_MIN_ROWS rows and above; the
+# few-row weight-streaming INT8 kernels read fewer weight bytes below that.
+FP6_MIN_ROWS = 256
+_fp6_operands = os.getenv("CONVROT_FP6_OPERANDS", "1") != "0"
+
+
+def set_fp6_operands(enabled: bool) -> None:
+    """Turn the FP6 operand path of ConvRotLinear on or off (default on; the environment
+    variable CONVROT_FP6_OPERANDS=0 turns it off at import).  Outputs are the same bits
+    either way."""
+    global _fp6_operands
+    _fp6_operands = bool(enabled)
+
+
+def fp6_operands_enabled() -> bool:
+    return _fp6_operands
+
+
+def fp6_eligible(m: int, n: int, k: int, output_dtype: torch.dtype) -> bool:
+    """Whether a W4A4 product of this shape runs on FP6 operands in ConvRotLinear."""
+    return (_fp6_operands and m >= FP6_MIN_ROWS and k % 128 == 0 and n % 8 == 0
+            and output_dtype in (torch.bfloat16, torch.float16) and 2 * m * n < 2 ** 31)
+
+
+def fp6_weight(qweight: torch.Tensor, out_features: int, in_features: int) -> torch.Tensor:
+    """CDNA4 W4 weight -> FP6 operand blocks [K/128, ceil(N/16), 1536] (an offline
+    conversion; every int4 code, -8 included, has an FP6 field)."""
+    if in_features % 128:
+        raise ValueError(f"FP6 operands require in_features divisible by 128, got {in_features}")
+    nat.require_device(qweight)
+    _check_cdna4(qweight, out_features, in_features)
+    out = torch.empty(fp6_shape(out_features, in_features), dtype=torch.uint8, device=qweight.device)
+    nat.check(nat.load().convrot_weight_fp6(nat.ptr(qweight.contiguous()), nat.ptr(out), out_features, in_features,
+                                            nat.stream_of(qweight.device)))
+    return out
+
+
+def hip_fused_prepare_convrot_activation_fp6(x: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE):
+    """The fused preparation with FP6 output: (FP6 blocks [K/128, ceil(M/16), 1536] of the
+    A4 codes, float32 row scales).  Rows of a ragged last 16-row block are left unwritten
+    (they only reach product rows that are never stored)."""
+    _validate_fused(x, group_size, "FP6")
+    if x.shape[-1] % 128:
+        raise ValueError(f"FP6 operands require features divisible by 128, got {x.shape[-1]}")
+    return _prepare(x, group_size, nat.PREP_FP6)
+
+
+def hip_w4a4_fp6_matmul(act6, w6, xscales, wscales, bias, *, output_dtype, rows: int, out_features: int,
+                        in_features: int):
+    """FP6 A4 activations x FP6 W4 weight -> output_dtype [rows, out_features]: the product
+    and epilogue of hip_w4a4_int8_matmul (core.py:1088-1120), same bits."""
+    m, n, k = rows, out_features, in_features
+    if k % 128 or n % 8 or output_dtype not in (torch.bfloat16, torch.float16) or 2 * m * n >= 2 ** 31:
+        raise ValueError(f"FP6 W4A4 product needs K % 128 == 0, N % 8 == 0, a 16-bit output and 2*M*N < 2^31; "
+                         f"got M={m} N={n} K={k} {output_dtype}")
+    if tuple(act6.shape) != fp6_shape(m, k) or tuple(w6.shape) != fp6_shape(n, k):
+        raise ValueError(f"FP6 operands must be {fp6_shape(m, k)} and {fp6_shape(n, k)}, got "
+                         f"{tuple(act6.shape)} and {tuple(w6.shape)}")
+    _validate_mpp_epilogue(m, n, xscales, wscales, bias)
+    nat.require_device(act6, w6, xscales, wscales, bias)
+    xs, ws, b = _f32(xscales), _f32(wscales), _f32(bias)
+    out = torch.empty((m, n), dtype=output_dtype, device=act6.device)
+    nat.check(nat.load().convrot_w4a4_gemm_fp6(nat.ptr(act6), nat.ptr(xs), nat.ptr(w6), nat.ptr(ws), nat.ptr(b),
+                                               m, n, k, nat.ptr(out), nat.dtype_code(output_dtype),
+                                               nat.stream_of(act6.device)))
+    return out
+
+
 def hip_w4a16_matmul(activations, qweight, wscales, bias, *, output_dtype, out_features=None, residual=None,
                      gate=None, inplace=False):
     """Rotated bf16/f16 activations x W4 weight -> output_dtype (core.py:1123-1152);
@@ -779,6 +853,7 @@ class ConvRotLinear(nn.Module):
         self.register_buffer("bias", torch.zeros((out_features,), dtype=torch.float32, device=device))
         self.source_has_bias = bias
         self._cdna4_cache: tuple | None = None
+        self._fp6_cache: tuple | None = None
 
     @property
     def a4(self) -> bool:
@@ -815,6 +890,13 @@ class ConvRotLinear(nn.Module):
             self._cdna4_cache = (key, repack_mpp_weight_for_cdna4(q))
         return self._cdna4_cache[1]
 
+    def _fp6_weight(self, w: torch.Tensor) -> torch.Tensor:
+        """The FP6 operand form of the CDNA4 weight `w`, converted once and cached."""
+        key = (w.data_ptr(), w._version, tuple(w.shape), w.device)
+        if self._fp6_cache is None or self._fp6_cache[0] != key:
+            self._fp6_cache = (key, fp6_weight(w, self.out_features, self.in_features))
+        return self._fp6_cache[1]
+
     def _project(self, prep, lead: tuple, dtype: torch.dtype, residual, gate, inplace: bool) -> torch.Tensor:
         """Run the prepared activation `prep(mode)` through this layer's GEMM, then the
         optional gated residual (residual + gate * linear) in the GEMM's epilogue."""
@@ -822,7 +904,12 @@ class ConvRotLinear(nn.Module):
             raise ValueError("gate and inplace need a residual")
         out_shape = (*lead, self.out_features)
         w = self._device_weight()
-        if self.a4:
+        rows = math.prod(lead)
+        if self.a4 and residual is None and fp6_eligible(rows, self.out_features, self.in_features, dtype):
+            act6, xscales = prep(nat.PREP_FP6)
+            out = hip_w4a4_fp6_matmul(act6, self._fp6_weight(w), xscales, self.scales, self.bias, output_dtype=dtype,
+                                      rows=rows, out_features=self.out_features, in_features=self.in_features)
+        elif self.a4:
             gr = None if residual is None else _gated_residual(residual, gate, out_shape, dtype, inplace)
             qact, xscales = prep(nat.PREP_INT8)
             out = _w4a4(qact, nat.ACT_INT8, self.in_features, w, xscales, self.scales, self.bias, dtype,

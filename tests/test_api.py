@@ -114,3 +114,47 @@ def test_eligible_linear():
     assert not api.eligible_linear(torch.nn.Linear(500, 8))
     assert api.eligible_linear(torch.nn.Linear(192, 8), 64)
     assert not api.eligible_linear(torch.nn.Conv1d(4, 4, 1))
+
+
+def test_fp6_operand_policy():
+    """FP6 operands (same bits as INT8, twice the MFMA rate) are used by ConvRotLinear for the
+    plain epilogue at FP6_MIN_ROWS rows and above, K % 128 == 0, N % 8 == 0, 16-bit outputs;
+    set_fp6_operands switches the path off and on."""
+    was = api.fp6_operands_enabled()
+    try:
+        api.set_fp6_operands(True)
+        m = api.core.FP6_MIN_ROWS
+        assert api.fp6_eligible(4608, 12288, 3072, torch.bfloat16)
+        assert api.fp6_eligible(m, 3072, 3072, torch.float16)
+        assert not api.fp6_eligible(m - 1, 3072, 3072, torch.bfloat16)  # few rows: INT8 weight streaming
+        assert not api.fp6_eligible(4608, 3072, 3072 + 64, torch.bfloat16)  # K % 128
+        assert not api.fp6_eligible(4608, 3076, 3072, torch.bfloat16)  # N % 8
+        assert not api.fp6_eligible(4608, 3072, 3072, torch.float32)  # 16-bit outputs only
+        assert not api.fp6_eligible(2 ** 20, 2 ** 11, 3072, torch.bfloat16)  # 2 M N >= 2^31
+        api.set_fp6_operands(False)
+        assert not api.fp6_eligible(4608, 12288, 3072, torch.bfloat16)
+    finally:
+        api.set_fp6_operands(was)
+
+
+def test_fp6_functional_validation():
+    """The FP6 entry points check shapes before any launch (and never compute on the CPU)."""
+    a6 = torch.zeros(api.core.fp6_shape(300, 256), dtype=torch.uint8)
+    w6 = torch.zeros(api.core.fp6_shape(64, 256), dtype=torch.uint8)
+    xs, ws, b = torch.ones(300), torch.ones(64), torch.zeros(64)
+    with pytest.raises(ValueError, match="K % 128"):
+        api.hip_w4a4_fp6_matmul(a6, w6, xs, ws, b, output_dtype=torch.bfloat16, rows=300, out_features=64,
+                                in_features=192)
+    with pytest.raises(ValueError, match="16-bit output"):
+        api.hip_w4a4_fp6_matmul(a6, w6, xs, ws, b, output_dtype=torch.float32, rows=300, out_features=64,
+                                in_features=256)
+    with pytest.raises(ValueError, match="FP6 operands must be"):
+        api.hip_w4a4_fp6_matmul(a6, w6, xs, ws, b, output_dtype=torch.bfloat16, rows=400, out_features=64,
+                                in_features=256)
+    with pytest.raises(ValueError, match="divisible by 128"):
+        api.hip_fused_prepare_convrot_activation_fp6(torch.zeros(4, 64, dtype=torch.bfloat16), 64)
+    with pytest.raises(ValueError, match="divisible by 128"):
+        api.fp6_weight(torch.zeros((1, 4, 1024), dtype=torch.uint8), 64, 192)
+    with pytest.raises(Exception):
+        api.hip_w4a4_fp6_matmul(a6, w6, xs, ws, b, output_dtype=torch.bfloat16, rows=300, out_features=64,
+                                in_features=256)  # CPU tensors: no fallback

@@ -232,12 +232,15 @@ FLUX_SHAPES = [(1536, 64, 3072, 9216), (1536, 64, 3072, 3072), (1536, 64, 3072, 
                (4608, 256, 3072, 21504), (4608, 256, 15360, 3072)]
 
 
+@pytest.mark.parametrize("operands", ["fp6", "int8"])
 @pytest.mark.parametrize("M,G,K,N", FLUX_SHAPES)
-def test_flux_shapes_complete_path(orc, dev, M, G, K, N):
+def test_flux_shapes_complete_path(orc, dev, M, G, K, N, operands):
     """benchmark configs 2/3 at full size through ConvRotLinear (prep kernel -> GEMM kernel),
-    on the configs' heavy-tailed inputs.  Every weight code and scale, every activation code
-    and scale, and every output must equal the oracle's bit for bit (the oracle's dots come
-    from w4a4_dots_exact, its epilogue from the C restatement)."""
+    on the configs' heavy-tailed inputs, on FP6 operands (the default at these sizes) and on
+    INT8 operands.  Every weight code and scale, every activation code and scale (and, on
+    FP6, every byte of the FP6 activation blocks), and every output must equal the oracle's
+    bit for bit (the oracle's dots come from w4a4_dots_exact, its epilogue from the C
+    restatement)."""
     api = _api()
     x = outlier_input(K + N, (M, K), "bfloat16", orc)
     w = outlier_input(K * 3 + N, (N, K), "bfloat16", orc, std=0.02, frac=0.01, factor=10.0)
@@ -246,7 +249,13 @@ def test_flux_shapes_complete_path(orc, dev, M, G, K, N):
     qw, ws = api.quantize_convrot_weight(wd, G)
     layer = api.ConvRotLinear(K, N, group_size=G, backend="hip-w4a4", device=dev)
     layer.load_nk_weight(qw, ws, torch.from_numpy(bias).to(dev))
-    y = from_dev(layer(xd))
+    was = api.fp6_operands_enabled()
+    api.set_fp6_operands(operands == "fp6")
+    try:
+        assert api.fp6_eligible(M, N, K, torch.bfloat16) == (operands == "fp6")
+        y = from_dev(layer(xd))
+    finally:
+        api.set_fp6_operands(was)
     a_dev, xs_dev = api.hip_fused_prepare_convrot_activation_i8(xd, G)
     w_codes, wscales = orc.prepare_codes(w, "bfloat16", G)
     assert np.array_equal(from_dev(ws), wscales), "weight scales"
@@ -254,8 +263,12 @@ def test_flux_shapes_complete_path(orc, dev, M, G, K, N):
     a_codes, xs = orc.prepare_codes(x, "bfloat16", G)
     assert np.array_equal(from_dev(xs_dev), xs), "activation scales"
     assert np.array_equal(from_dev(a_dev), a_codes), "activation codes"
+    if operands == "fp6":
+        a6, xs6 = api.hip_fused_prepare_convrot_activation_fp6(xd, G)
+        assert np.array_equal(from_dev(xs6), xs), "activation scales (FP6 preparation)"
+        assert np.array_equal(from_dev(a6), orc.codes_to_fp6(a_codes)), "FP6 activation blocks"
     expected = orc.w4a4_matmul_codes_large(a_codes, w_codes, xs, wscales, bias, "bfloat16")
-    _assert_exact(y, expected, f"{M}x{K}->{N}")
+    _assert_exact(y, expected, f"{M}x{K}->{N} {operands}")
 
 
 @pytest.mark.parametrize("cfg", ["A", "B", "C", "F"])
