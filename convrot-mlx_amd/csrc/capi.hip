@@ -92,7 +92,8 @@ int convrot_set_tuning(const char* name, const char* value) {
                 {"gemm_smallm_max", kTuneGemmSmallmMax}, {"w4a4_smallm_cfg", kTuneW4a4SmallmCfg},
                 {"w4a16_cfg", kTuneW4a16Cfg},         {"w4a16_tile", kTuneW4a16Tile},
                 {"prep_ni", kTunePrepNi},             {"sk_spin_limit", kTuneSkSpinLimit},
-                {"gemm_persist", kTuneGemmPersist},   {"gemm_mfma32", kTuneGemmMfma32}};
+                {"gemm_persist", kTuneGemmPersist},   {"gemm_mfma32", kTuneGemmMfma32},
+                {"fp6_tile", kTuneFp6Tile}};
   int key = -1;
   for (const auto& n : kNames)
     if (strcmp(n.name, name) == 0) key = n.key;
@@ -109,6 +110,7 @@ int convrot_set_tuning(const char* name, const char* value) {
         v = bm | bn << 10 | wm << 20 | wn << 24 | st << 28;
         break;
       }
+      case kTuneFp6Tile:
       case kTuneW4a16Tile: {
         int bm = 0, bn = 0;
         good = sscanf(value, "%dx%d", &bm, &bn) == 2 && bm > 0 && bm <= 512 && bn > 0 && bn <= 512;

@@ -27,6 +27,7 @@ enum TuneKey : int {
   kTuneSkSpinLimit,      // stream-K bounded wait: polls before an owner gives up
   kTuneGemmPersist,      // persistent 4-wave W4A4 kernel: 0 never, G > 0 always, on a grid of G workgroups
   kTuneGemmMfma32,       // 1: the 4-wave 256x256 tile on v_mfma_i32_32x32x32_i8
+  kTuneFp6Tile,          // FP6 W4A4 tile: bm | bn << 10
   kTuneCount
 };
 int tuning(TuneKey key);

@@ -1406,16 +1406,18 @@ struct Fp6Engine {
   static constexpr int NW = 4, STAGES = 3;
   static constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 16, FN = TN / 16, HM = FM / 2;
   static constexpr int A_BYTES = (BM / 16) * 1536, B_BYTES = (BN / 16) * 1536, STAGE_BYTES = A_BYTES + B_BYTES;
-  static constexpr int A_DMAS = A_BYTES / 1024, B_DMAS = B_BYTES / 1024, LOADS = A_DMAS + B_DMAS;
-  static constexpr int LPW = LOADS / NW, APW = A_DMAS / NW, BPW = B_DMAS / NW;
+  // 1 KB DMA pieces per k-block; a wave issues APW + BPW of them (a count that
+  // does not divide by the waves is padded with repeats of the last piece,
+  // which rewrite the same bytes)
+  static constexpr int A_DMAS = A_BYTES / 1024, B_DMAS = B_BYTES / 1024;
+  static constexpr int APW = (A_DMAS + NW - 1) / NW, BPW = (B_DMAS + NW - 1) / NW, LPW = APW + BPW;
   static constexpr int XS_DMAS = (BM * 4 + 255) / 256, WS_DMAS = (BN * 4 + 255) / 256;
   static constexpr int EPI_DMAS = XS_DMAS + 2 * WS_DMAS;
   static constexpr int EPI_OFF = STAGES * STAGE_BYTES;
   static constexpr int WS_OFF = EPI_OFF + XS_DMAS * 256, BIAS_OFF = WS_OFF + WS_DMAS * 256;
   static constexpr int SMEM_BYTES = EPI_OFF + EPI_DMAS * 256;
   static constexpr int RS = TN * 2 + 16, STAGING = TM * RS;
-  static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0 && A_DMAS % NW == 0 && B_DMAS % NW == 0,
-                "whole DMA pieces per wave");
+  static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole DMA pieces (BM and BN multiples of 32)");
   static_assert(FM % 2 == 0 && NW * STAGING <= EPI_OFF && SMEM_BYTES <= 160 * 1024, "LDS of one CU");
   static_assert((STAGES - 1) * LPW <= 63, "vmcnt counts at most 63 DMAs");
 
@@ -1464,12 +1466,12 @@ struct Fp6Engine {
   __device__ __forceinline__ void issue_piece(int kb, int stage, int idx) {
     const uint32_t base = smem_addr + (uint32_t)(stage * STAGE_BYTES);
     if (idx < APW) {
-      const uint32_t j = (uint32_t)(wave * APW + idx);
+      const uint32_t j = (uint32_t)min(wave * APW + idx, A_DMAS - 1);
       uint32_t so = j * 1024u + (uint32_t)kb * a_kstride;
       asm volatile("" : "+s"(so));
       dma16(ra, vl + so, base + j * 1024u);
     } else {
-      const uint32_t j = (uint32_t)(wave * BPW + idx - APW);
+      const uint32_t j = (uint32_t)min(wave * BPW + idx - APW, B_DMAS - 1);
       uint32_t so = j * 1024u + (uint32_t)kb * w_kstride;
       asm volatile("" : "+s"(so));
       dma16(rw, vl + so, base + (uint32_t)A_BYTES + j * 1024u);
@@ -2338,18 +2340,68 @@ int w4a4_workspace_status(const void* workspace, hipStream_t stream, const char*
 
 // FP6-operand W4A4 GEMM (activation and weight layouts above; K % 128 == 0,
 // N % 8 == 0, 16-bit output, 2 M N < 2^31).
+namespace {
+
+// FP6 tiles and the time per tile each takes relative to 256 x 256 (per tile,
+// at the same K).  The plan takes the tile with the least modelled time,
+// rounds of whole tiles over the CUs times the tile's relative time: at 4608
+// tokens, 256 x 224 turns 216 tiles (N = 3072) into 252 and 864 (N = 12288)
+// into 990, both a near-whole number of rounds; 128 x 256 fills the CUs at a
+// few thousand tokens.
+struct Fp6Tile {
+  int bm, bn;
+  double rel;
+};
+constexpr Fp6Tile kFp6Tiles[3] = {{256, 256, 1.0}, {256, 224, 0.9}, {128, 256, 0.62}};
+
+Fp6Tile fp6_tile(int64_t M, int64_t N) {
+  const int forced = tuning(kTuneFp6Tile);
+  if (forced >= 0)
+    for (const Fp6Tile& t : kFp6Tiles)
+      if ((forced & 1023) == t.bm && (forced >> 10) == t.bn) return t;
+  const int64_t cus = device_cus();
+  Fp6Tile best = kFp6Tiles[0];
+  double best_cost = -1.0;
+  for (const Fp6Tile& t : kFp6Tiles) {
+    const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+    const double cost = (double)((tiles + cus - 1) / cus) * t.rel;
+    if (best_cost < 0 || cost < best_cost - 1e-9) {
+      best = t;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
+template <int BM, int BN, int ODT>
+hipError_t launch_fp6_tile(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
+                           const float* bias, int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+  const int nblocks = (int)((N + 15) / 16);
+  const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
+  hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<BM, BN, ODT>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, act6,
+                     xscales, w6, wscales, bias, out, (int)M, (int)N, (int)K, nblocks, tm, tn);
+  return hipGetLastError();
+}
+
+template <int ODT>
+hipError_t launch_fp6_t(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
+                        const float* bias, int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+  const Fp6Tile t = fp6_tile(M, N);
+  if (t.bm == 256 && t.bn == 224)
+    return launch_fp6_tile<256, 224, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, stream);
+  if (t.bm == 128)
+    return launch_fp6_tile<128, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, stream);
+  return launch_fp6_tile<256, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, stream);
+}
+
+}  // namespace
+
 hipError_t launch_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
                                 const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
                                 hipStream_t stream) {
-  const int nblocks = (int)((N + 15) / 16);
-  const int tm = (int)((M + 255) / 256), tn = (int)((N + 255) / 256);
-  if (out_dtype == kBF16)
-    hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<256, 256, kBF16>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, act6,
-                       xscales, w6, wscales, bias, out, (int)M, (int)N, (int)K, nblocks, tm, tn);
-  else
-    hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<256, 256, kF16>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, act6,
-                       xscales, w6, wscales, bias, out, (int)M, (int)N, (int)K, nblocks, tm, tn);
-  return hipGetLastError();
+  if (M == 0 || N == 0) return hipSuccess;
+  if (out_dtype == kBF16) return launch_fp6_t<kBF16>(act6, xscales, w6, wscales, bias, M, N, K, out, stream);
+  return launch_fp6_t<kF16>(act6, xscales, w6, wscales, bias, M, N, K, out, stream);
 }
 
 }  // namespace convrot

@@ -232,3 +232,24 @@ def test_fp6_complete_path_equals_int8_path(orc, dev, M, G, K, N):
     got = _gemm_fp6(nat, a6, xs6, w6, ws.float().contiguous(), bias.float().contiguous(), M, N, K, torch.bfloat16, dev)
     assert torch.equal(xs6, xs8)
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("tile", ["256x256", "256x224", "128x256"])
+@pytest.mark.parametrize("M,K,N", [(300, 384, 1000), (37, 128, 48), (520, 1536, 264), (1000, 640, 232)])
+def test_fp6_every_tile(orc, dev, tuning, tile, M, K, N):
+    """Each FP6 tile (forced through the fp6_tile tuning override) on ragged M / N tails --
+    partial 224- and 256-wide column tiles, partial 128- and 256-row tiles -- bit-exact
+    against the oracle, in bf16 and f16."""
+    nat = _nat()
+    tuning.set("fp6_tile", tile)
+    rng = np.random.default_rng(M * 3 + K + N)
+    a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    b = rng.normal(size=(N,)).astype(np.float32)
+    args = (_u8(orc.codes_to_fp6(a), dev), _u8(xs, dev), _u8(orc.codes_to_fp6(w), dev), _u8(ws, dev), _u8(b, dev))
+    for out_dtype, dt in (("bfloat16", torch.bfloat16), ("float16", torch.float16)):
+        out = _gemm_fp6(nat, *args, M, N, K, dt, dev)
+        _assert_exact(from_dev(out), orc.w4a4_matmul_codes_large(a, w, xs, ws, b, out_dtype),
+                      f"tile {tile} {M}x{K}x{N} {out_dtype}")
