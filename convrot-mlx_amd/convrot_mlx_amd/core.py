@@ -664,9 +664,11 @@ def hip_w4a4_int8_matmul(activations, qweight, xscales, wscales, bias, *, output
 # instruction, with both operand scales 2^3, sums the exact products v*w at
 # twice the INT8 instruction's rate: the same GEMM with the same outputs bit
 # for bit (layout and encoding in include/convrot_amd.h).  ConvRotLinear
-# takes this path for the plain epilogue at FP6_MIN_ROWS rows and above; the
-# few-row weight-streaming INT8 kernels read fewer weight bytes below that.
+# takes this path at FP6_MIN_ROWS rows and above when in_features % 128 == 0;
+# below that the few-row INT8 kernels, which stream half a byte of weight per
+# code instead of three quarters, are as fast or faster.
 FP6_MIN_ROWS = 256
+FP6_MAX_FEATURES = 262144  # exclusive: sums of K products of |v*w| <= 64 stay below 2^24
 _fp6_operands = os.getenv("CONVROT_FP6_OPERANDS", "1") != "0"
 
 
@@ -684,8 +686,8 @@ def fp6_operands_enabled() -> bool:
 
 def fp6_eligible(m: int, n: int, k: int, output_dtype: torch.dtype) -> bool:
     """Whether a W4A4 product of this shape runs on FP6 operands in ConvRotLinear."""
-    return (_fp6_operands and m >= FP6_MIN_ROWS and k % 128 == 0 and n % 8 == 0
-            and output_dtype in (torch.bfloat16, torch.float16) and 2 * m * n < 2 ** 31)
+    return (_fp6_operands and m >= FP6_MIN_ROWS and k % 128 == 0 and 0 < k < FP6_MAX_FEATURES
+            and output_dtype in (torch.bfloat16, torch.float16, torch.float32))
 
 
 def fp6_weight(qweight: torch.Tensor, out_features: int, in_features: int) -> torch.Tensor:
@@ -711,25 +713,49 @@ def hip_fused_prepare_convrot_activation_fp6(x: torch.Tensor, group_size: int = 
     return _prepare(x, group_size, nat.PREP_FP6)
 
 
-def hip_w4a4_fp6_matmul(act6, w6, xscales, wscales, bias, *, output_dtype, rows: int, out_features: int,
-                        in_features: int):
-    """FP6 A4 activations x FP6 W4 weight -> output_dtype [rows, out_features]: the product
-    and epilogue of hip_w4a4_int8_matmul (core.py:1088-1120), same bits."""
-    m, n, k = rows, out_features, in_features
-    if k % 128 or n % 8 or output_dtype not in (torch.bfloat16, torch.float16) or 2 * m * n >= 2 ** 31:
-        raise ValueError(f"FP6 W4A4 product needs K % 128 == 0, N % 8 == 0, a 16-bit output and 2*M*N < 2^31; "
-                         f"got M={m} N={n} K={k} {output_dtype}")
+def _w4a4_fp6(act6, w6, xscales, wscales, bias, output_dtype, m: int, n: int, k: int,
+              gr: GatedResidual | None = None):
+    if k % 128 or not 0 < k < FP6_MAX_FEATURES or output_dtype not in (torch.bfloat16, torch.float16,
+                                                                         torch.float32):
+        raise ValueError(f"FP6 W4A4 product needs K % 128 == 0 with K < {FP6_MAX_FEATURES} and a float32, "
+                         f"float16 or bfloat16 output; got M={m} N={n} K={k} {output_dtype}")
     if tuple(act6.shape) != fp6_shape(m, k) or tuple(w6.shape) != fp6_shape(n, k):
         raise ValueError(f"FP6 operands must be {fp6_shape(m, k)} and {fp6_shape(n, k)}, got "
                          f"{tuple(act6.shape)} and {tuple(w6.shape)}")
     _validate_mpp_epilogue(m, n, xscales, wscales, bias)
     nat.require_device(act6, w6, xscales, wscales, bias)
     xs, ws, b = _f32(xscales), _f32(wscales), _f32(bias)
-    out = torch.empty((m, n), dtype=output_dtype, device=act6.device)
-    nat.check(nat.load().convrot_w4a4_gemm_fp6(nat.ptr(act6), nat.ptr(xs), nat.ptr(w6), nat.ptr(ws), nat.ptr(b),
-                                               m, n, k, nat.ptr(out), nat.dtype_code(output_dtype),
-                                               nat.stream_of(act6.device)))
+    if gr is not None and gr.residual.numel() != m * n:
+        raise ValueError(f"residual has {gr.residual.numel()} elements, the output {m * n}")
+    if gr is not None and gr.inplace:
+        out = gr.residual.view(m, n)
+    else:
+        out = torch.empty((m, n), dtype=output_dtype, device=act6.device)
+    lib, stream = nat.load(), nat.stream_of(act6.device)
+    if gr is None:
+        nat.check(lib.convrot_w4a4_gemm_fp6(nat.ptr(act6), nat.ptr(xs), nat.ptr(w6), nat.ptr(ws), nat.ptr(b), m, n, k,
+                                            nat.ptr(out), nat.dtype_code(output_dtype), stream))
+    else:
+        nat.check(lib.convrot_w4a4_gemm_fp6_residual(
+            nat.ptr(act6), nat.ptr(xs), nat.ptr(w6), nat.ptr(ws), nat.ptr(b), m, n, k, nat.ptr(gr.residual),
+            nat.ptr(gr.gate), gr.stride, gr.rows_per_gate, nat.ptr(out), nat.dtype_code(output_dtype), stream))
     return out
+
+
+def hip_w4a4_fp6_matmul(act6, w6, xscales, wscales, bias, *, output_dtype, rows: int, out_features: int,
+                        in_features: int, residual=None, gate=None, inplace=False):
+    """FP6 A4 activations x FP6 W4 weight -> output_dtype [rows, out_features]: the product
+    and epilogue of hip_w4a4_int8_matmul (core.py:1088-1120), same bits; residual, gate and
+    inplace as in hip_w4a4_matmul."""
+    m, n = rows, out_features
+    gr = None
+    if residual is not None:
+        if residual.ndim < 1 or residual.shape[-1] != n or residual.numel() != m * n:
+            raise ValueError(f"residual {tuple(residual.shape)} must hold the [{m}, {n}] output as [..., {n}]")
+        gr = _gated_residual(residual, gate, tuple(residual.shape), output_dtype, inplace)
+    elif gate is not None or inplace:
+        raise ValueError("gate and inplace need a residual")
+    return _w4a4_fp6(act6, w6, xscales, wscales, bias, output_dtype, m, n, in_features, gr)
 
 
 def hip_w4a16_matmul(activations, qweight, wscales, bias, *, output_dtype, out_features=None, residual=None,
@@ -905,12 +931,13 @@ class ConvRotLinear(nn.Module):
         out_shape = (*lead, self.out_features)
         w = self._device_weight()
         rows = math.prod(lead)
-        if self.a4 and residual is None and fp6_eligible(rows, self.out_features, self.in_features, dtype):
-            act6, xscales = prep(nat.PREP_FP6)
-            out = hip_w4a4_fp6_matmul(act6, self._fp6_weight(w), xscales, self.scales, self.bias, output_dtype=dtype,
-                                      rows=rows, out_features=self.out_features, in_features=self.in_features)
-        elif self.a4:
+        if self.a4:
             gr = None if residual is None else _gated_residual(residual, gate, out_shape, dtype, inplace)
+        if self.a4 and fp6_eligible(rows, self.out_features, self.in_features, dtype):
+            act6, xscales = prep(nat.PREP_FP6)
+            out = _w4a4_fp6(act6, self._fp6_weight(w), xscales, self.scales, self.bias, dtype, rows,
+                            self.out_features, self.in_features, gr)
+        elif self.a4:
             qact, xscales = prep(nat.PREP_INT8)
             out = _w4a4(qact, nat.ACT_INT8, self.in_features, w, xscales, self.scales, self.bias, dtype,
                         self.out_features, gr)

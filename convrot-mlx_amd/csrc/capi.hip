@@ -306,22 +306,34 @@ int convrot_w4a4_gemm(const void* act, int act_format, const float* xscales, con
                        "convrot_w4a4_gemm");
 }
 
-int convrot_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
-                          const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype, void* stream) {
-  if (M < 0 || N < 0 || K <= 0 || K % 128 || M > INT32_MAX || N > INT32_MAX || K > 300000)
-    return fail(CONVROT_ERR_INVALID, "FP6 W4A4 GEMM: bad shape M=%lld N=%lld K=%lld (K a multiple of 128)",
-                (long long)M, (long long)N, (long long)K);
-  if (out_dtype != CONVROT_DTYPE_BF16 && out_dtype != CONVROT_DTYPE_F16)
-    return fail(CONVROT_ERR_INVALID, "FP6 W4A4 GEMM: 16-bit outputs only");
-  if (N % 8 || M * N * 2 >= ((int64_t)1 << 31))
-    return fail(CONVROT_ERR_INVALID, "FP6 W4A4 GEMM: N must be a multiple of 8 and 2*M*N < 2^31");
+namespace {
+
+int check_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales, int64_t M,
+              int64_t N, int64_t K, void* out, int out_dtype, int* odt) {
+  if (M < 0 || N < 0 || K <= 0 || K % 128 || M > INT32_MAX || N > INT32_MAX || K >= 262144)
+    return fail(CONVROT_ERR_INVALID,
+                "FP6 W4A4 GEMM: bad shape M=%lld N=%lld K=%lld (K a multiple of 128 below 262144)", (long long)M,
+                (long long)N, (long long)K);
+  if (out_dtype != CONVROT_DTYPE_BF16 && out_dtype != CONVROT_DTYPE_F16 && out_dtype != CONVROT_DTYPE_F32)
+    return fail(CONVROT_ERR_INVALID, "unsupported output dtype %d", out_dtype);
+  *odt = out_dtype == CONVROT_DTYPE_BF16 ? convrot::kBF16 : out_dtype == CONVROT_DTYPE_F16 ? convrot::kF16
+                                                                                             : convrot::kF32;
   if (M == 0 || N == 0) return ok();
   if (!act6 || !xscales || !w6 || !wscales || !out) return fail(CONVROT_ERR_INVALID, "null pointer argument");
   if (!aligned(act6, 16) || !aligned(w6, 16) || !aligned(out, 16))
     return fail(CONVROT_ERR_INVALID, "act6, w6 and out must be 16-byte aligned");
-  const int odt = out_dtype == CONVROT_DTYPE_BF16 ? convrot::kBF16 : convrot::kF16;
+  return ok();
+}
+
+}  // namespace
+
+int convrot_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
+                          const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype, void* stream) {
+  int odt = 0;
+  if (int rc = check_fp6(act6, xscales, w6, wscales, M, N, K, out, out_dtype, &odt)) return rc;
+  if (M == 0 || N == 0) return ok();
   return launch_status(convrot::launch_w4a4_gemm_fp6(act6, xscales, w6, wscales, bias, M, N, K, out, odt,
-                                                     (hipStream_t)stream),
+                                                     (hipStream_t)stream, convrot::GatedResidual{}),
                        "convrot_w4a4_gemm_fp6");
 }
 
@@ -358,6 +370,22 @@ int convrot_w4a4_gemm_residual(const void* act, int act_format, const float* xsc
   return launch_status(convrot::launch_w4a4_gemm(act, act_format, xscales, qweight, wscales, bias, M, N, K, out,
                                                  out_dtype, (hipStream_t)stream, gr),
                        "convrot_w4a4_gemm_residual");
+}
+
+int convrot_w4a4_gemm_fp6_residual(const uint8_t* act6, const float* xscales, const uint8_t* w6,
+                                   const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
+                                   const void* residual, const void* gate, int64_t gate_stride,
+                                   int64_t rows_per_gate, void* out, int out_dtype, void* stream) {
+  int odt = 0;
+  if (int rc = check_fp6(act6, xscales, w6, wscales, M, N, K, out, out_dtype, &odt)) return rc;
+  if (gate && rows_per_gate <= 0)
+    return fail(CONVROT_ERR_INVALID, "rows_per_gate must be positive, got %lld", (long long)rows_per_gate);
+  if (M == 0 || N == 0) return ok();
+  convrot::GatedResidual gr{};
+  if (int rc = check_residual(residual, gate, gate_stride, rows_per_gate, M, N, &gr)) return rc;
+  return launch_status(convrot::launch_w4a4_gemm_fp6(act6, xscales, w6, wscales, bias, M, N, K, out, odt,
+                                                     (hipStream_t)stream, gr),
+                       "convrot_w4a4_gemm_fp6_residual");
 }
 
 int64_t convrot_w4a4_workspace_bytes(void) { return (int64_t)convrot::kSkWorkspaceBytes; }

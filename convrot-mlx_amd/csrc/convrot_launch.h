@@ -93,7 +93,7 @@ hipError_t noalloc_scratch(hipStream_t stream, Workspace* out);
 
 hipError_t launch_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
                                 const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
-                                hipStream_t stream);
+                                hipStream_t stream, const GatedResidual& gr);
 
 // Few-row W4A4 kernel (int8 activation codes only); launch_w4a4_gemm routes
 // small M here.

@@ -227,8 +227,19 @@ __global__ __launch_bounds__(WM* WN * 64) void w4a4_gemm_kernel(
 //
 // `poison` (a stream-K owner whose bounded wait for a partial tile gave up)
 // makes every output of the wave's tile NaN instead of a silently wrong value.
-template <int ODT, int TM, int TN, int SHIFT, bool LDS_OPS = false>
-__device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], uint8_t* region, int lane,
+// An accumulator element as the float the epilogue scales: int32 sums of
+// codes x 2^SHIFT, or (FP6 kernel) the exact float sum of code products.
+template <int SHIFT>
+__device__ __forceinline__ float acc_value(int v) {
+  return (float)(v >> SHIFT);
+}
+template <int SHIFT>
+__device__ __forceinline__ float acc_value(float v) {
+  return v;
+}
+
+template <int ODT, int TM, int TN, int SHIFT, bool LDS_OPS = false, class V = i32x4>
+__device__ __forceinline__ void epilogue(const V (&acc)[TN / 16][TM / 16], uint8_t* region, int lane,
                                          int mw, int nw, int M, int N, const float* __restrict__ xscales,
                                          const float* __restrict__ wscales, const float* __restrict__ bias,
                                          void* __restrict__ out, const GatedResidual& gr, int m0 = 0,
@@ -280,7 +291,7 @@ __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], u
         if (m >= M) continue;
         float o[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = (((float)(acc[fn][fm][r] >> SHIFT) * xs[fm]) * wsv[r]) + bv[r];
+        for (int r = 0; r < 4; ++r) o[r] = ((acc_value<SHIFT>(acc[fn][fm][r]) * xs[fm]) * wsv[r]) + bv[r];
         if (gr.residual) {
           if constexpr (FB > 1) gate_apply4<ODT>(ops[fm % FB], o);
           else gate_residual4<ODT>(gr, m, n, N, vec_ok, o);
@@ -318,7 +329,7 @@ __device__ __forceinline__ void epilogue(const i32x4 (&acc)[TN / 16][TM / 16], u
       for (int fm = 0; fm < FM; ++fm) {
         float o[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = (((float)(acc[fn][fm][r] >> SHIFT) * xs[fm]) * wsv[r]) + bv[r];
+        for (int r = 0; r < 4; ++r) o[r] = ((acc_value<SHIFT>(acc[fn][fm][r]) * xs[fm]) * wsv[r]) + bv[r];
         const uint2 w = ODT == kBF16 ? make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]))
                                      : make_uint2(pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3]));
         *(uint2*)(region + (fm * 16 + (lane & 15)) * RS + nl * 2) = w;
@@ -1099,16 +1110,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // as in `epilogue`, staged through the wave's LDS region and written as 16-byte
 // buffer stores; a chunk outside the M x N output gets an offset past the
 // buffer's range, which the hardware drops.  Needs N % 8 == 0 and 2 M N < 2^31.
-// An accumulator element as the float the epilogue scales: int32 sums of
-// codes x 2^SHIFT, or (FP6 kernel) the exact float sum of code products.
-template <int SHIFT>
-__device__ __forceinline__ float acc_value(int v) {
-  return (float)(v >> SHIFT);
-}
-template <int SHIFT>
-__device__ __forceinline__ float acc_value(float v) {
-  return v;
-}
 
 template <int ODT, int TM, int TN, int SHIFT, int FM0, int FM1, class V = i32x4>
 __device__ __forceinline__ void epilogue_pass(const V (&acc)[TN / 16][TM / 16], uint8_t* region, int lane,
@@ -1550,13 +1551,13 @@ struct Fp6Engine {
   }
 };
 
-// The 4-wave FP6 GEMM, one BM x BN tile per workgroup, plain 16-bit epilogue
-// (N % 8 == 0, 2 M N < 2^31).
+// The 4-wave FP6 GEMM, one BM x BN tile per workgroup, with the epilogue of
+// every W4A4 kernel (16-bit or float32 outputs, optional gated residual).
 template <int BM, int BN, int ODT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void w4a4_gemm_fp6_kernel(
     const uint8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
-    int K, int nblocks, int tiles_m, int tiles_n) {
+    int K, int nblocks, int tiles_m, int tiles_n, GatedResidual gr) {
   using E = Fp6Engine<BM, BN>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
   E e(smem);
@@ -1577,12 +1578,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   e.prologue(kblocks);
   e.run(kblocks, acc);
   __syncthreads();  // ring -> output staging
-  const __amdgpu_buffer_rsrc_t orsrc =
-      __builtin_amdgcn_make_buffer_rsrc(out, (short)0, (int)((int64_t)M * N * 2), 0x00020000);
-  epilogue_pass<ODT, E::TM, E::TN, 0, 0, E::FM, f32x4>(
-      acc, smem + e.wave * E::STAGING, e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M, N,
-      (const float*)(smem + E::EPI_OFF), (const float*)(smem + E::WS_OFF), (const float*)(smem + E::BIAS_OFF), orsrc,
-      m0, n0);
+  epilogue<ODT, E::TM, E::TN, 0, true>(acc, smem + e.wave * E::STAGING, e.lane, m0 + e.wm * E::TM,
+                                       n0 + e.wn * E::TN, M, N, (const float*)(smem + E::EPI_OFF),
+                                       (const float*)(smem + E::WS_OFF), (const float*)(smem + E::BIAS_OFF), out, gr,
+                                       m0, n0);
 }
 
 // ---- stream-K
@@ -2338,8 +2337,8 @@ int w4a4_workspace_status(const void* workspace, hipStream_t stream, const char*
   return 0;
 }
 
-// FP6-operand W4A4 GEMM (activation and weight layouts above; K % 128 == 0,
-// N % 8 == 0, 16-bit output, 2 M N < 2^31).
+// FP6-operand W4A4 GEMM (activation and weight layouts above; K % 128 == 0),
+// with the same epilogues as the INT8 kernels.
 namespace {
 
 // FP6 tiles and the time per tile each takes relative to 256 x 256 (per tile,
@@ -2375,33 +2374,38 @@ Fp6Tile fp6_tile(int64_t M, int64_t N) {
 
 template <int BM, int BN, int ODT>
 hipError_t launch_fp6_tile(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
-                           const float* bias, int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+                           const float* bias, int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr,
+                           hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16);
   const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
   hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<BM, BN, ODT>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, act6,
-                     xscales, w6, wscales, bias, out, (int)M, (int)N, (int)K, nblocks, tm, tn);
+                     xscales, w6, wscales, bias, out, (int)M, (int)N, (int)K, nblocks, tm, tn, gr);
   return hipGetLastError();
 }
 
 template <int ODT>
 hipError_t launch_fp6_t(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
-                        const float* bias, int64_t M, int64_t N, int64_t K, void* out, hipStream_t stream) {
+                        const float* bias, int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr,
+                        hipStream_t stream) {
   const Fp6Tile t = fp6_tile(M, N);
   if (t.bm == 256 && t.bn == 224)
-    return launch_fp6_tile<256, 224, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, stream);
+    return launch_fp6_tile<256, 224, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
   if (t.bm == 128)
-    return launch_fp6_tile<128, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, stream);
-  return launch_fp6_tile<256, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, stream);
+    return launch_fp6_tile<128, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+  return launch_fp6_tile<256, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
 }
 
 }  // namespace
 
 hipError_t launch_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
                                 const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
-                                hipStream_t stream) {
+                                hipStream_t stream, const GatedResidual& gr) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (out_dtype == kBF16) return launch_fp6_t<kBF16>(act6, xscales, w6, wscales, bias, M, N, K, out, stream);
-  return launch_fp6_t<kF16>(act6, xscales, w6, wscales, bias, M, N, K, out, stream);
+  switch (out_dtype) {
+    case kF32: return launch_fp6_t<kF32>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+    case kF16: return launch_fp6_t<kF16>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+    default: return launch_fp6_t<kBF16>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+  }
 }
 
 }  // namespace convrot

@@ -299,13 +299,24 @@ int convrot_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K,
 
 /*
  * convrot_w4a4_gemm on FP6 operands: act6 from convrot_prepare(..., CONVROT_PREP_FP6,
- * ...), w6 from convrot_weight_fp6.  Same epilogue and outputs as
- * convrot_w4a4_gemm with act_format CONVROT_ACT_INT8.  out_dtype f16 or bf16,
- * K % 128 == 0, N % 8 == 0, 2 M N < 2^31.
+ * ...), w6 from convrot_weight_fp6.  Same epilogue and outputs, bit for bit, as
+ * convrot_w4a4_gemm with act_format CONVROT_ACT_INT8 (out_dtype f32, f16 or
+ * bf16); K a multiple of 128 below 262144.  Replaces the same launch site
+ * (core.py:1088-1120).
  */
 int convrot_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6,
                           const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
                           void* out, int out_dtype, void* stream);
+
+/*
+ * convrot_w4a4_gemm_fp6 followed by the gated residual of
+ * convrot_w4a4_gemm_residual (same arguments and rounding; no counterpart in
+ * the reference).
+ */
+int convrot_w4a4_gemm_fp6_residual(const uint8_t* act6, const float* xscales, const uint8_t* w6,
+                                   const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
+                                   const void* residual, const void* gate, int64_t gate_stride,
+                                   int64_t rows_per_gate, void* out, int out_dtype, void* stream);
 
 /* Thread-local message of the last failed call on this thread ("" if none). */
 const char* convrot_last_error(void);

@@ -117,20 +117,19 @@ def test_eligible_linear():
 
 
 def test_fp6_operand_policy():
-    """FP6 operands (same bits as INT8, twice the MFMA rate) are used by ConvRotLinear for the
-    plain epilogue at FP6_MIN_ROWS rows and above, K % 128 == 0, N % 8 == 0, 16-bit outputs;
-    set_fp6_operands switches the path off and on."""
+    """FP6 operands (same bits as INT8, twice the MFMA rate) are used by ConvRotLinear at
+    FP6_MIN_ROWS rows and above with in_features % 128 == 0 (below 262144); set_fp6_operands
+    switches the path off and on."""
     was = api.fp6_operands_enabled()
     try:
         api.set_fp6_operands(True)
         m = api.core.FP6_MIN_ROWS
         assert api.fp6_eligible(4608, 12288, 3072, torch.bfloat16)
-        assert api.fp6_eligible(m, 3072, 3072, torch.float16)
+        assert api.fp6_eligible(m, 3076, 3072, torch.float16)  # any N
+        assert api.fp6_eligible(m, 3072, 3072, torch.float32)
         assert not api.fp6_eligible(m - 1, 3072, 3072, torch.bfloat16)  # few rows: INT8 weight streaming
         assert not api.fp6_eligible(4608, 3072, 3072 + 64, torch.bfloat16)  # K % 128
-        assert not api.fp6_eligible(4608, 3076, 3072, torch.bfloat16)  # N % 8
-        assert not api.fp6_eligible(4608, 3072, 3072, torch.float32)  # 16-bit outputs only
-        assert not api.fp6_eligible(2 ** 20, 2 ** 11, 3072, torch.bfloat16)  # 2 M N >= 2^31
+        assert not api.fp6_eligible(4608, 3072, 262144, torch.bfloat16)  # sums no longer exact in float32
         api.set_fp6_operands(False)
         assert not api.fp6_eligible(4608, 12288, 3072, torch.bfloat16)
     finally:
@@ -145,9 +144,12 @@ def test_fp6_functional_validation():
     with pytest.raises(ValueError, match="K % 128"):
         api.hip_w4a4_fp6_matmul(a6, w6, xs, ws, b, output_dtype=torch.bfloat16, rows=300, out_features=64,
                                 in_features=192)
-    with pytest.raises(ValueError, match="16-bit output"):
-        api.hip_w4a4_fp6_matmul(a6, w6, xs, ws, b, output_dtype=torch.float32, rows=300, out_features=64,
+    with pytest.raises(ValueError, match="float32, float16 or bfloat16"):
+        api.hip_w4a4_fp6_matmul(a6, w6, xs, ws, b, output_dtype=torch.float64, rows=300, out_features=64,
                                 in_features=256)
+    with pytest.raises(ValueError, match="gate and inplace need a residual"):
+        api.hip_w4a4_fp6_matmul(a6, w6, xs, ws, b, output_dtype=torch.bfloat16, rows=300, out_features=64,
+                                in_features=256, inplace=True)
     with pytest.raises(ValueError, match="FP6 operands must be"):
         api.hip_w4a4_fp6_matmul(a6, w6, xs, ws, b, output_dtype=torch.bfloat16, rows=400, out_features=64,
                                 in_features=256)

@@ -55,6 +55,8 @@ def _gemm_fp6(nat, a6, xs, w6, ws, b, M, N, K, dtype, dev):
 
 
 def _assert_exact(got, want, label):
+    if want.dtype == np.float32:
+        got, want = got.view(np.uint32), want.view(np.uint32)
     bad = int((got != want).sum())
     assert bad == 0, f"{label}: {bad} of {want.size} differ"
 
@@ -167,12 +169,13 @@ def test_modulated_and_gelu_producers_fp6(orc, dev):
     _assert_exact(from_dev(g6).reshape(-1)[: want.size], want, "gelu")
 
 
-@pytest.mark.parametrize("out_dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("out_dtype", ["bfloat16", "float16", "float32"])
 @pytest.mark.parametrize("M,K,N", [(300, 128, 264), (37, 384, 48), (1000, 640, 1000), (520, 1536, 1000),
-                                   (4608, 3072, 3072)])
+                                   (4608, 3072, 3072), (301, 256, 1003), (33, 128, 46)])
 def test_fp6_gemm_matches_oracle(orc, dev, out_dtype, M, K, N):
-    """FP6-operand GEMM, every output bit-exact against the oracle: ragged tiles, one and many
-    k-blocks, all-zero activation rows (+0 sums) and a row of extreme codes."""
+    """FP6-operand GEMM, every output bit-exact against the oracle: ragged tiles (N not a
+    multiple of 8 included), one and many k-blocks, all-zero activation rows (+0 sums), a row
+    of extreme codes, 16-bit and float32 outputs."""
     nat = _nat()
     rng = np.random.default_rng(M + K + N)
     a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
@@ -184,7 +187,7 @@ def test_fp6_gemm_matches_oracle(orc, dev, out_dtype, M, K, N):
     ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
     b = rng.normal(size=(N,)).astype(np.float32)
     b[:4] = 0.0
-    dt = {"bfloat16": torch.bfloat16, "float16": torch.float16}[out_dtype]
+    dt = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}[out_dtype]
     out = _gemm_fp6(nat, _u8(orc.codes_to_fp6(a), dev), _u8(xs, dev), _u8(orc.codes_to_fp6(w), dev), _u8(ws, dev),
                     _u8(b, dev), M, N, K, dt, dev)
     _assert_exact(from_dev(out), orc.w4a4_matmul_codes_large(a, w, xs, ws, b, out_dtype), f"{M}x{K}x{N}")

@@ -42,9 +42,12 @@ PATHS = {
     "register": ({"gemm_smallm_max": "0", "gemm_no_dma": "1"}, 2, 90, 256, 100, "int8"),
     "packed": ({"gemm_smallm_max": "0"}, 2, 90, 256, 102, "packed"),
     "packed_kernel": ({}, 2, 90, 256, 102, "packed_kernel"),
+    "fp6_256x256": ({"fp6_tile": "256x256"}, 2, 150, 384, 270, "fp6"),
+    "fp6_256x224": ({"fp6_tile": "256x224"}, 3, 101, 256, 460, "fp6"),
+    "fp6_128x256": ({"fp6_tile": "128x256"}, 2, 130, 640, 202, "fp6"),
 }
 _ENV_KEYS = ("w4a4_smallm_cfg", "gemm_smallm_max", "gemm_tile", "gemm_sk",
-             "gemm_sk_min", "gemm_no_dma")
+             "gemm_sk_min", "gemm_no_dma", "fp6_tile")
 
 
 def _set_env(tuning, env):
@@ -98,6 +101,11 @@ def _call(api, orc, dev, fmt, a, w, xs, ws, b, dtype, residual, gate, inplace=Fa
     if fmt == "packed":
         qact = torch.from_numpy(orc.pack_signed_int4(a)).to(dev)
         return api.hip_w4a4_matmul(qact, wq, *args, **kw)
+    if fmt == "fp6":  # FP6 operands (the same epilogue)
+        a6 = torch.from_numpy(orc.codes_to_fp6(a)).to(dev)
+        w6 = torch.from_numpy(orc.codes_to_fp6(w)).to(dev)
+        kw.pop("out_features")
+        return api.hip_w4a4_fp6_matmul(a6, w6, *args, rows=a.shape[0], out_features=N, in_features=a.shape[1], **kw)
     if fmt == "packed_kernel":  # the C ABI's register-staged kernel on the packed codes
         from convrot_mlx_amd import _native as nat
 
@@ -151,7 +159,7 @@ def test_every_kernel_path(orc, dev, tuning, path, dtype):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
 @pytest.mark.parametrize("form", ["chunk", "odd_stride", "vector", "full", "none"])
-@pytest.mark.parametrize("path", ["smallm_A", "dma_128x128", "register", "dma_288x192"])
+@pytest.mark.parametrize("path", ["smallm_A", "dma_128x128", "register", "dma_288x192", "fp6_256x224"])
 def test_gate_forms(orc, dev, tuning, path, form, dtype):
     api = _api()
     env, B, L, K, N, fmt = PATHS[path]
