@@ -238,7 +238,7 @@ __device__ __forceinline__ float acc_value(float v) {
   return v;
 }
 
-template <int ODT, int TM, int TN, int SHIFT, bool LDS_OPS = false, class V = i32x4>
+template <int ODT, int TM, int TN, int SHIFT, bool LDS_OPS = false, class V = i32x4, bool PIPE = false>
 __device__ __forceinline__ void epilogue(const V (&acc)[TN / 16][TM / 16], uint8_t* region, int lane,
                                          int mw, int nw, int M, int N, const float* __restrict__ xscales,
                                          const float* __restrict__ wscales, const float* __restrict__ bias,
@@ -367,6 +367,34 @@ __device__ __forceinline__ void epilogue(const V (&acc)[TN / 16][TM / 16], uint8
 #pragma unroll
       for (int it = 0; it < NIT; ++it)
         if (live(it)) store_row(it, staged(it));
+    } else if constexpr (PIPE) {
+      // Software-pipelined (kernels with registers to spare after the k-loop):
+      // batch b+1's residual and gate loads go out before batch b is applied
+      // and stored, so one memory round trip is exposed instead of one per
+      // batch.  Batches cover disjoint chunks, so an in-place residual is
+      // still read before it is overwritten.
+      constexpr int B = NIT < 8 ? NIT : 8, NB = (NIT + B - 1) / B;
+      Gated8 ops[2][B];
+      auto load_batch = [&](int bi, Gated8(&dst)[B]) {
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          const int it = bi * B + i;
+          if (it < NIT && live(it)) {
+            const int n = col_of(it);
+            gate_load8<ODT>(gr, mw + row_of(it), n, N, (N & 7) == 0 && n + 8 <= N, dst[i]);
+          }
+        }
+      };
+      load_batch(0, ops[0]);
+#pragma unroll
+      for (int bi = 0; bi < NB; ++bi) {
+        if (bi + 1 < NB) load_batch(bi + 1, ops[(bi + 1) & 1]);
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          const int it = bi * B + i;
+          if (it < NIT && live(it)) store_row(it, gate_apply8<ODT>(ops[bi & 1][i], staged(it)));
+        }
+      }
     } else {
       // Residual and gate loads of BATCH rows go out before their stores (a
       // load cannot be moved above a store that may alias it, so one row at a
@@ -1101,8 +1129,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int b = 0; b < E::FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
   e.run(0, kblocks, acc);
   __syncthreads();  // all waves done with the LDS ring before it is reused for output staging
-  epilogue<ODT, E::TM, E::TN, E::SHIFT, true>(acc, e.staging(), e.lane, m0 + e.wm * E::TM, n0 + e.wn * E::TN, M,
-                                              N, e.epi_xs(), e.epi_ws(), e.epi_bias(), out, gr, m0, n0);
+  epilogue<ODT, E::TM, E::TN, E::SHIFT, true, i32x4, true>(acc, e.staging(), e.lane, m0 + e.wm * E::TM,
+                                                           n0 + e.wn * E::TN, M, N, e.epi_xs(), e.epi_ws(),
+                                                           e.epi_bias(), out, gr, m0, n0);
 }
 
 // One pass of the 16-bit epilogue of the persistent 4-wave kernel: fragment
@@ -1578,7 +1607,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   e.prologue(kblocks);
   e.run(kblocks, acc);
   __syncthreads();  // ring -> output staging
-  epilogue<ODT, E::TM, E::TN, 0, true>(acc, smem + e.wave * E::STAGING, e.lane, m0 + e.wm * E::TM,
+  epilogue<ODT, E::TM, E::TN, 0, true, f32x4, true>(acc, smem + e.wave * E::STAGING, e.lane, m0 + e.wm * E::TM,
                                        n0 + e.wn * E::TN, M, N, (const float*)(smem + E::EPI_OFF),
                                        (const float*)(smem + E::WS_OFF), (const float*)(smem + E::BIAS_OFF), out, gr,
                                        m0, n0);
