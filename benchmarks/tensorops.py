@@ -11,6 +11,8 @@ Kernel names map as follows (reference -> here):
   mppW4A4 (int8 A4 codes)               -> hipW4A4      (convrot_w4a4_gemm, int8 activations)
   legacyPackedMetalM32N32K64 (packed A4) -> hipW4A4Packed (convrot_w4a4_gemm, packed activations)
   mppW4A16                              -> hipW4A16     (convrot_w4a16_gemm)
+  (none)                                -> hipW4A4Fp6   (convrot_w4a4_gemm_fp6: the A4 / W4 codes as FP6
+                                           operands, same outputs; K % 128 == 0 shapes only)
 The correctness gate checks the kernels against a float64 CPU evaluation of the eager
 contract written here in torch (exact integer dot, then the float32 epilogue in the
 reference's order), at the reference's gate sizes (37 x 256 -> 46).
@@ -112,9 +114,18 @@ def correctness_gate(gen: torch.Generator, dev) -> dict[str, object]:
     expected_a16 = ((activation.cpu().double() @ w_codes.double().T) * ws.cpu().double()[None, :]
                     + bias.cpu().double()[None, :])
     actual_a16 = api.hip_w4a16_matmul(activation, qweight, ws, bias, output_dtype=torch.float32, out_features=n)
+    # FP6 operands: the same codes (the activation rows converted like weight columns)
+    a6 = api.fp6_weight(api.repack_nk_weight_for_cdna4(qact), m, k)
+    w6 = api.fp6_weight(qweight, n, k)
+    actual_int6 = api.hip_w4a4_fp6_matmul(a6, w6, ones_m, ones_n, zero_n, output_dtype=torch.float32, rows=m,
+                                          out_features=n, in_features=k)
+    actual_a6 = api.hip_w4a4_fp6_matmul(a6, w6, xs, ws, bias, output_dtype=torch.float32, rows=m, out_features=n,
+                                        in_features=k)
     torch.cuda.synchronize()
 
     integer_exact = bool(torch.equal(actual_int.cpu(), dots.to(torch.float32)))
+    fp6_exact = bool(torch.equal(actual_int6.cpu(), dots.to(torch.float32))) and bool(
+        torch.equal(actual_a6.cpu(), actual_a4.cpu()))
     a4_max = float((actual_a4.cpu() - expected_a4).abs().max())
     a16_max = float((actual_a16.cpu().double() - expected_a16).abs().max())
     # float32 accumulation bound for the W4A16 dot: K * 2^-24 * sum|a*w| * ws, plus one output ulp
@@ -122,12 +133,15 @@ def correctness_gate(gen: torch.Generator, dev) -> dict[str, object]:
     a16_tol = float((k * 2.0**-24 * mag * ws.cpu().double()[None, :]).max() + 2.0**-23 * expected_a16.abs().max())
     if not integer_exact:
         raise RuntimeError("W4A4 failed the exact integer-dot gate")
+    if not fp6_exact:
+        raise RuntimeError("W4A4 on FP6 operands failed the exact integer-dot / same-output gate")
     if a4_max > 1e-5:
         raise RuntimeError(f"W4A4 failed the FP32 epilogue gate: maximum error {a4_max}")
     if a16_max > a16_tol:
         raise RuntimeError(f"W4A16 failed the FP32 gate: maximum error {a16_max} > {a16_tol}")
     return {
         "hipW4A4ExactIntegerDot": integer_exact,
+        "hipW4A4Fp6ExactIntegerDotAndSameOutput": fp6_exact,
         "hipW4A4Float32EpilogueMaximumAbsoluteError": a4_max,
         "hipW4A4Float32EpilogueTolerance": 1e-5,
         "hipW4A16MaximumAbsoluteError": a16_max,
@@ -147,6 +161,10 @@ def benchmark_shape(m: int, k: int, n: int, *, iterations: int, gen: torch.Gener
     qact, xscales = api.hip_fused_prepare_convrot_activation(activation, GROUP)
     qact_i8, xscales_i8 = api.hip_fused_prepare_convrot_activation_i8(activation, GROUP)
     rotated = api.hip_fused_rotate_convrot_activation(activation, GROUP)
+    fp6 = k % 128 == 0  # FP6 operands: the same codes as e2m3 values v/8 (this build's own path)
+    if fp6:
+        qact6, xscales6 = api.hip_fused_prepare_convrot_activation_fp6(activation, GROUP)
+        w6 = api.fp6_weight(qweight, n, k)
     torch.cuda.synchronize()
     bf16 = torch.bfloat16
 
@@ -181,7 +199,23 @@ def benchmark_shape(m: int, k: int, n: int, *, iterations: int, gen: torch.Gener
     packed_path_result = timed(packed_path, iterations=iterations)
     a4_path_result = timed(a4_path, iterations=iterations)
     a16_path_result = timed(a16_path, iterations=iterations)
-    for result in (packed_kernel, a4_kernel, a16_kernel, packed_path_result, a4_path_result, a16_path_result):
+    extra = []
+    if fp6:
+        fp6_kernel = timed(lambda: api.hip_w4a4_fp6_matmul(qact6, w6, xscales6, wscales, bias, output_dtype=bf16,
+                                                           rows=m, out_features=n, in_features=k),
+                           iterations=iterations)
+        fp6_preparation = timed(lambda: api.hip_fused_prepare_convrot_activation_fp6(activation, GROUP),
+                                iterations=iterations)
+
+        def fp6_path():
+            prepared, scales = api.hip_fused_prepare_convrot_activation_fp6(activation, GROUP)
+            return api.hip_w4a4_fp6_matmul(prepared, w6, scales, wscales, bias, output_dtype=bf16, rows=m,
+                                           out_features=n, in_features=k)
+
+        fp6_path_result = timed(fp6_path, iterations=iterations)
+        extra = [fp6_kernel, fp6_path_result]
+    for result in (packed_kernel, a4_kernel, a16_kernel, packed_path_result, a4_path_result, a16_path_result,
+                   *extra):
         result["speedupVsDenseBf16"] = round(dense["medianSeconds"] / result["medianSeconds"], 3)
     a4_kernel["speedupVsPackedKernel"] = round(packed_kernel["medianSeconds"] / a4_kernel["medianSeconds"], 3)
     a16_kernel["speedupVsPackedKernel"] = round(packed_kernel["medianSeconds"] / a16_kernel["medianSeconds"], 3)
@@ -189,7 +223,7 @@ def benchmark_shape(m: int, k: int, n: int, *, iterations: int, gen: torch.Gener
         packed_path_result["medianSeconds"] / a4_path_result["medianSeconds"], 3)
     a16_path_result["speedupVsPackedPath"] = round(
         packed_path_result["medianSeconds"] / a16_path_result["medianSeconds"], 3)
-    return {
+    receipt = {
         "shape": {"m": m, "k": k, "n": n},
         "denseBf16": dense,
         "activationPreparation": {
@@ -202,6 +236,14 @@ def benchmark_shape(m: int, k: int, n: int, *, iterations: int, gen: torch.Gener
         "completeLinearPath": {"hipW4A4Packed": packed_path_result, "hipW4A4": a4_path_result,
                                "hipW4A16": a16_path_result},
     }
+    if fp6:
+        fp6_kernel["speedupVsInt8Kernel"] = round(a4_kernel["medianSeconds"] / fp6_kernel["medianSeconds"], 3)
+        fp6_path_result["speedupVsInt8Path"] = round(
+            a4_path_result["medianSeconds"] / fp6_path_result["medianSeconds"], 3)
+        receipt["activationPreparation"]["fusedHadamardAndA4Fp6"] = fp6_preparation
+        receipt["kernelOnly"]["hipW4A4Fp6"] = fp6_kernel
+        receipt["completeLinearPath"]["hipW4A4Fp6"] = fp6_path_result
+    return receipt
 
 
 def parse_shape(value: str) -> tuple[int, int, int]:

@@ -18,13 +18,15 @@ def test_receipt(dev, tmp_path):
     assert json.loads(out.read_text()) == receipt
     gate = receipt["correctness"]
     assert gate["hipW4A4ExactIntegerDot"] is True
+    assert gate["hipW4A4Fp6ExactIntegerDotAndSameOutput"] is True
     assert gate["hipW4A4Float32EpilogueMaximumAbsoluteError"] <= 1e-5
     assert gate["hipW4A16MaximumAbsoluteError"] <= gate["hipW4A16Tolerance"]
     (bench,) = receipt["benchmarks"]
     assert bench["shape"] == {"m": 256, "k": 512, "n": 258}
     sections = [bench["denseBf16"], *bench["activationPreparation"].values(), *bench["kernelOnly"].values(),
                 *bench["completeLinearPath"].values()]
-    assert len(sections) == 11
+    assert len(sections) == 14  # the reference's 11, plus FP6 preparation, kernel and complete path
+    assert {"hipW4A4Fp6"} <= set(bench["kernelOnly"]) and {"hipW4A4Fp6"} <= set(bench["completeLinearPath"])
     for s in sections:
         assert len(s["seconds"]) == 2 and 0 < s["bestSeconds"] <= s["medianSeconds"]
         assert s["totalPeakGiB"] > 0
