@@ -45,6 +45,39 @@ __device__ __forceinline__ i32x4 expand8(uint32_t w) {
   return r;
 }
 
+// Activation fragments of one 128-feature block.  Load c gives lane
+// L = 16 u1 + 4 u0 + j the 8 features 32 u1 + 8 j .. +7 of token row
+// 4 u0 + c, so the 16 lanes of each 4-lane quad group read a row's 256
+// contiguous bytes (the MFMA layout, lane 16q + r holding row r, would put a
+// row's 64 bytes in lanes 16 apart, one cache access per lane).  The MFMA
+// wants lane 16q + r to hold features 32q + 8s .. +7 of row r in a[s]: with
+// q = u1 and r = 4 u0 + c that is the 4 x 4 transpose of (lane bits 0-1,
+// slot) inside every quad -- two rounds of exchanges with the lane 2 and
+// then 1 apart (DPP quad permutes).
+__device__ __forceinline__ void transpose_quads4(i32x4 (&a)[4], int lane) {
+  const bool b1 = (lane & 2) != 0, b0 = (lane & 1) != 0;
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int x = a[s][e], y = a[s + 2][e];
+      const int xs = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);  // quad_perm [2,3,0,1]: lane ^ 2
+      const int ys = __builtin_amdgcn_mov_dpp(y, 0x4E, 0xF, 0xF, true);
+      a[s][e] = b1 ? ys : x;
+      a[s + 2][e] = b1 ? y : xs;
+    }
+#pragma unroll
+  for (int s = 0; s < 4; s += 2)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int x = a[s][e], y = a[s + 1][e];
+      const int xs = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]: lane ^ 1
+      const int ys = __builtin_amdgcn_mov_dpp(y, 0xB1, 0xF, 0xF, true);
+      a[s][e] = b0 ? ys : x;
+      a[s + 1][e] = b0 ? y : xs;
+    }
+}
+
 template <int ADT>
 __device__ __forceinline__ f32x4 mfma16(i32x4 a, i32x4 b, f32x4 c) {
   if constexpr (ADT == kBF16)
@@ -57,7 +90,7 @@ __device__ __forceinline__ f32x4 mfma16(i32x4 a, i32x4 b, f32x4 c) {
 
 // Single token tile: four waves per SIMD (at most 128 VGPRs), so that the
 // whole grid's weight loads can be in flight at once.
-template <int ADT, int ODT, int FM, int NB, int SPLIT, int KPW>
+template <int ADT, int ODT, int FM, int NB, int SPLIT, int KPW, bool QL>
 __global__ __launch_bounds__(SPLIT * 64) __attribute__((amdgpu_waves_per_eu(FM == 1 ? 4 : 1)))
 void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
                                                                 const uint8_t* __restrict__ wq,
@@ -90,7 +123,7 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
       (void*)(wq + (int64_t)nb0 * 1024), (short)0, (int)(((int64_t)kblocks * nblocks - nb0) * 1024), 0x00020000);
   for (int kb0 = wave * KPW; kb0 < kblocks; kb0 += SPLIT * KPW) {
     uint4 w[KPW][NB];
-    i32x4 aop[KPW][FM][4];  // lane (m = r, q) -> 8 values at features kb*128 + 32q + 8c
+    i32x4 aop[KPW][FM][4];  // lane (q, r) -> 8 values at features kb*128 + 32q + 8c of row r (after QL's transpose)
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
       const int kb = kb0 + i;  // blocks at or past kblocks read zeros
@@ -104,15 +137,22 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
       for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const int k = kb * 128 + 32 * q + 8 * c;
+          // QL: quad-coalesced order (transposed before use); else the MFMA
+          // order, lane (q, r) reading row r, features 32q + 8c (a token
+          // row's 64 bytes spread over lanes 16 apart)
+          const int k = QL ? kb * 128 + 32 * q + 8 * (lane & 3) : kb * 128 + 32 * q + 8 * c;
+          const int row = QL ? fm * 16 + 4 * ((lane >> 2) & 3) + c : fm * 16 + r;
           const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-              ra, (int)((uint32_t)(fm * 16 + r) * (uint32_t)K * 2u + (uint32_t)k * 2u), 0, 0);
+              ra, (int)((uint32_t)row * (uint32_t)K * 2u + (uint32_t)k * 2u), 0, 0);
           // a ragged K end would read the next row: zero it (K is a multiple of 8)
           aop[i][fm][c] = k < K ? (i32x4){(int)v.x, (int)v.y, (int)v.z, (int)v.w} : (i32x4){0, 0, 0, 0};
         }
     }
 #pragma unroll
-    for (int i = 0; i < KPW; ++i)
+    for (int i = 0; i < KPW; ++i) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+        if constexpr (QL) transpose_quads4(aop[i][fm], lane);
 #pragma unroll
       for (int t = 0; t < NB; ++t) {
         const uint32_t wd[4] = {w[i][t].x, w[i][t].y, w[i][t].z, w[i][t].w};
@@ -123,6 +163,7 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
           for (int fm = 0; fm < FM; ++fm) acc[t][fm] = mfma16<ADT>(bop, aop[i][fm][c], acc[t][fm]);
         }
       }
+    }
   }
 
   if constexpr (SPLIT > 1) {
@@ -475,12 +516,12 @@ hipError_t launch_tiled(const void* act, const uint8_t* wq, const float* ws, con
   }
 }
 
-template <int ADT, int ODT, int FM, int NB, int SPLIT, int KPW>
+template <int ADT, int ODT, int FM, int NB, int SPLIT, int KPW, bool QL>
 hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M, int64_t N,
                     int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
   dim3 grid((unsigned)((nblocks + NB - 1) / NB), (unsigned)((M + 16 * FM - 1) / (16 * FM)));
-  hipLaunchKernelGGL((w4a16_gemm_kernel<ADT, ODT, FM, NB, SPLIT, KPW>), grid, dim3(64 * SPLIT), 0, stream,
+  hipLaunchKernelGGL((w4a16_gemm_kernel<ADT, ODT, FM, NB, SPLIT, KPW, QL>), grid, dim3(64 * SPLIT), 0, stream,
                      (const uint16_t*)act, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, gr);
   return hipGetLastError();
 }
@@ -502,6 +543,14 @@ hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const f
 // (~2 VALU ops per code) and the launch/tail.  The w4a16_cfg tuning override
 // (A|B|C|F|T) forces the kernel (sweeps and tests).
 constexpr int64_t kTiledMinM = 64;
+// From kQuadMinM rows on, splits A and B load activations in the quad-coalesced
+// order and transpose them in registers (transpose_quads4): at M = 16 on the
+// config-4 shapes 9.3 against 12.0 us (3072->12288) and 11.2 against 16.8 us
+// (12288->3072), at M = 32 12.1 against 15.5 and 15.8 against 19.0.  With a
+// few rows, the 64 transpose ops per block cost more than the scattered loads
+// save (M = 1: 8.8 against 8.0 us; M = 6: 8.6 against 8.3; M = 8: 8.7 against
+// 9.1).
+constexpr int64_t kQuadMinM = 8;
 template <int ADT, int ODT>
 hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
                         int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
@@ -517,10 +566,14 @@ hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, con
   if (const int v = tuning(kTuneW4a16Cfg); v == 'A' || v == 'B' || v == 'C' || v == 'F' || v == 'T') cfg = (char)v;
   switch (cfg) {
     case 'T': return launch_tiled<ADT, ODT>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    case 'C': return launch_t<ADT, ODT, 2, 2, 8, 2>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    case 'A': return launch_t<ADT, ODT, 1, 2, 8, 3>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    case 'B': return launch_t<ADT, ODT, 1, 1, 16, 4>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    default: return launch_t<ADT, ODT, 4, 2, 4, 2>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'C': return launch_t<ADT, ODT, 2, 2, 8, 2, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'A':
+      return M >= kQuadMinM ? launch_t<ADT, ODT, 1, 2, 8, 3, true>(act, wq, ws, bias, M, N, K, out, gr, stream)
+                            : launch_t<ADT, ODT, 1, 2, 8, 3, false>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'B':
+      return M >= kQuadMinM ? launch_t<ADT, ODT, 1, 1, 16, 4, true>(act, wq, ws, bias, M, N, K, out, gr, stream)
+                            : launch_t<ADT, ODT, 1, 1, 16, 4, false>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    default: return launch_t<ADT, ODT, 4, 2, 4, 2, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
   }
 }
 

@@ -109,6 +109,33 @@ def test_w4a16_every_split(orc, dev, tuning, cfg, M, K, N):
     _w4a16_check(orc, dev, act, "bfloat16", w, ws, b, "bfloat16")
 
 
+@pytest.mark.parametrize("cfg", ["A", "B"])
+@pytest.mark.parametrize("act_dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("K,N", [(3072, 12288), (2720, 530), (12288, 3072)])
+def test_w4a16_load_orders_agree(orc, dev, tuning, cfg, act_dtype, K, N):
+    """Splits A and B load activations in two orders: from 8 rows on, quad-coalesced reads that
+    are transposed in registers; below that, each lane reads its MFMA fragment directly.  Both
+    feed the same MFMAs in the same order, so rows 0..5 of a 40-row launch (quad order, two
+    token tiles) equal a 6-row launch (direct order) bit for bit; on the ragged shape the 40-row
+    launch is also checked against the oracle (the config-4 shapes are, at M = 8 and 32, by
+    test_w4a16_config4)."""
+    api = _api()
+    tuning.set("w4a16_cfg", cfg)
+    rng = np.random.default_rng(K * 3 + N)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.01, size=(N,)).astype(np.float32)
+    b = rng.normal(0, 0.02, size=(N,)).astype(np.float32)
+    act = normal_input(K + N + 1, (40, K), act_dtype, orc)
+    wq = _u8(orc.codes_to_cdna4(w), dev)
+    wsd, bd = torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev)
+    xd = to_dev(act, act_dtype, dev)
+    many = api.hip_w4a16_matmul(xd, wq, wsd, bd, output_dtype=torch.float32, out_features=N)
+    few = api.hip_w4a16_matmul(xd[:6].contiguous(), wq, wsd, bd, output_dtype=torch.float32, out_features=N)
+    assert torch.equal(many[:6].view(torch.int32), few.view(torch.int32))
+    if N < 1000:
+        _w4a16_check(orc, dev, act, act_dtype, w, ws, b)
+
+
 def _w4a16_tiled_case(orc, dev, act_dtype, out_dtype, M, K, N):
     rng = np.random.default_rng(M * 17 + K * 3 + N)
     w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
