@@ -214,6 +214,30 @@ def test_fp6_gemm_largest_sums(orc, dev):
     _assert_exact(from_dev(out), orc.w4a4_matmul_codes_large(a, w, xs, ws, b, "bfloat16"), "largest sums")
 
 
+def test_fp6_gemm_near_the_k_limit(orc, dev):
+    """K = 262016, the largest multiple of 128 the FP6 entry accepts (K < 262144): rows of 7 x 7,
+    7 x -8 and -7 x 7 codes reach |sums| of 14.7 M, within 2^24, so the float32 accumulators
+    are still exact.  float32 output with unit scales and no bias compares the accumulators
+    themselves with the oracle's int64 dots."""
+    nat = _nat()
+    M, K, N = 32, 262016, 48
+    rng = np.random.default_rng(262016)
+    a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    a[:4] = 7
+    a[4:8] = -7
+    w[:4] = 7
+    w[4:8] = -8
+    xs = np.ones(M, np.float32)
+    ws = np.ones(N, np.float32)
+    b = np.zeros(N, np.float32)
+    out = _gemm_fp6(nat, _u8(orc.codes_to_fp6(a), dev), _u8(xs, dev), _u8(orc.codes_to_fp6(w), dev), _u8(ws, dev),
+                    _u8(b, dev), M, N, K, torch.float32, dev)
+    want = orc.w4a4_matmul_codes_large(a, w, xs, ws, b, "float32")
+    assert np.abs(want[:8, :8]).max() == 8 * 7 * K
+    _assert_exact(from_dev(out), want, "K = 262016")
+
+
 @pytest.mark.parametrize("M,G,K,N", [(1536, 256, 3072, 9216), (4608, 256, 12288, 3072), (1000, 64, 3072, 1000)])
 def test_fp6_complete_path_equals_int8_path(orc, dev, M, G, K, N):
     """prep(FP6) -> FP6 GEMM on the FP6 conversion of a quantized weight gives the INT8 path's
