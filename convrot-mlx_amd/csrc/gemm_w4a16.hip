@@ -52,30 +52,27 @@ __device__ __forceinline__ i32x4 expand8(uint32_t w) {
 // row's 64 bytes in lanes 16 apart, one cache access per lane).  The MFMA
 // wants lane 16q + r to hold features 32q + 8s .. +7 of row r in a[s]: with
 // q = u1 and r = 4 u0 + c that is the 4 x 4 transpose of (lane bits 0-1,
-// slot) inside every quad -- two rounds of exchanges with the lane 2 and
-// then 1 apart (DPP quad permutes).
-__device__ __forceinline__ void transpose_quads4(i32x4 (&a)[4], int lane) {
-  const bool b1 = (lane & 2) != 0, b0 = (lane & 1) != 0;
+// slot) inside every quad.  It goes through the wave's own 4160-byte LDS
+// buffer: load c's registers at byte c * 1040 + 16 L (contiguous writes), and
+// lane 16q + r reads slot s from (r & 3) * 1040 + 16 (16q + 4 (r >> 2) + s).
+// The 1040-byte stride puts the 16 rows a read instruction's 16-lane group
+// touches in 16 different 16-byte bank groups.
+constexpr int kXposeStride = 1040, kXposeBytes = 4 * kXposeStride;
+
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ void transpose_quads4(i32x4 (&a)[4], uint8_t* buf, int lane) {
+  const int q = lane >> 4, r = lane & 15;
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
+  for (int c = 0; c < 4; ++c) *(i32x4*)(buf + c * kXposeStride + lane * 16) = a[c];
+  wave_lds_fence();
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int x = a[s][e], y = a[s + 2][e];
-      const int xs = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);  // quad_perm [2,3,0,1]: lane ^ 2
-      const int ys = __builtin_amdgcn_mov_dpp(y, 0x4E, 0xF, 0xF, true);
-      a[s][e] = b1 ? ys : x;
-      a[s + 2][e] = b1 ? y : xs;
-    }
-#pragma unroll
-  for (int s = 0; s < 4; s += 2)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int x = a[s][e], y = a[s + 1][e];
-      const int xs = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]: lane ^ 1
-      const int ys = __builtin_amdgcn_mov_dpp(y, 0xB1, 0xF, 0xF, true);
-      a[s][e] = b0 ? ys : x;
-      a[s + 1][e] = b0 ? y : xs;
-    }
+  for (int s = 0; s < 4; ++s) a[s] = *(const i32x4*)(buf + (r & 3) * kXposeStride + (16 * q + 4 * (r >> 2) + s) * 16);
+  wave_lds_fence();  // the buffer's next writes come after these reads
 }
 
 template <int ADT>
@@ -99,6 +96,7 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
                                                                 void* __restrict__ out, int M, int N, int K,
                                                                 int nblocks, int kblocks, GatedResidual gr) {
   __shared__ __attribute__((aligned(16))) f32x4 red[SPLIT > 1 ? SPLIT : 1][NB * FM][64];
+  __shared__ __attribute__((aligned(16))) uint8_t xpose[QL ? SPLIT * kXposeBytes : 16];  // per-wave buffers
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nb0 = blockIdx.x * NB;
   const int m0 = blockIdx.y * 16 * FM;
@@ -152,7 +150,7 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
     for (int i = 0; i < KPW; ++i) {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
-        if constexpr (QL) transpose_quads4(aop[i][fm], lane);
+        if constexpr (QL) transpose_quads4(aop[i][fm], xpose + wave * kXposeBytes, lane);
 #pragma unroll
       for (int t = 0; t < NB; ++t) {
         const uint32_t wd[4] = {w[i][t].x, w[i][t].y, w[i][t].z, w[i][t].w};
@@ -544,13 +542,16 @@ hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const f
 // (A|B|C|F|T) forces the kernel (sweeps and tests).
 constexpr int64_t kTiledMinM = 64;
 // From kQuadMinM rows on, splits A and B load activations in the quad-coalesced
-// order and transpose them in registers (transpose_quads4): at M = 16 on the
+// order and transpose them through LDS (transpose_quads4): at M = 16 on the
 // config-4 shapes 9.3 against 12.0 us (3072->12288) and 11.2 against 16.8 us
 // (12288->3072), at M = 32 12.1 against 15.5 and 15.8 against 19.0.  With a
-// few rows, the 64 transpose ops per block cost more than the scattered loads
-// save (M = 1: 8.8 against 8.0 us; M = 6: 8.6 against 8.3; M = 8: 8.7 against
-// 9.1).
-constexpr int64_t kQuadMinM = 8;
+// few rows the transposes cost more than the scattered loads save: M = 4 runs
+// 7.9 against 8.2 us direct (3072->12288) and 8.9 against 9.3 (12288->3072),
+// M = 6 8.3 against 8.3 and 9.6 against 9.2.  (The LDS transpose replaced a
+// register one of 64 VALU ops per block, which lost up to M = 6; it took M = 32
+// from 12.4 to 12.0 us (3072->12288) and 15.8 to 14.4 us (12288->3072),
+// bit-identical.)
+constexpr int64_t kQuadMinM = 6;
 template <int ADT, int ODT>
 hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
                         int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
