@@ -1583,7 +1583,7 @@ struct Fp6Engine {
 // The 4-wave FP6 GEMM, one BM x BN tile per workgroup, with the epilogue of
 // every W4A4 kernel (16-bit or float32 outputs, optional gated residual).
 template <int BM, int BN, int ODT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void w4a4_gemm_fp6_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, BM * BN <= 128 * 128 ? 2 : 1))) void w4a4_gemm_fp6_kernel(
     const uint8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
     int K, int nblocks, int tiles_m, int tiles_n, GatedResidual gr) {
@@ -2374,13 +2374,15 @@ namespace {
 // at the same K).  The plan takes the tile with the least modelled time,
 // rounds of whole tiles over the CUs times the tile's relative time: at 4608
 // tokens, 256 x 224 turns 216 tiles (N = 3072) into 252 and 864 (N = 12288)
-// into 990, both a near-whole number of rounds; 128 x 256 fills the CUs at a
-// few thousand tokens.
+// into 990, both a near-whole number of rounds; 128 x 256 fills the CUs at
+// 1024-1536 tokens; 128 x 128 (two workgroups per CU) at 256-1024 tokens with
+// N = 3072: 12288 -> 3072 at 512 tokens takes 28.5 us against 42.0 on
+// 128 x 256 (its relative time 0.43 measured at 256-1024 tokens).
 struct Fp6Tile {
   int bm, bn;
   double rel;
 };
-constexpr Fp6Tile kFp6Tiles[3] = {{256, 256, 1.0}, {256, 224, 0.9}, {128, 256, 0.62}};
+constexpr Fp6Tile kFp6Tiles[4] = {{256, 256, 1.0}, {256, 224, 0.9}, {128, 256, 0.62}, {128, 128, 0.43}};
 
 Fp6Tile fp6_tile(int64_t M, int64_t N) {
   const int forced = tuning(kTuneFp6Tile);
@@ -2419,6 +2421,8 @@ hipError_t launch_fp6_t(const uint8_t* act6, const float* xscales, const uint8_t
   const Fp6Tile t = fp6_tile(M, N);
   if (t.bm == 256 && t.bn == 224)
     return launch_fp6_tile<256, 224, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+  if (t.bm == 128 && t.bn == 128)
+    return launch_fp6_tile<128, 128, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
   if (t.bm == 128)
     return launch_fp6_tile<128, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
   return launch_fp6_tile<256, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
