@@ -2375,14 +2375,16 @@ namespace {
 // rounds of whole tiles over the CUs times the tile's relative time: at 4608
 // tokens, 256 x 224 turns 216 tiles (N = 3072) into 252 and 864 (N = 12288)
 // into 990, both a near-whole number of rounds; 128 x 256 fills the CUs at
-// 1024-1536 tokens; 128 x 128 (two workgroups per CU) at 256-1024 tokens with
-// N = 3072: 12288 -> 3072 at 512 tokens takes 28.5 us against 42.0 on
-// 128 x 256 (its relative time 0.43 measured at 256-1024 tokens).
+// a few thousand tokens; 128 x 128 (two workgroups per CU) at 256-1024 tokens
+// with N = 3072: 12288 -> 3072 at 512 tokens takes 28.5 us against 42.0 on
+// 128 x 256 (its relative time 0.43 measured at 256-1024 tokens); 128 x 192
+// (192 tiles: one round) at 1536 tokens, 12288 -> 3072 in 37.0 us against 45.1
+// (relative time 0.56 at 1536-2048 tokens).
 struct Fp6Tile {
   int bm, bn;
   double rel;
 };
-constexpr Fp6Tile kFp6Tiles[4] = {{256, 256, 1.0}, {256, 224, 0.9}, {128, 256, 0.62}, {128, 128, 0.43}};
+constexpr Fp6Tile kFp6Tiles[5] = {{256, 256, 1.0}, {256, 224, 0.9}, {128, 256, 0.62}, {128, 128, 0.43}, {128, 192, 0.56}};
 
 Fp6Tile fp6_tile(int64_t M, int64_t N) {
   const int forced = tuning(kTuneFp6Tile);
@@ -2423,6 +2425,8 @@ hipError_t launch_fp6_t(const uint8_t* act6, const float* xscales, const uint8_t
     return launch_fp6_tile<256, 224, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
   if (t.bm == 128 && t.bn == 128)
     return launch_fp6_tile<128, 128, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+  if (t.bm == 128 && t.bn == 192)
+    return launch_fp6_tile<128, 192, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
   if (t.bm == 128)
     return launch_fp6_tile<128, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
   return launch_fp6_tile<256, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);

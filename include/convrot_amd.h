@@ -341,7 +341,7 @@ const char* convrot_last_error(void);
  *                                         on a grid of that many workgroups
  *   gemm_mfma32      "0" | "1"            4-wave 256x256 W4A4 tile on 32x32x32 MFMAs: never,
  *                                         or always (plain 16-bit outputs)
- *   fp6_tile         "BMxBN"              FP6 W4A4 tile: 256x256, 256x224, 128x256 or 128x128
+ *   fp6_tile         "BMxBN"              FP6 W4A4 tile: 256x256, 256x224, 128x256, 128x192 or 128x128
  * Returns CONVROT_ERR_INVALID for an unknown name or a malformed value.
  */
 int convrot_set_tuning(const char* name, const char* value);

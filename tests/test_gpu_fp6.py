@@ -261,11 +261,11 @@ def test_fp6_complete_path_equals_int8_path(orc, dev, M, G, K, N):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x224", "128x256", "128x128"])
+@pytest.mark.parametrize("tile", ["256x256", "256x224", "128x256", "128x128", "128x192"])
 @pytest.mark.parametrize("M,K,N", [(300, 384, 1000), (37, 128, 48), (520, 1536, 264), (1000, 640, 232)])
 def test_fp6_every_tile(orc, dev, tuning, tile, M, K, N):
     """Each FP6 tile (forced through the fp6_tile tuning override) on ragged M / N tails --
-    partial 128-, 224- and 256-wide column tiles, partial 128- and 256-row tiles -- bit-exact
+    partial 128-, 192-, 224- and 256-wide column tiles, partial 128- and 256-row tiles -- bit-exact
     against the oracle, in bf16 and f16."""
     nat = _nat()
     tuning.set("fp6_tile", tile)

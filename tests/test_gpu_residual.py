@@ -46,6 +46,7 @@ PATHS = {
     "fp6_256x224": ({"fp6_tile": "256x224"}, 3, 101, 256, 460, "fp6"),
     "fp6_128x256": ({"fp6_tile": "128x256"}, 2, 130, 640, 202, "fp6"),
     "fp6_128x128": ({"fp6_tile": "128x128"}, 3, 101, 384, 330, "fp6"),
+    "fp6_128x192": ({"fp6_tile": "128x192"}, 2, 130, 512, 410, "fp6"),
 }
 _ENV_KEYS = ("w4a4_smallm_cfg", "gemm_smallm_max", "gemm_tile", "gemm_sk",
              "gemm_sk_min", "gemm_no_dma", "fp6_tile")
