@@ -31,7 +31,10 @@ Prints ONE JSON line (the driver's contract).  Extra keys:
   config2_m1536   configs[1] (M=1536, G=64, four double-block shapes), complete path
   flux_m4608_column_shard_8  4608x3072->1536, one GPU's share of an 8-way column split
   w4a16_config4   configs[3] (W4A16, M in {1, 8, 32}): int4-weight GB/s, HIP-graph replays
-  flux_dit_config5  configs[4]: one step of a random-init FLUX.1-dev DiT, dense vs W4A4
+  flux_dit_config5  configs[4]: one step of a random-init FLUX.1-dev DiT, dense vs W4A4, with the
+                  Linears' weight bytes and the step's peak device memory
+  video_transfer_shapes  the reference's published projection shapes (M = 7800 / 8800), complete
+                  path on MI355X beside its M4 Pro latencies (context, other hardware)
 """
 
 from __future__ import annotations
@@ -58,6 +61,11 @@ CONFIG3 = {"M": 4608, "G": 256,
            "shapes": [(3072, 9216), (3072, 3072), (3072, 12288), (12288, 3072), (3072, 21504), (15360, 3072)]}
 CONFIG2 = {"M": 1536, "G": 64, "shapes": [(3072, 9216), (3072, 3072), (3072, 12288), (12288, 3072)]}
 CONFIG4 = {"G": 256, "Ms": (1, 8, 32), "shapes": [(3072, 12288), (12288, 3072)]}
+# The reference's only published single-projection timings (docs/benchmarks/video-transfer.md:15-20):
+# (model, M, K, N, median complete-projection seconds of its MPP W4A4 path on an M4 Pro).
+VIDEO_SHAPES = [("Wan 2.2 A14B", 7800, 5120, 5120, 0.103394), ("Wan expansion", 7800, 5120, 13824, 0.290321),
+                ("Wan contraction", 7800, 13824, 5120, 0.352751), ("LTX 2.5", 8800, 4096, 4096, 0.075218),
+                ("LTX expansion", 8800, 4096, 16384, 0.297969), ("LTX contraction", 8800, 16384, 4096, 0.408371)]
 TRAFFIC_FILE = ROOT / "profiles" / "gemm_w4a4_fp6_flux_m4608_traffic.json"
 
 
@@ -320,6 +328,7 @@ def main() -> int:
         result["config2_m1536"] = config2_figure(torch, np, core, nat, dev, fp6)
         result["flux_m4608_column_shard_8"] = shard_figure(torch, np, core, nat, dev, fp6)
         result["w4a16_config4"] = w4a16_figure(torch, core, nat, dev)
+        result["video_transfer_shapes"] = video_figure(torch, np, core, nat, dev)
         if not args.no_config5:
             from examples.flux1_dev.dit import config5_figure
 
@@ -379,6 +388,34 @@ def config2_figure(torch, np, core, nat, dev, fp6):
             "gemm_tops": round(float(ops.sum() / (gemm_ms.sum() * 1e-3) / 1e12), 1),
             "gemm_per_shape_us": [round(t * 1e3, 2) for t in gemm_ms],
             "prep_per_shape_us": [round(t * 1e3, 2) for t in prep_ms]}
+
+
+def video_figure(torch, np, core, nat, dev):
+    """The complete W4A4 path (G=256, FP6 operands, as ConvRotLinear runs these sizes) and torch's
+    dense bf16 linear on the reference's published video-transformer projections; two buffer sets
+    cycled (each set is 0.2-0.8 GB).  The reference's figures are an M4 Pro's, listed as context."""
+    G = 256
+    rows = []
+    for name, M, K, N, ref_s in VIDEO_SHAPES:
+        sets = make_layers(torch, core, dev, M, G, [(K, N)], seed=M + K + N, sets=2, fp6=True)
+        runner = PathRunner(nat, dev, M, G, fp6=True)
+        ms, prep_ms, gemm_ms, _, _ = measure_path(torch, np, runner, sets, [(K, N)], M, 20, 3)
+        dense = dense_control(torch, sets[0], M, [(K, N)])
+        ops = 2.0 * M * K * N
+        rows.append({"shape": f"{name}: M={M} K={K} N={N}", "path_us": round(ms * 1e3, 2),
+                     "tops": round(ops / (ms * 1e-3) / 1e12, 1),
+                     "pct_int8_peak": round(100 * ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 2),
+                     "prep_us": round(float(prep_ms[0]) * 1e3, 2), "gemm_us": round(float(gemm_ms[0]) * 1e3, 2),
+                     "dense_bf16_us": round(dense["ms_per_step"] * 1e3, 2),
+                     "speedup_vs_dense_bf16": round(dense["ms_per_step"] / ms, 3),
+                     "reference_m4pro_mpp_w4a4_us": round(ref_s * 1e6, 1)})
+        del sets
+        torch.cuda.empty_cache()
+    return {"what": "complete W4A4 path (fused prep writing FP6 operands + FP6 GEMM + epilogue, G=256, bf16, "
+                    "with bias) vs torch bf16 F.linear on the reference's published projection shapes; the "
+                    "reference column is its M4 Pro MPP W4A4 median (docs/benchmarks/video-transfer.md:15-20), "
+                    "other hardware, context only",
+            "shapes": rows}
 
 
 def shard_figure(torch, np, core, nat, dev, fp6):

@@ -46,6 +46,7 @@ SIGNATURES = {
     "convrot_repack_weight": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _vp]),
     "convrot_cdna4_bytes": (_i64, [_i64, _i64]),
     "convrot_fp6_bytes": (_i64, [_i64, _i64]),
+    "convrot_w4a4_fp6_tile": (_i32, [_i64, _i64, _vp, _vp]),
     "convrot_weight_fp6": (_i32, [_vp, _vp, _i64, _i64, _vp]),
     "convrot_w4a4_gemm_fp6": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_w4a4_gemm_fp6_residual": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp,
@@ -141,3 +142,14 @@ def set_tuning(name: str, value: str | None) -> None:
 
 def cdna4_bytes(n: int, k: int) -> int:
     return int(load().convrot_cdna4_bytes(n, k))
+
+
+def fp6_bytes(rows: int, k: int) -> int:
+    return int(load().convrot_fp6_bytes(rows, k))
+
+
+def fp6_tile(m: int, n: int) -> tuple[int, int]:
+    """The (BM, BN) tile the FP6 W4A4 GEMM runs for an m x n product."""
+    bm, bn = ctypes.c_int(0), ctypes.c_int(0)
+    check(load().convrot_w4a4_fp6_tile(m, n, ctypes.byref(bm), ctypes.byref(bn)))
+    return bm.value, bn.value

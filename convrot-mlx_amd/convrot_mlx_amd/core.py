@@ -669,6 +669,9 @@ def hip_w4a4_int8_matmul(activations, qweight, xscales, wscales, bias, *, output
 # code instead of three quarters, are as fast or faster.
 FP6_MIN_ROWS = 256
 FP6_MAX_FEATURES = 262144  # exclusive: sums of K products of |v*w| <= 64 stay below 2^24
+# The FP6 GEMM addresses each operand with 32-bit buffer offsets (include/convrot_amd.h):
+# larger products run on INT8 operands instead.
+FP6_MAX_OPERAND_BYTES = (1 << 32) - (1 << 20)
 _fp6_operands = os.getenv("CONVROT_FP6_OPERANDS", "1") != "0"
 
 
@@ -684,10 +687,16 @@ def fp6_operands_enabled() -> bool:
     return _fp6_operands
 
 
+def fp6_bytes(rows: int, features: int) -> int:
+    """Bytes of the FP6 operand blocks of a [rows, features] operand (features % 128 == 0)."""
+    return math.prod(fp6_shape(rows, features))
+
+
 def fp6_eligible(m: int, n: int, k: int, output_dtype: torch.dtype) -> bool:
     """Whether a W4A4 product of this shape runs on FP6 operands in ConvRotLinear."""
     return (_fp6_operands and m >= FP6_MIN_ROWS and k % 128 == 0 and 0 < k < FP6_MAX_FEATURES
-            and output_dtype in (torch.bfloat16, torch.float16, torch.float32))
+            and output_dtype in (torch.bfloat16, torch.float16, torch.float32)
+            and max(fp6_bytes(m, k), fp6_bytes(n, k)) <= FP6_MAX_OPERAND_BYTES)
 
 
 def fp6_weight(qweight: torch.Tensor, out_features: int, in_features: int) -> torch.Tensor:

@@ -74,6 +74,10 @@ constexpr int64_t kMaxFeatures = 65536;
 // through buffer resources with 32-bit signed offsets: below 2 GiB.
 constexpr int64_t kMaxWeightBytes = int64_t(1) << 31;
 int64_t packed_weight_bytes(int64_t N, int64_t K) { return ((K + 127) / 128) * ((N + 15) / 16) * 1024; }
+// The FP6 GEMM reads each operand through one buffer resource: 32-bit offsets
+// (a k-block's offset plus a tile's pieces) must not wrap, so an operand stays
+// 1 MiB below 4 GiB.
+constexpr int64_t kMaxFp6OperandBytes = (int64_t(1) << 32) - (int64_t(1) << 20);
 
 }  // namespace
 
@@ -106,14 +110,16 @@ int convrot_set_tuning(const char* name, const char* value) {
         int bm = 0, bn = 0, wm = 2, wn = 2, st = 0;
         const int got = sscanf(value, "%dx%dw%dx%ds%d", &bm, &bn, &wm, &wn, &st);
         good = got >= 2 && bm > 0 && bm <= 512 && bn > 0 && bn <= 512 && wm > 0 && wm < 16 && wn > 0 && wn < 16 &&
-               st >= 0 && st < 8;
+               st >= 0 && st < 8 && w4a4_tile_known(bm, bn, wm, wn, st);
         v = bm | bn << 10 | wm << 20 | wn << 24 | st << 28;
         break;
       }
       case kTuneFp6Tile:
       case kTuneW4a16Tile: {
         int bm = 0, bn = 0;
-        good = sscanf(value, "%dx%d", &bm, &bn) == 2 && bm > 0 && bm <= 512 && bn > 0 && bn <= 512;
+        char tail = 0;
+        good = sscanf(value, "%dx%d%c", &bm, &bn, &tail) == 2 &&
+               (key == kTuneFp6Tile ? fp6_tile_known(bm, bn) : w4a16_tile_known(bm, bn));
         v = bm | bn << 10;
         break;
       }
@@ -148,6 +154,13 @@ int64_t convrot_cdna4_bytes(int64_t N, int64_t K) {
 int64_t convrot_fp6_bytes(int64_t R, int64_t K) {
   if (R < 0 || K < 0 || K % 128) return -1;
   return (K / 128) * ((R + 15) / 16) * 1536;
+}
+
+int convrot_w4a4_fp6_tile(int64_t M, int64_t N, int* bm, int* bn) {
+  if (M <= 0 || N <= 0 || !bm || !bn)
+    return fail(CONVROT_ERR_INVALID, "FP6 tile query needs M, N > 0 and two result pointers");
+  convrot::fp6_plan_tile(M, N, bm, bn);
+  return ok();
 }
 
 int convrot_prepare(const void* x, int dtype, int64_t rows, int64_t features, int group_size, int mode,
@@ -314,6 +327,11 @@ int check_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, cons
     return fail(CONVROT_ERR_INVALID,
                 "FP6 W4A4 GEMM: bad shape M=%lld N=%lld K=%lld (K a multiple of 128 below 262144)", (long long)M,
                 (long long)N, (long long)K);
+  if (convrot_fp6_bytes(M, K) > kMaxFp6OperandBytes || convrot_fp6_bytes(N, K) > kMaxFp6OperandBytes)
+    return fail(CONVROT_ERR_UNSUPPORTED,
+                "FP6 W4A4 GEMM: an operand of M=%lld or N=%lld rows at K=%lld exceeds %lld FP6 bytes (32-bit "
+                "buffer offsets); use the INT8 GEMM",
+                (long long)M, (long long)N, (long long)K, (long long)kMaxFp6OperandBytes);
   if (out_dtype != CONVROT_DTYPE_BF16 && out_dtype != CONVROT_DTYPE_F16 && out_dtype != CONVROT_DTYPE_F32)
     return fail(CONVROT_ERR_INVALID, "unsupported output dtype %d", out_dtype);
   *odt = out_dtype == CONVROT_DTYPE_BF16 ? convrot::kBF16 : out_dtype == CONVROT_DTYPE_F16 ? convrot::kF16
@@ -540,6 +558,9 @@ int convrot_repack_weight(const uint8_t* in, int in_layout, uint8_t* out, int ou
 
 int convrot_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, void* stream) {
   if (N < 0 || K < 0) return fail(CONVROT_ERR_INVALID, "invalid weight shape (%lld, %lld)", (long long)N, (long long)K);
+  if (K % 128)
+    return fail(CONVROT_ERR_UNSUPPORTED, "FP6 operands require in_features divisible by 128, got %lld",
+                (long long)K);
   if (N == 0 || K == 0) return ok();
   if (!cdna4 || !fp6) return fail(CONVROT_ERR_INVALID, "null pointer argument");
   if (!aligned(cdna4, 16) || !aligned(fp6, 16)) return fail(CONVROT_ERR_INVALID, "cdna4 and fp6 must be 16-byte aligned");

@@ -32,6 +32,16 @@ enum TuneKey : int {
 };
 int tuning(TuneKey key);
 
+// Whether a tile forced through convrot_set_tuning is one the library builds:
+// a W4A4 INT8 tile (DMA kernels with ring depth `stages`, 0 for any, or the
+// register-staged kernel), an FP6 W4A4 tile, a W4A16 tiled-kernel tile.
+bool w4a4_tile_known(int bm, int bn, int wm, int wn, int stages);
+bool fp6_tile_known(int bm, int bn);
+bool w4a16_tile_known(int bm, int bn);
+
+// The FP6 W4A4 tile the plan (and the fp6_tile override) picks for M x N.
+void fp6_plan_tile(int64_t M, int64_t N, int* bm, int* bn);
+
 bool prep_plan(int64_t rows, int64_t K, int* ni_out, int* waves_out);
 
 hipError_t launch_prep(const void* x, int dtype, int64_t rows, int64_t K, int log4g, int mode, void* out,

@@ -598,4 +598,10 @@ hipError_t launch_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qwei
   return launch_odt<kBF16>(out_dtype, act, qweight, wscales, bias, M, N, K, out, gr, stream);
 }
 
+bool w4a16_tile_known(int bm, int bn) {
+  for (const TiledCand& c : kTiledCands)
+    if (c.bm == bm && c.bn == bn) return true;
+  return false;
+}
+
 }  // namespace convrot

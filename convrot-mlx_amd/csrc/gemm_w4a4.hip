@@ -2306,6 +2306,18 @@ hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscale
   return launch_odt<false>(out_dtype, act, xscales, qweight, wscales, bias, M, N, K, out, gr, src, stream);
 }
 
+bool w4a4_tile_known(int bm, int bn, int wm, int wn, int stages) {
+  for (const Cand& c : kCands)
+    if (c.t.bm == bm && c.t.bn == bn && c.t.wm == wm && c.t.wn == wn && (stages == 0 || c.t.stages == stages))
+      return true;
+  // tiles of the register-staged kernel (no LDS ring, so no ring depth)
+  constexpr int kRegTiles[][4] = {{256, 256, 2, 4}, {256, 256, 4, 2}, {256, 256, 2, 2}, {256, 128, 2, 2},
+                                  {256, 128, 4, 2}, {128, 256, 2, 2}, {128, 256, 2, 4}, {128, 128, 2, 2}};
+  for (const auto& t : kRegTiles)
+    if (t[0] == bm && t[1] == bn && t[2] == wm && t[3] == wn && stages == 0) return true;
+  return false;
+}
+
 size_t w4a4_plan_workspace_bytes(int act_format, int64_t M, int64_t N, int64_t K) {
   if (M == 0 || N == 0 || act_format == CONVROT_ACT_PACKED || M <= smallm_limit(N, K)) return 0;
   const bool dma = tuning(kTuneGemmNoDma) != 1;
@@ -2433,6 +2445,18 @@ hipError_t launch_fp6_t(const uint8_t* act6, const float* xscales, const uint8_t
 }
 
 }  // namespace
+
+bool fp6_tile_known(int bm, int bn) {
+  for (const Fp6Tile& t : kFp6Tiles)
+    if (t.bm == bm && t.bn == bn) return true;
+  return false;
+}
+
+void fp6_plan_tile(int64_t M, int64_t N, int* bm, int* bn) {
+  const Fp6Tile t = fp6_tile(M, N);
+  *bm = t.bm;
+  *bn = t.bn;
+}
 
 hipError_t launch_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
                                 const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,

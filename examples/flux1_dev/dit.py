@@ -372,6 +372,41 @@ def time_step(model, inputs, steps: int) -> tuple[torch.Tensor, float, float]:
     return out, eager_ms, graph_ms
 
 
+def linear_weight_bytes(model: nn.Module) -> dict:
+    """Device bytes the model's Linears hold: dense weights and biases, or a ConvRotLinear's
+    qweight, scales and bias plus the derived forms it caches (the FP6 operand weight, and the
+    CDNA4 repack of a K x packed-N qweight), and the weight count they serve."""
+    from convrot_mlx_amd import ConvRotLinear
+
+    stored = derived = weights = 0
+    for m in model.modules():
+        if isinstance(m, ConvRotLinear):
+            weights += m.in_features * m.out_features
+            stored += sum(t.numel() * t.element_size() for t in (m.qweight, m.scales, m.bias))
+            for cache in (m._fp6_cache, m._cdna4_cache):
+                if cache is not None:
+                    derived += cache[1].numel() * cache[1].element_size()
+        elif isinstance(m, nn.Linear):
+            weights += m.weight.numel()
+            stored += sum(t.numel() * t.element_size() for t in (m.weight, m.bias) if t is not None)
+    return {"weights": weights, "stored_bytes": stored, "derived_bytes": derived,
+            "bytes_per_weight": round((stored + derived) / max(1, weights), 4)}
+
+
+def step_peak_memory(model: nn.Module, inputs: dict) -> dict:
+    """Device memory around one eager step (torch's allocator): resident before it and the peak
+    during it, in GiB."""
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
+    resident = torch.cuda.memory_allocated()
+    with torch.no_grad():
+        model(**inputs)
+    torch.cuda.synchronize()
+    gib = float(1 << 30)
+    return {"resident_GiB": round(resident / gib, 3), "step_peak_GiB": round(torch.cuda.max_memory_allocated() / gib, 3)}
+
+
 def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_tokens: int = 512,
                    group_size: int = 64, steps: int = 5) -> dict:
     """One denoising step, dense bf16 vs every eligible Linear as W4A4 ConvRotLinear."""
@@ -381,6 +416,8 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
     dev = torch.device("cuda:0")
     model = build(p, dev)
     inputs = make_inputs(p, img_tokens, txt_tokens, dev)
+    dense_weights = linear_weight_bytes(model)
+    dense_memory = step_peak_memory(model, inputs)
     dense, dense_ms, dense_graph_ms = time_step(model, inputs, steps)
     dense = dense.float()
     linears = sum(1 for m in model.modules() if isinstance(m, nn.Linear))
@@ -401,6 +438,8 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
     set_fused_residual(model, True)
     allf, all_ms, all_graph_ms = time_step(model, inputs, steps)
     allf = allf.float()
+    convrot_weights = linear_weight_bytes(model)
+    convrot_memory = step_peak_memory(model, inputs)
 
     def dev_stats(out):
         diff = out - dense
@@ -443,6 +482,18 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
             "graph_speedup_vs_dense": round(dense_graph_ms / all_graph_ms, 3),
             "rel_l2_vs_dense": arel, "cosine_vs_dense": acos,
             "identical_to_fused_modulation_and_gelu": bool(torch.equal(allf, both)),
+        },
+        "memory": {
+            "what": "torch allocator bytes on the device: the Linears' weights (dense bf16 weight + bias, or "
+                    "ConvRotLinear qweight + scales + bias as stored, plus the derived FP6 operand weights "
+                    "cached for products of 256+ rows), and the resident / peak bytes of one eager step of "
+                    "the whole model (dense, and W4A4 with every fusion on)",
+            "dense_linears": dense_weights, "w4a4_linears": convrot_weights,
+            "dense_step": dense_memory, "w4a4_step": convrot_memory,
+            "step_peak_reduction_pct": round(100.0 * (1.0 - convrot_memory["step_peak_GiB"] /
+                                                      dense_memory["step_peak_GiB"]), 1),
+            "reference": "M4 Pro, MLX allocator peak over a whole 20-step generation: 24.603 GiB dense vs "
+                         "9.296 GiB ConvRot, 62.2 % less (docs/benchmarks/m4-pro.md:23-31)",
         },
     }
 

@@ -292,8 +292,16 @@ int64_t convrot_cdna4_bytes(int64_t N, int64_t K);
 int64_t convrot_fp6_bytes(int64_t R, int64_t K);
 
 /*
+ * The BM x BN tile convrot_w4a4_gemm_fp6 runs for an M x N product (the
+ * automatic plan, or the fp6_tile tuning override): an introspection call for
+ * sweeps and tests, no counterpart in the reference.
+ */
+int convrot_w4a4_fp6_tile(int64_t M, int64_t N, int* bm, int* bn);
+
+/*
  * CDNA4-layout weight -> FP6 operand blocks (an offline conversion, like
  * convrot_repack_weight); every int4 code, -8 included, has an FP6 field.
+ * K % 128 == 0 (else CONVROT_ERR_UNSUPPORTED).
  */
 int convrot_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, void* stream);
 
@@ -301,8 +309,10 @@ int convrot_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K,
  * convrot_w4a4_gemm on FP6 operands: act6 from convrot_prepare(..., CONVROT_PREP_FP6,
  * ...), w6 from convrot_weight_fp6.  Same epilogue and outputs, bit for bit, as
  * convrot_w4a4_gemm with act_format CONVROT_ACT_INT8 (out_dtype f32, f16 or
- * bf16); K a multiple of 128 below 262144.  Replaces the same launch site
- * (core.py:1088-1120).
+ * bf16); K a multiple of 128 below 262144.  Each operand is addressed with
+ * 32-bit offsets: convrot_fp6_bytes(M, K) and convrot_fp6_bytes(N, K) must be
+ * at most 2^32 - 2^20, else CONVROT_ERR_UNSUPPORTED (the INT8 GEMM has no such
+ * limit).  Replaces the same launch site (core.py:1088-1120).
  */
 int convrot_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6,
                           const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
@@ -342,7 +352,8 @@ const char* convrot_last_error(void);
  *   gemm_mfma32      "0" | "1"            4-wave 256x256 W4A4 tile on 32x32x32 MFMAs: never,
  *                                         or always (plain 16-bit outputs)
  *   fp6_tile         "BMxBN"              FP6 W4A4 tile: 256x256, 256x224, 128x256, 128x192 or 128x128
- * Returns CONVROT_ERR_INVALID for an unknown name or a malformed value.
+ * Returns CONVROT_ERR_INVALID for an unknown name, a malformed value or a
+ * tile the library does not build.
  */
 int convrot_set_tuning(const char* name, const char* value);
 

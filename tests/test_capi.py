@@ -215,3 +215,63 @@ def test_errors_are_thread_local(lib):
     t.start()
     t.join()
     assert seen["msg"] == "" and _err(lib).startswith("W4A4 GEMM requires")
+
+
+def test_fp6_validation(lib):
+    """The FP6 entry points reject what their kernels cannot address before any launch: a
+    weight conversion with in_features not divisible by 128 (no FP6 layout, no GEMM accepts
+    it), and operands whose FP6 blocks pass 2^32 - 2^20 bytes (the GEMM's buffer offsets are
+    32-bit; e.g. 373k rows at K = 15360).  ConvRotLinear sends such products to INT8."""
+    import ctypes
+
+    import torch
+
+    from convrot_mlx_amd import core
+
+    p = 0x10000
+    assert lib.convrot_weight_fp6(None, None, 64, 192, None) == 2
+    assert _err(lib) == "FP6 operands require in_features divisible by 128, got 192"
+    assert lib.convrot_weight_fp6(p, p, 0, 256, None) == 0  # valid, nothing to do
+    g = lib.convrot_w4a4_gemm_fp6
+    limit = core.FP6_MAX_OPERAND_BYTES
+    assert limit == (1 << 32) - (1 << 20)
+    big_m = (limit // (120 * 1536) + 1) * 16  # first 16-row count past the limit at K = 15360
+    assert lib.convrot_fp6_bytes(big_m, 15360) > limit >= lib.convrot_fp6_bytes(big_m - 16, 15360)
+    assert g(p, p, p, p, None, big_m, 3072, 15360, p, BF16, None) == 2
+    assert "exceeds" in _err(lib) and "INT8" in _err(lib)
+    assert g(p, p, p, p, None, 4608, big_m, 15360, p, BF16, None) == 2  # a weight with that many columns
+    assert g(None, p, p, p, None, big_m - 16, 3072, 15360, p, BF16, None) == 1  # in range: next check
+    assert _err(lib) == "null pointer argument"
+    assert not core.fp6_eligible(big_m, 3072, 15360, torch.bfloat16)
+    assert core.fp6_eligible(big_m - 16, 3072, 15360, torch.bfloat16) == core.fp6_operands_enabled()
+    assert core.fp6_bytes(4608, 3072) == lib.convrot_fp6_bytes(4608, 3072) == 24 * 288 * 1536
+    bm, bn = ctypes.c_int(0), ctypes.c_int(0)
+    assert lib.convrot_w4a4_fp6_tile(0, 64, ctypes.byref(bm), ctypes.byref(bn)) == 1
+
+
+@pytest.mark.parametrize("name,value", [("fp6_tile", "64x64"), ("fp6_tile", "256x256x"), ("fp6_tile", "256x192"),
+                                        ("gemm_tile", "100x100"), ("gemm_tile", "192x128w2x2"),
+                                        ("gemm_tile", "256x256w4x2s3"), ("w4a16_tile", "192x128"),
+                                        ("w4a4_smallm_cfg", "T"), ("prep_ni", "x")])
+def test_tuning_rejects_unbuilt_tiles(lib, name, value):
+    """A tile override the library does not build is an error, not a silent fallback to the
+    automatic plan (256x256w4x2 exists only in the register-staged kernel, which has no ring
+    depth)."""
+    assert lib.convrot_set_tuning(name.encode(), value.encode()) == 1
+    assert _err(lib) == f"invalid value '{value}' for tuning override '{name}'"
+
+
+@pytest.mark.parametrize("name,value", [("fp6_tile", "128x192"), ("gemm_tile", "288x192w2x2"),
+                                        ("gemm_tile", "256x256w4x2"), ("gemm_tile", "128x256w2x4s4"),
+                                        ("w4a16_tile", "256x128")])
+def test_tuning_accepts_built_tiles(lib, name, value):
+    import ctypes
+
+    try:
+        assert lib.convrot_set_tuning(name.encode(), value.encode()) == 0
+        if name == "fp6_tile":  # the forced tile is what the plan query reports (no device needed)
+            bm, bn = ctypes.c_int(0), ctypes.c_int(0)
+            assert lib.convrot_w4a4_fp6_tile(4608, 3072, ctypes.byref(bm), ctypes.byref(bn)) == 0
+            assert f"{bm.value}x{bn.value}" == value
+    finally:
+        assert lib.convrot_set_tuning(name.encode(), None) == 0

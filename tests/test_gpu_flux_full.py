@@ -8,6 +8,14 @@ image streams' projections, both single-block linears and the final layer -- mus
 oracle's W4A4 linear bit for bit on the activations the model feeds them (every weight code and
 scale, every output), the whole step must stay within a relative-L2 / cosine bound of the dense
 bf16 step, and repeated steps must be bit-identical.
+
+The same model then runs the fully fused variant the benchmark reports (adaLN modulation and the
+MLP GELU / concatenation inside the preparation kernel, every gated residual in the GEMM
+epilogue).  Its calls bypass forward hooks (forward_modulated, forward_gelu, forward with
+residual=), so wrappers record their operands: each sampled layer's output must equal the oracle's
+producer transform (oracle.modulate, oracle.gelu_producer_rows), W4A4 linear and gated residual
+(oracle.gated_residual) composed, bit for bit, at the row counts the model feeds them (512 / 1024 /
+1536: the FP6 operand path, and 1 row: the INT8 few-row path).
 """
 
 from __future__ import annotations
@@ -42,18 +50,86 @@ SAMPLED = {
     "final_adaln": 1,
     "final_linear": 1024,
 }
+# the fully fused variant: (module name, ConvRotLinear method, rows, gated residual)
+SAMPLED_FUSED = {
+    "double_blocks.0.img_qkv": ("forward_modulated", 1024, False),
+    "double_blocks.0.txt_qkv": ("forward_modulated", 512, False),
+    "double_blocks.0.img_mod.lin": ("forward", 1, False),
+    "double_blocks.9.img_proj": ("forward", 1024, True),
+    "double_blocks.9.txt_proj": ("forward", 512, True),
+    "double_blocks.18.img_mlp.0": ("forward_modulated", 1024, False),
+    "double_blocks.18.img_mlp.2": ("forward_gelu", 1024, True),
+    "double_blocks.18.txt_mlp.2": ("forward_gelu", 512, True),
+    "single_blocks.0.linear1": ("forward_modulated", 1536, False),
+    "single_blocks.37.linear2": ("forward_gelu", 1536, True),
+    "final_linear": ("forward_modulated", 1024, False),
+}
 
 
-@pytest.mark.timeout(600)
+def _record_calls(layer, name, seen):
+    """Instance-level wrappers of the layer's three forwards that store host copies of every
+    operand and of the output (the fused calls do not pass through forward hooks)."""
+    orig = {m: getattr(layer, m) for m in ("forward", "forward_modulated", "forward_gelu")}
+
+    def rows(t):
+        return from_dev(t.reshape(-1, t.shape[-1]))
+
+    def common(kw):
+        res, gate = kw.get("residual"), kw.get("gate")
+        return dict(residual=None if res is None else rows(res), gate=None if gate is None else rows(gate))
+
+    def forward(x, **kw):
+        rec = dict(kind="forward", x=rows(x), **common(kw))
+        out = orig["forward"](x, **kw)
+        seen[name] = dict(rec, out=rows(out))
+        return out
+
+    def forward_modulated(x, shift, scale, eps=1e-6, **kw):
+        rec = dict(kind="forward_modulated", x=rows(x), shift=rows(shift), scale=rows(scale), eps=eps, **common(kw))
+        out = orig["forward_modulated"](x, shift, scale, eps, **kw)
+        seen[name] = dict(rec, out=rows(out))
+        return out
+
+    def forward_gelu(x, head=None, **kw):
+        rec = dict(kind="forward_gelu", x=rows(x), head=None if head is None else rows(head), **common(kw))
+        out = orig["forward_gelu"](x, head, **kw)
+        seen[name] = dict(rec, out=rows(out))
+        return out
+
+    layer.forward, layer.forward_modulated, layer.forward_gelu = forward, forward_modulated, forward_gelu
+    return lambda: [delattr(layer, m) for m in orig]
+
+
+def _oracle_call(orc, rec, w_codes, wscales, bias):
+    """The oracle's composition for one recorded call: producer transform -> A4 codes -> exact
+    dots and epilogue -> gated residual."""
+    x = rec["x"]
+    if rec["kind"] == "forward_modulated":
+        per_vector = x.shape[0] // rec["shift"].shape[0]
+        x = orc.modulate(x, "bfloat16", rec["shift"], rec["scale"], per_vector, rec["eps"])
+    elif rec["kind"] == "forward_gelu":
+        x = orc.gelu_producer_rows(rec["head"], x, "bfloat16")
+    a_codes, xs = orc.prepare_codes(x, "bfloat16", G)
+    out = orc.w4a4_matmul_codes_large(a_codes, w_codes, xs, wscales, bias, "bfloat16")
+    if rec["residual"] is not None:
+        gate = rec["gate"]
+        per_gate = out.shape[0] // gate.shape[0] if gate is not None else 1
+        out = orc.gated_residual(out, rec["residual"], gate, per_gate, "bfloat16")
+    return out
+
+
+@pytest.mark.timeout(900)
 def test_full_size_dit_step(orc, dev):
-    from convrot_mlx_amd import ConvRotLinear, replace_convrot_linears
+    from convrot_mlx_amd import ConvRotLinear, core, replace_convrot_linears
+    from examples.flux1_dev.dit import set_fused_gelu, set_fused_modulation, set_fused_residual
 
     p = FluxParams()
     model = build(p, dev, seed=11)
     inputs = make_inputs(p, img_tokens=1024, txt_tokens=512, device=dev, seed=12)
     modules = dict(model.named_modules())
-    assert all(isinstance(modules[n], nn.Linear) for n in SAMPLED)
-    dense_w = {n: (from_dev(modules[n].weight), from_dev(modules[n].bias.float())) for n in SAMPLED}
+    sampled = sorted(set(SAMPLED) | set(SAMPLED_FUSED))
+    assert all(isinstance(modules[n], nn.Linear) for n in sampled)
+    dense_w = {n: (from_dev(modules[n].weight), from_dev(modules[n].bias.float())) for n in sampled}
     with torch.no_grad():
         ref = model(**inputs).float()
     linears = sum(1 for m in model.modules() if isinstance(m, nn.Linear))
@@ -101,3 +177,33 @@ def test_full_size_dit_step(orc, dev):
     # measured on MI355X at this size: relative L2 ~0.29, cosine ~0.96 (bench seed); a dropped
     # scale or a transposed weight decorrelates the output (relative L2 near 1)
     assert rel < 0.35 and cos > 0.93
+
+    # the fully fused variant (the benchmark's config-5 figure)
+    set_fused_modulation(model, True)
+    set_fused_gelu(model, True)
+    set_fused_residual(model, True)
+    fused_seen: dict[str, dict] = {}
+    restore = [_record_calls(mods[n], n, fused_seen) for n in SAMPLED_FUSED]
+    with torch.no_grad():
+        fused = model(**inputs)
+    for r in restore:
+        r()
+    with torch.no_grad():
+        fused_again = model(**inputs)
+    assert torch.equal(fused, fused_again), "repeated fused steps differ"
+    for name, (kind, rows, with_residual) in SAMPLED_FUSED.items():
+        rec = fused_seen[name]
+        assert rec["kind"] == kind and rec["x"].shape[0] == rows, (name, rec["kind"], rec["x"].shape)
+        assert (rec["residual"] is not None) == with_residual, name
+        layer = mods[name]
+        assert core.fp6_eligible(rows, layer.out_features, layer.in_features, torch.bfloat16) == (rows >= 256), name
+        w, b = dense_w[name]
+        w_codes, wscales = orc.prepare_codes(w, "bfloat16", G)
+        want = _oracle_call(orc, rec, w_codes, wscales, b)
+        bad = int((rec["out"] != want).sum())
+        assert bad == 0, f"fused {name} ({kind}, {rows} rows): {bad} of {want.size} outputs differ from the oracle"
+    fused = fused.float()
+    frel = ((fused - ref).norm() / ref.norm()).item()
+    fcos = F.cosine_similarity(fused.flatten(), ref.flatten(), dim=0).item()
+    print(f"full-size config 5, fused: rel_l2={frel:.4f} cosine={fcos:.5f}")
+    assert frel < 0.35 and fcos > 0.93

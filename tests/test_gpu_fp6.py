@@ -269,6 +269,7 @@ def test_fp6_every_tile(orc, dev, tuning, tile, M, K, N):
     against the oracle, in bf16 and f16."""
     nat = _nat()
     tuning.set("fp6_tile", tile)
+    assert nat.fp6_tile(M, N) == tuple(int(v) for v in tile.split("x")), "the forced tile is not the one planned"
     rng = np.random.default_rng(M * 3 + K + N)
     a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
     w = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
@@ -280,3 +281,79 @@ def test_fp6_every_tile(orc, dev, tuning, tile, M, K, N):
         out = _gemm_fp6(nat, *args, M, N, K, dt, dev)
         _assert_exact(from_dev(out), orc.w4a4_matmul_codes_large(a, w, xs, ws, b, out_dtype),
                       f"tile {tile} {M}x{K}x{N} {out_dtype}")
+
+
+@pytest.mark.parametrize("M", [300, 4600])
+@pytest.mark.parametrize("call", ["forward", "forward_modulated", "forward_gelu"])
+def test_layer_fp6_ragged_rows(orc, dev, M, call):
+    """ConvRotLinear on FP6 operands at a row count that is not a multiple of 16, through each
+    forward with a per-image gated residual, on the library's own torch.empty buffers: a freed
+    allocation of random bytes sits in torch's cache first, so the padding rows of the FP6
+    activation's last 16-row block (never written by the preparation) hold garbage.  Every
+    output equals the oracle's -- the producer transform (oracle.modulate / gelu_producer_rows),
+    the A4 codes, the exact dots, the epilogue, then oracle.gated_residual -- bit for bit
+    (reference: the full-shape route checks of test_core.py:128-137,375-402)."""
+    from convrot_mlx_amd import ConvRotLinear, core, quantize_convrot_weight
+
+    B, K, N, G, HEAD = 2, 3072, 1000, 64, 768
+    L = M // B
+    assert core.fp6_eligible(M, N, K, torch.bfloat16)
+    rng = np.random.default_rng(M + len(call))
+    w16 = outlier_input(int(rng.integers(1 << 30)), (N, K), "bfloat16", orc, std=0.02, frac=0.01, factor=10.0)
+    bias = rng.normal(0, 0.02, size=N).astype(np.float32)
+    qw, ws = quantize_convrot_weight(to_dev(w16, "bfloat16", dev), G)
+    layer = ConvRotLinear(K, N, group_size=G, device=dev).load_nk_weight(qw, ws, torch.from_numpy(bias).to(dev))
+    w_codes, wscales = orc.prepare_codes(w16, "bfloat16", G)
+    assert np.array_equal(from_dev(layer.scales), wscales)
+
+    x16 = outlier_input(int(rng.integers(1 << 30)), (M, K), "bfloat16", orc)
+    res16 = orc.from_f32((rng.normal(size=(M, N)) * 4).astype(np.float32), "bfloat16")
+    gate16 = orc.from_f32(rng.normal(size=(B, N)).astype(np.float32), "bfloat16")
+    x = to_dev(x16, "bfloat16", dev).reshape(B, L, K)
+    res = to_dev(res16, "bfloat16", dev).reshape(B, L, N)
+    gate = to_dev(gate16, "bfloat16", dev).reshape(B, 1, N)
+    junk = torch.randint(0, 256, (64 << 20,), dtype=torch.uint8, device=dev)
+    del junk
+    if call == "forward":
+        rows = x16
+        got = layer(x, residual=res, gate=gate)
+    elif call == "forward_modulated":
+        sh16 = orc.from_f32(rng.normal(size=(B, K)).astype(np.float32), "bfloat16")
+        sc16 = orc.from_f32(rng.normal(size=(B, K)).astype(np.float32), "bfloat16")
+        rows = orc.modulate(x16, "bfloat16", sh16, sc16, L, 1e-6)
+        got = layer.forward_modulated(x, to_dev(sh16, "bfloat16", dev).reshape(B, 1, K),
+                                      to_dev(sc16, "bfloat16", dev).reshape(B, 1, K), eps=1e-6,
+                                      residual=res, gate=gate)
+    else:
+        rows = orc.gelu_producer_rows(x16[:, :HEAD], np.ascontiguousarray(x16[:, HEAD:]), "bfloat16")
+        got = layer.forward_gelu(x[..., HEAD:], head=x[..., :HEAD], residual=res, gate=gate)
+    torch.cuda.synchronize()
+    a_codes, xs = orc.prepare_codes(rows, "bfloat16", G)
+    lin = orc.w4a4_matmul_codes_large(a_codes, w_codes, xs, wscales, bias, "bfloat16")
+    want = orc.gated_residual(lin, res16, gate16, L, "bfloat16")
+    assert got.shape == (B, L, N)
+    _assert_exact(from_dev(got.reshape(M, N)), want, f"{call} M={M}")
+
+
+@pytest.mark.timeout(300)
+def test_video_transfer_shape_bit_exact(orc, dev):
+    """The reference's published Wan 2.2 projection (docs/benchmarks/video-transfer.md:15),
+    M = 7800, K = N = 5120, through ConvRotLinear (G = 256, FP6 operands, with bias) on
+    heavy-tailed operands: weight codes and scales, and every output, equal the oracle's."""
+    from convrot_mlx_amd import ConvRotLinear, core, quantize_convrot_weight
+
+    M, K, N, G = 7800, 5120, 5120, 256
+    assert core.fp6_eligible(M, N, K, torch.bfloat16)
+    w16 = outlier_input(7800, (N, K), "bfloat16", orc, std=0.02, frac=0.01, factor=10.0)
+    x16 = outlier_input(5120, (M, K), "bfloat16", orc)
+    bias = np.random.default_rng(7).normal(0, 0.02, size=N).astype(np.float32)
+    qw, ws = quantize_convrot_weight(to_dev(w16, "bfloat16", dev), G)
+    layer = ConvRotLinear(K, N, group_size=G, device=dev).load_nk_weight(qw, ws, torch.from_numpy(bias).to(dev))
+    got = layer(to_dev(x16, "bfloat16", dev))
+    torch.cuda.synchronize()
+    w_codes, wscales = orc.prepare_codes(w16, "bfloat16", G)
+    assert np.array_equal(orc.unpack_signed_int4(from_dev(qw)), w_codes)
+    assert np.array_equal(from_dev(ws), wscales)
+    a_codes, xs = orc.prepare_codes(x16, "bfloat16", G)
+    _assert_exact(from_dev(got), orc.w4a4_matmul_codes_large(a_codes, w_codes, xs, wscales, bias, "bfloat16"),
+                  "7800x5120->5120")
