@@ -112,6 +112,8 @@ def make_layers(torch, core, dev, M, G, shapes, seed, sets=1, fp6=True):
             layers.append(dict(
                 K=K, N=N, w=w, qw=qw, wq=wq, ws=ws,
                 w6=core.fp6_weight(wq, N, K) if fp6 else None,
+                w6c=core.fp6_weight_compact(wq, N, K) if fp6 else None,
+                form=core.fp6_weight_form(M, N) if fp6 else None,  # the form ConvRotLinear caches
                 a6=torch.empty(core.fp6_shape(M, K), dtype=torch.uint8, device=dev) if fp6 else None,
                 bias=(torch.randn(N, generator=gen, device=dev) * 0.02).float(),
                 x=outliers(torch, gen, dev, (M, K), 1.0, 0.005, 20.0),
@@ -124,11 +126,14 @@ def make_layers(torch, core, dev, M, G, shapes, seed, sets=1, fp6=True):
 
 class PathRunner:
     """Launches of the complete path (prep -> GEMM) of one set of linears on one stream,
-    on FP6 or INT8 operands, with optional HIP events around every launch."""
+    on FP6 or INT8 operands, with optional HIP events around every launch.  FP6 weights are
+    the form ConvRotLinear caches for the shape (core.fp6_weight_form: the compact 0.5-byte
+    form where the GEMM runs a 256-row tile, else the 0.75-byte operand blocks), or with
+    full_weights the operand blocks everywhere."""
 
-    def __init__(self, nat, dev, M, G, fp6=True):
+    def __init__(self, nat, dev, M, G, fp6=True, full_weights=False):
         self.nat, self.lib, self.stream, self.M, self.G = nat, nat.load(), nat.stream_of(dev), M, G
-        self.fp6 = fp6
+        self.fp6, self.full = fp6, full_weights
 
     def prep(self, L):
         nat = self.nat
@@ -138,7 +143,11 @@ class PathRunner:
 
     def gemm(self, L):
         nat = self.nat
-        if self.fp6:
+        if self.fp6 and not self.full and L["form"] == "compact":
+            nat.check(self.lib.convrot_w4a4_gemm_fp6_compact(
+                nat.ptr(L["a6"]), nat.ptr(L["xs"]), nat.ptr(L["w6c"]), nat.ptr(L["ws"]), nat.ptr(L["bias"]), self.M,
+                L["N"], L["K"], None, None, 0, 1, nat.ptr(L["out"]), nat.DTYPE_BF16, self.stream))
+        elif self.fp6:
             nat.check(self.lib.convrot_w4a4_gemm_fp6(nat.ptr(L["a6"]), nat.ptr(L["xs"]), nat.ptr(L["w6"]),
                                                      nat.ptr(L["ws"]), nat.ptr(L["bias"]), self.M, L["N"], L["K"],
                                                      nat.ptr(L["out"]), nat.DTYPE_BF16, self.stream))
@@ -276,8 +285,8 @@ def main() -> int:
             "pct_int8_peak": round(100.0 * tops / INT8_PEAK_TOPS, 2),
         },
         "roofline": {
-            "kernel": ("W4A4 GEMM on FP6 operands (w4a4_gemm_fp6_kernel: v_mfma_scale_f32_16x16x128_f8f6f4 + "
-                       "fused epilogue)" if fp6 else
+            "kernel": ("W4A4 GEMM on FP6 operands, compact weights (w4a4_gemm_fp6_kernel<..., CW=true>: "
+                       "v_mfma_scale_f32_16x16x128_f8f6f4 + fused epilogue)" if fp6 else
                        "W4A4 GEMM (w4a4_gemm_agpr_kernel, 288x192 and 256x256 tiles: INT8 MFMA + fused epilogue)"),
             "bound": "mfma",
             "achieved": round(float(gemm_agg), 2),
@@ -321,6 +330,16 @@ def main() -> int:
             "pct_int8_peak": round(100.0 * ops.sum() / (o_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 2),
             "gemm_per_shape_us": [round(t * 1e3, 2) for t in o_gemm],
             "prep_per_shape_us": [round(t * 1e3, 2) for t in o_prep]}
+        if fp6:
+            full = PathRunner(nat, dev, M, G, fp6=True, full_weights=True)
+            f_ms, f_prep, f_gemm, _, _ = measure_path(torch, np, full, sets, shapes, M, args.steps, 3)
+            result["fp6_full_weights"] = {
+                "what": "the same step on the 1536-byte FP6 weight blocks (0.75 byte a weight) for every shape, "
+                        "instead of the compact ones (0.5 byte a weight, expanded in registers) that "
+                        "ConvRotLinear caches where the GEMM runs a 256-row tile (forms used: "
+                        + ", ".join(L["form"] for L in sets[0]) + ")",
+                "ms_per_step": round(f_ms, 4), "tops": round(float(ops.sum() / (f_ms * 1e-3) / 1e12), 1),
+                "gemm_per_shape_us": [round(t * 1e3, 2) for t in f_gemm]}
     if not args.no_extras:
         dense = dense_control(torch, sets[0], M, shapes)
         dense["convrot_speedup"] = round(dense["ms_per_step"] / ms_per_step, 3)

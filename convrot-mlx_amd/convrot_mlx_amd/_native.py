@@ -51,6 +51,9 @@ SIGNATURES = {
     "convrot_w4a4_gemm_fp6": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_w4a4_gemm_fp6_residual": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp,
                                               _i32, _vp]),
+    "convrot_weight_fp6_compact": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp]),
+    "convrot_w4a4_gemm_fp6_compact": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp,
+                                             _i32, _vp]),
     "convrot_last_error": (ctypes.c_char_p, []),
     "convrot_set_tuning": (_i32, [ctypes.c_char_p, ctypes.c_char_p]),
     "convrot_version": (ctypes.c_char_p, []),

@@ -673,6 +673,13 @@ FP6_MAX_FEATURES = 262144  # exclusive: sums of K products of |v*w| <= 64 stay b
 # larger products run on INT8 operands instead.
 FP6_MAX_OPERAND_BYTES = (1 << 32) - (1 << 20)
 _fp6_operands = os.getenv("CONVROT_FP6_OPERANDS", "1") != "0"
+# Which FP6 weight form ConvRotLinear caches: "compact" (0.5 byte per weight, each
+# fragment expanded in registers inside the GEMM), "full" (the 0.75-byte operand
+# blocks), or "auto": compact where the GEMM's tile for the layer's first FP6
+# product has 256 rows (the expansions hide between its MFMAs: as fast or faster
+# than full), full where it has 128 (compact measured ~10 % slower there).
+FP6_WEIGHT_FORMS = ("auto", "compact", "full")
+_fp6_weight_form = os.getenv("CONVROT_FP6_WEIGHTS", "auto")
 
 
 def set_fp6_operands(enabled: bool) -> None:
@@ -685,6 +692,24 @@ def set_fp6_operands(enabled: bool) -> None:
 
 def fp6_operands_enabled() -> bool:
     return _fp6_operands
+
+
+def set_fp6_weight_form(form: str) -> None:
+    """Choose the FP6 weight form ConvRotLinear caches ("auto", "compact" or "full"; the
+    environment variable CONVROT_FP6_WEIGHTS sets it at import).  Outputs are the same bits
+    with every form; caches built under another form are rebuilt on the next product."""
+    global _fp6_weight_form
+    if form not in FP6_WEIGHT_FORMS:
+        raise ValueError(f"FP6 weight form must be one of {FP6_WEIGHT_FORMS}, got {form!r}")
+    _fp6_weight_form = form
+
+
+def fp6_weight_form(rows: int, out_features: int) -> str:
+    """The FP6 weight form ("compact" or "full") ConvRotLinear caches for a layer whose first
+    FP6 product has `rows` rows and `out_features` output features, under the current setting."""
+    if _fp6_weight_form != "auto":
+        return _fp6_weight_form
+    return "compact" if nat.fp6_tile(rows, out_features)[0] == 256 else "full"
 
 
 def fp6_bytes(rows: int, features: int) -> int:
@@ -712,6 +737,22 @@ def fp6_weight(qweight: torch.Tensor, out_features: int, in_features: int) -> to
     return out
 
 
+def fp6_weight_compact(qweight: torch.Tensor, out_features: int, in_features: int) -> torch.Tensor | None:
+    """CDNA4 W4 weight -> compact FP6 blocks [K/128, ceil(N/16), 1024] (the FP6 fields
+    without their exponent bits, 0.5 byte per weight; include/convrot_amd.h), or None when
+    a code is -8, which has no compact field (fp6_weight holds it).  Reads a flag back from
+    the device, so it synchronizes the stream (an offline conversion)."""
+    if in_features % 128:
+        raise ValueError(f"FP6 operands require in_features divisible by 128, got {in_features}")
+    nat.require_device(qweight)
+    _check_cdna4(qweight, out_features, in_features)
+    out = torch.empty(cdna4_shape(out_features, in_features), dtype=torch.uint8, device=qweight.device)
+    flag = torch.empty((1,), dtype=torch.int32, device=qweight.device)
+    nat.check(nat.load().convrot_weight_fp6_compact(nat.ptr(qweight.contiguous()), nat.ptr(out), nat.ptr(flag),
+                                                    out_features, in_features, nat.stream_of(qweight.device)))
+    return None if int(flag.item()) else out
+
+
 def hip_fused_prepare_convrot_activation_fp6(x: torch.Tensor, group_size: int = CONVROT_GROUP_SIZE):
     """The fused preparation with FP6 output: (FP6 blocks [K/128, ceil(M/16), 1536] of the
     A4 codes, float32 row scales).  Rows of a ragged last 16-row block are left unwritten
@@ -728,9 +769,10 @@ def _w4a4_fp6(act6, w6, xscales, wscales, bias, output_dtype, m: int, n: int, k:
                                                                          torch.float32):
         raise ValueError(f"FP6 W4A4 product needs K % 128 == 0 with K < {FP6_MAX_FEATURES} and a float32, "
                          f"float16 or bfloat16 output; got M={m} N={n} K={k} {output_dtype}")
-    if tuple(act6.shape) != fp6_shape(m, k) or tuple(w6.shape) != fp6_shape(n, k):
-        raise ValueError(f"FP6 operands must be {fp6_shape(m, k)} and {fp6_shape(n, k)}, got "
-                         f"{tuple(act6.shape)} and {tuple(w6.shape)}")
+    compact = tuple(w6.shape) == cdna4_shape(n, k)  # 1024-byte blocks: the compact weight layout
+    if tuple(act6.shape) != fp6_shape(m, k) or (tuple(w6.shape) != fp6_shape(n, k) and not compact):
+        raise ValueError(f"FP6 operands must be {fp6_shape(m, k)} and {fp6_shape(n, k)} (or compact "
+                         f"{cdna4_shape(n, k)}), got {tuple(act6.shape)} and {tuple(w6.shape)}")
     _validate_mpp_epilogue(m, n, xscales, wscales, bias)
     nat.require_device(act6, w6, xscales, wscales, bias)
     xs, ws, b = _f32(xscales), _f32(wscales), _f32(bias)
@@ -741,7 +783,13 @@ def _w4a4_fp6(act6, w6, xscales, wscales, bias, output_dtype, m: int, n: int, k:
     else:
         out = torch.empty((m, n), dtype=output_dtype, device=act6.device)
     lib, stream = nat.load(), nat.stream_of(act6.device)
-    if gr is None:
+    if compact:
+        nat.check(lib.convrot_w4a4_gemm_fp6_compact(
+            nat.ptr(act6), nat.ptr(xs), nat.ptr(w6), nat.ptr(ws), nat.ptr(b), m, n, k,
+            nat.ptr(gr.residual if gr is not None else None), nat.ptr(gr.gate if gr is not None else None),
+            gr.stride if gr is not None else 0, gr.rows_per_gate if gr is not None else 1, nat.ptr(out),
+            nat.dtype_code(output_dtype), stream))
+    elif gr is None:
         nat.check(lib.convrot_w4a4_gemm_fp6(nat.ptr(act6), nat.ptr(xs), nat.ptr(w6), nat.ptr(ws), nat.ptr(b), m, n, k,
                                             nat.ptr(out), nat.dtype_code(output_dtype), stream))
     else:
@@ -755,7 +803,8 @@ def hip_w4a4_fp6_matmul(act6, w6, xscales, wscales, bias, *, output_dtype, rows:
                         in_features: int, residual=None, gate=None, inplace=False):
     """FP6 A4 activations x FP6 W4 weight -> output_dtype [rows, out_features]: the product
     and epilogue of hip_w4a4_int8_matmul (core.py:1088-1120), same bits; residual, gate and
-    inplace as in hip_w4a4_matmul."""
+    inplace as in hip_w4a4_matmul.  w6 is fp6_weight's [K/128, ceil(N/16), 1536] blocks or
+    fp6_weight_compact's [K/128, ceil(N/16), 1024]."""
     m, n = rows, out_features
     gr = None
     if residual is not None:
@@ -925,11 +974,22 @@ class ConvRotLinear(nn.Module):
             self._cdna4_cache = (key, repack_mpp_weight_for_cdna4(q))
         return self._cdna4_cache[1]
 
-    def _fp6_weight(self, w: torch.Tensor) -> torch.Tensor:
-        """The FP6 operand form of the CDNA4 weight `w`, converted once and cached."""
-        key = (w.data_ptr(), w._version, tuple(w.shape), w.device)
+    def _fp6_weight(self, w: torch.Tensor, rows: int) -> torch.Tensor | None:
+        """The FP6 form of the CDNA4 weight `w`, converted once and cached per tensor version
+        (and weight-form setting, see set_fp6_weight_form): the compact layout (0.5 byte per
+        weight) or the FP6 operand blocks (0.75 byte), which also hold a weight with a -8 code
+        (no compact field).  The compact conversion reads a flag back from the device; under
+        graph capture, where it cannot, a layer without a cached form returns None and the
+        product runs on INT8 operands (the same bits)."""
+        key = (w.data_ptr(), w._version, tuple(w.shape), w.device, _fp6_weight_form)
         if self._fp6_cache is None or self._fp6_cache[0] != key:
-            self._fp6_cache = (key, fp6_weight(w, self.out_features, self.in_features))
+            form = fp6_weight_form(rows, self.out_features)
+            if form == "compact" and torch.cuda.is_current_stream_capturing():
+                return None
+            w6 = fp6_weight_compact(w, self.out_features, self.in_features) if form == "compact" else None
+            if w6 is None:
+                w6 = fp6_weight(w, self.out_features, self.in_features)
+            self._fp6_cache = (key, w6)
         return self._fp6_cache[1]
 
     def _project(self, prep, lead: tuple, dtype: torch.dtype, residual, gate, inplace: bool) -> torch.Tensor:
@@ -942,10 +1002,12 @@ class ConvRotLinear(nn.Module):
         rows = math.prod(lead)
         if self.a4:
             gr = None if residual is None else _gated_residual(residual, gate, out_shape, dtype, inplace)
-        if self.a4 and fp6_eligible(rows, self.out_features, self.in_features, dtype):
+        w6 = (self._fp6_weight(w, rows) if self.a4 and fp6_eligible(rows, self.out_features, self.in_features, dtype)
+              else None)
+        if w6 is not None:
             act6, xscales = prep(nat.PREP_FP6)
-            out = _w4a4_fp6(act6, self._fp6_weight(w), xscales, self.scales, self.bias, dtype, rows,
-                            self.out_features, self.in_features, gr)
+            out = _w4a4_fp6(act6, w6, xscales, self.scales, self.bias, dtype, rows, self.out_features,
+                            self.in_features, gr)
         elif self.a4:
             qact, xscales = prep(nat.PREP_INT8)
             out = _w4a4(qact, nat.ACT_INT8, self.in_features, w, xscales, self.scales, self.bias, dtype,

@@ -128,7 +128,7 @@ int convrot_set_tuning(const char* name, const char* value) {
         v = value[0];
         break;
       case kTuneW4a16Cfg:
-        good = strchr("ABCFT", value[0]) != nullptr && value[1] == '\0';
+        good = strchr("ABCDEFGHIJKT", value[0]) != nullptr && value[1] == '\0';
         v = value[0];
         break;
       default: {
@@ -406,6 +406,24 @@ int convrot_w4a4_gemm_fp6_residual(const uint8_t* act6, const float* xscales, co
                        "convrot_w4a4_gemm_fp6_residual");
 }
 
+int convrot_w4a4_gemm_fp6_compact(const uint8_t* act6, const float* xscales, const uint8_t* w6c,
+                                  const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
+                                  const void* residual, const void* gate, int64_t gate_stride,
+                                  int64_t rows_per_gate, void* out, int out_dtype, void* stream) {
+  int odt = 0;
+  if (int rc = check_fp6(act6, xscales, w6c, wscales, M, N, K, out, out_dtype, &odt)) return rc;
+  if (gate && !residual) return fail(CONVROT_ERR_INVALID, "a gate needs a residual");
+  if (gate && rows_per_gate <= 0)
+    return fail(CONVROT_ERR_INVALID, "rows_per_gate must be positive, got %lld", (long long)rows_per_gate);
+  if (M == 0 || N == 0) return ok();
+  convrot::GatedResidual gr{};
+  if (residual)
+    if (int rc = check_residual(residual, gate, gate_stride, rows_per_gate, M, N, &gr)) return rc;
+  return launch_status(convrot::launch_w4a4_gemm_fp6(act6, xscales, w6c, wscales, bias, M, N, K, out, odt,
+                                                     (hipStream_t)stream, gr, true),
+                       "convrot_w4a4_gemm_fp6_compact");
+}
+
 int64_t convrot_w4a4_workspace_bytes(void) { return (int64_t)convrot::kSkWorkspaceBytes; }
 
 int convrot_w4a4_gemm_ws(const void* act, int act_format, const float* xscales, const uint8_t* qweight,
@@ -554,6 +572,20 @@ int convrot_repack_weight(const uint8_t* in, int in_layout, uint8_t* out, int ou
   if (in == out) return fail(CONVROT_ERR_INVALID, "repack cannot run in place");
   return launch_status(convrot::launch_repack(in, in_layout, out, out_layout, N, K, (hipStream_t)stream),
                        "convrot_repack_weight");
+}
+
+int convrot_weight_fp6_compact(const uint8_t* cdna4, uint8_t* fp6c, int* minus8, int64_t N, int64_t K,
+                               void* stream) {
+  if (N < 0 || K < 0) return fail(CONVROT_ERR_INVALID, "invalid weight shape (%lld, %lld)", (long long)N, (long long)K);
+  if (K % 128)
+    return fail(CONVROT_ERR_UNSUPPORTED, "FP6 operands require in_features divisible by 128, got %lld",
+                (long long)K);
+  if ((N == 0 || K == 0) && !minus8) return ok();
+  if (((N && K) && (!cdna4 || !fp6c))) return fail(CONVROT_ERR_INVALID, "null pointer argument");
+  if (!aligned(cdna4, 16) || !aligned(fp6c, 16) || !aligned(minus8, 4))
+    return fail(CONVROT_ERR_INVALID, "cdna4 and fp6c must be 16-byte aligned, minus8 4-byte aligned");
+  return launch_status(convrot::launch_weight_fp6c(cdna4, fp6c, minus8, N, K, (hipStream_t)stream),
+                       "convrot_weight_fp6_compact");
 }
 
 int convrot_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, void* stream) {

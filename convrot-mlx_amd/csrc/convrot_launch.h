@@ -101,9 +101,11 @@ size_t w4a4_plan_workspace_bytes(int act_format, int64_t M, int64_t N, int64_t K
 constexpr size_t kNoAllocScratchBytes = kSkWorkspaceBytes;
 hipError_t noalloc_scratch(hipStream_t stream, Workspace* out);
 
+// w6: FP6 operand blocks (1536 bytes a 16 x 128 block), or with compact_weights
+// the compact layout of weights whose codes lie in [-7, 7] (1024 bytes a block).
 hipError_t launch_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
                                 const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
-                                hipStream_t stream, const GatedResidual& gr);
+                                hipStream_t stream, const GatedResidual& gr, bool compact_weights = false);
 
 // Few-row W4A4 kernel (int8 activation codes only); launch_w4a4_gemm routes
 // small M here.
@@ -128,5 +130,10 @@ hipError_t launch_repack(const uint8_t* in, int in_layout, uint8_t* out, int out
                          hipStream_t stream);
 
 hipError_t launch_weight_fp6(const uint8_t* cdna4, uint8_t* fp6, int64_t N, int64_t K, hipStream_t stream);
+
+// CDNA4 int4 weight -> compact FP6 blocks; *minus8 (device int, may be null) is
+// zeroed, then set to 1 if a code is -8 (no compact field: those blocks are void).
+hipError_t launch_weight_fp6c(const uint8_t* cdna4, uint8_t* fp6c, int* minus8, int64_t N, int64_t K,
+                              hipStream_t stream);
 
 }  // namespace convrot

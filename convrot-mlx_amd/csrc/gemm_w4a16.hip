@@ -564,9 +564,16 @@ hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, con
   // tiles of long K and stays in A up to M = 256, 78 us against 99 us).
   const double m16 = (double)((M + 15) / 16 * 16);
   if (M >= kTiledMinM && tiled_plan(M, N, K).us < 2.0 * m16 * (double)N * (double)K / 246e6 + 5.0) cfg = 'T';
-  if (const int v = tuning(kTuneW4a16Cfg); v == 'A' || v == 'B' || v == 'C' || v == 'F' || v == 'T') cfg = (char)v;
+  if (const int v = tuning(kTuneW4a16Cfg); v >= 'A' && v <= 'Z') cfg = (char)v;
   switch (cfg) {
     case 'T': return launch_tiled<ADT, ODT>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'D': return launch_t<ADT, ODT, 2, 3, 12, 2, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'E': return launch_t<ADT, ODT, 2, 1, 16, 3, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'G': return launch_t<ADT, ODT, 2, 2, 12, 2, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'H': return launch_t<ADT, ODT, 2, 1, 12, 4, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'I': return launch_t<ADT, ODT, 2, 1, 16, 2, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'J': return launch_t<ADT, ODT, 1, 3, 8, 3, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'K': return launch_t<ADT, ODT, 2, 3, 8, 3, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
     case 'C': return launch_t<ADT, ODT, 2, 2, 8, 2, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
     case 'A':
       return M >= kQuadMinM ? launch_t<ADT, ODT, 1, 2, 8, 3, true>(act, wq, ws, bias, M, N, K, out, gr, stream)

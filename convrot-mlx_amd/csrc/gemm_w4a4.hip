@@ -1424,6 +1424,36 @@ __device__ __forceinline__ i32x6 fp6_operand(const uint8_t* head, const uint8_t*
   return (i32x6){h[0], h[1], h[2], h[3], t[0], t[1]};
 }
 
+// Compact FP6 weights: a weight whose codes lie in [-7, 7] has FP6 fields with
+// both exponent bits zero, 4 bits of information each.  A lane's 32 fields
+// are stored as four dwords i0..i3 of the 6-dword operand d0..d5:
+//   i0 = (d0 & ~Z0) | (d2 & Z0), i1 = (d1 & ~Z1) | (d2 & Z1)  (i2, i3 from d3 .. d5)
+// where Z0 and Z1 are the exponent bits of d0 and d1; d2's exponent bits are
+// the positions in neither mask.  The expansion back is four bit operations
+// per 16 fields, in inline asm so that the scheduler keeps it where the
+// k-loop places it (between MFMAs) and the masks stay in SGPRs.
+constexpr uint32_t kFp6cZ0 = 0x18618618u, kFp6cZ1 = 0x86186186u;
+
+template <bool PAD = false>
+__device__ __forceinline__ i32x6 fp6c_expand(const i32x4& i, uint32_t z0, uint32_t z1) {
+  i32x6 d;
+  asm volatile(
+      "v_bfi_b32 %0, %8, 0, %6\n\t"      // d0 = i0 & ~Z0
+      "v_bfi_b32 %1, %9, 0, %7\n\t"      // d1 = i1 & ~Z1
+      "v_and_b32 %2, %9, %7\n\t"         // i1 & Z1
+      "v_and_or_b32 %2, %6, %8, %2\n\t"  // d2 = (i0 & Z0) | (i1 & Z1)
+      "v_bfi_b32 %3, %8, 0, %10\n\t"     // d3 = i2 & ~Z0
+      "v_bfi_b32 %4, %9, 0, %11\n\t"     // d4 = i3 & ~Z1
+      "v_and_b32 %5, %9, %11\n\t"        // i3 & Z1
+      "v_and_or_b32 %5, %10, %8, %5"       // d5 = (i2 & Z0) | (i3 & Z1)
+      : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5])
+      : "v"(i[0]), "v"(i[1]), "s"(z0), "s"(z1), "v"(i[2]), "v"(i[3]));
+  // wait states between these VALU writes and an MFMA that reads them one
+  // instruction later (callers whose next reader is further away skip it)
+  if constexpr (PAD) asm volatile("s_nop 2" ::: "memory");
+  return d;
+}
+
 // The 4-wave FP6 tile: BM x BN, waves 2 x 2, FN x FM 16 x 16 accumulator
 // blocks per wave in the AGPRs; a 3-stage LDS ring of k-blocks (the tile's
 // activation blocks, then its weight blocks).  Per k-block, one k-step of FN x
@@ -1431,11 +1461,21 @@ __device__ __forceinline__ i32x6 fp6_operand(const uint8_t* head, const uint8_t*
 // block's other activation fragments; a barrier publishes block i+1 and frees
 // the block's stage; half 1 reads block i+1's weights (into the spare set) and
 // first activation fragments, and issues the DMAs of block i+3.
-template <int BM, int BN>
+//
+// CW (compact weights): the weight blocks are 1024 bytes (the compact layout
+// above).  Half 1 reads block i+1's weight fragments raw (16 bytes a lane);
+// fragment 0 is expanded at the end of half 1, after its last use, and
+// fragment fn >= 1 during half 0 of block i+1, which runs its MFMAs fragment
+// by fragment (fn-major), so each expansion overlaps the MFMAs of fragment
+// fn - 1.
+template <int BM, int BN, bool CW = false>
 struct Fp6Engine {
-  static constexpr int NW = 4, STAGES = 3;
+  // A fourth ring stage on the 128-row compact tiles that run one workgroup per
+  // CU: their block i+1 is published at block i's start, half a block earlier.
+  static constexpr int NW = 4, STAGES = (CW && BM == 128 && BN > 128) ? 4 : 3;
   static constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 16, FN = TN / 16, HM = FM / 2;
-  static constexpr int A_BYTES = (BM / 16) * 1536, B_BYTES = (BN / 16) * 1536, STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int WBLK = CW ? 1024 : 1536;  // bytes of one 16 x 128 weight block
+  static constexpr int A_BYTES = (BM / 16) * 1536, B_BYTES = (BN / 16) * WBLK, STAGE_BYTES = A_BYTES + B_BYTES;
   // 1 KB DMA pieces per k-block; a wave issues APW + BPW of them (a count that
   // does not divide by the waves is padded with repeats of the last piece,
   // which rewrite the same bytes)
@@ -1443,10 +1483,12 @@ struct Fp6Engine {
   static constexpr int APW = (A_DMAS + NW - 1) / NW, BPW = (B_DMAS + NW - 1) / NW, LPW = APW + BPW;
   static constexpr int XS_DMAS = (BM * 4 + 255) / 256, WS_DMAS = (BN * 4 + 255) / 256;
   static constexpr int EPI_DMAS = XS_DMAS + 2 * WS_DMAS;
-  static constexpr int EPI_OFF = STAGES * STAGE_BYTES;
+  static constexpr int RS = TN * 2 + 16, STAGING = TM * RS;
+  // the epilogue operands sit past both the ring and the output staging (which
+  // outgrows the ring of compact-weight tiles)
+  static constexpr int EPI_OFF = STAGES * STAGE_BYTES > NW * STAGING ? STAGES * STAGE_BYTES : NW * STAGING;
   static constexpr int WS_OFF = EPI_OFF + XS_DMAS * 256, BIAS_OFF = WS_OFF + WS_DMAS * 256;
   static constexpr int SMEM_BYTES = EPI_OFF + EPI_DMAS * 256;
-  static constexpr int RS = TN * 2 + 16, STAGING = TM * RS;
   static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole DMA pieces (BM and BN multiples of 32)");
   static_assert(FM % 2 == 0 && NW * STAGING <= EPI_OFF && SMEM_BYTES <= 160 * 1024, "LDS of one CU");
   static_assert((STAGES - 1) * LPW <= 63, "vmcnt counts at most 63 DMAs");
@@ -1487,10 +1529,10 @@ struct Fp6Engine {
                                            int m0, int n0) {
     const int kblocks = K / 128, mblocks = (M + 15) / 16;
     ra = buffer_rsrc(act + (int64_t)(m0 / 16) * 1536, (uint32_t)(((int64_t)kblocks * mblocks - m0 / 16) * 1536));
-    rw = buffer_rsrc(wq + (int64_t)(n0 / 16) * 1536, (uint32_t)(((int64_t)kblocks * nblocks - n0 / 16) * 1536));
+    rw = buffer_rsrc(wq + (int64_t)(n0 / 16) * WBLK, (uint32_t)(((int64_t)kblocks * nblocks - n0 / 16) * WBLK));
     vl = (uint32_t)lane * 16u;
     a_kstride = (uint32_t)mblocks * 1536u;
-    w_kstride = (uint32_t)nblocks * 1536u;
+    w_kstride = (uint32_t)nblocks * (uint32_t)WBLK;
   }
 
   __device__ __forceinline__ void issue_piece(int kb, int stage, int idx) {
@@ -1523,6 +1565,110 @@ struct Fp6Engine {
     const uint8_t* blk = smem + stage * STAGE_BYTES + A_BYTES + (wn * FN + fn) * 1536;
     return fp6_operand(blk + 16 * lane, blk + 1024 + 8 * lane);
   }
+  __device__ __forceinline__ i32x4 read_b_raw(int stage, int fn) const {
+    return *(const i32x4*)(smem + stage * STAGE_BYTES + A_BYTES + (wn * FN + fn) * 1024 + 16 * lane);
+  }
+
+  // One quarter of a compact fragment's expansion (two instructions) into d.
+  template <int PART>
+  __device__ __forceinline__ static void expand_part(const i32x4& r, i32x6& d, uint32_t z0, uint32_t z1) {
+    int x, y;
+    if constexpr (PART == 0) {
+      asm volatile("v_bfi_b32 %0, %2, 0, %4\n\tv_bfi_b32 %1, %3, 0, %5"
+                   : "=&v"(x), "=&v"(y) : "s"(z0), "s"(z1), "v"(r[0]), "v"(r[1]));
+      d[0] = x, d[1] = y;
+    } else if constexpr (PART == 1) {
+      asm volatile("v_and_b32 %0, %2, %4\n\tv_and_or_b32 %0, %3, %1, %0"
+                   : "=&v"(x) : "s"(z0), "s"(z1), "v"(r[0]), "v"(r[1]));
+      d[2] = x;
+    } else if constexpr (PART == 2) {
+      asm volatile("v_bfi_b32 %0, %2, 0, %4\n\tv_bfi_b32 %1, %3, 0, %5"
+                   : "=&v"(x), "=&v"(y) : "s"(z0), "s"(z1), "v"(r[2]), "v"(r[3]));
+      d[3] = x, d[4] = y;
+    } else {
+      asm volatile("v_and_b32 %0, %2, %4\n\tv_and_or_b32 %0, %3, %1, %0"
+                   : "=&v"(x) : "s"(z0), "s"(z1), "v"(r[2]), "v"(r[3]));
+      d[5] = x;
+    }
+  }
+
+  // Compact weights: k-block i (ring stage st) with expanded fragments b; block
+  // i+1's raw fragments are read and expanded into bn a quarter fragment (two
+  // instructions) at a time between later MFMAs, so the MFMA pipe never waits
+  // on a burst of expansions.  On the 256-row tiles (FM = 8) half 1 has room
+  // for them all: it reads block i+1's raw fragments first (its stage is
+  // published by the barrier between the halves) and expands them after MFMA
+  // kT0 on.  The 128-row tiles (FM = 4) need both halves (EARLY): a second
+  // barrier at the block's start publishes block i+1's stage, half 0 reads the
+  // raw fragments, and the expansions run from half 0's MFMA kT0 to the end.
+  static constexpr bool kEarly = HM == 2;
+  static constexpr int kT0 = FN + 2;  // first MFMA gap of the expansions (the raw reads landed)
+  static constexpr int kGaps = (kEarly ? 2 : 1) * HM * FN - kT0;
+  // part k of the 4 FN goes after MFMA kT0 + floor(k kGaps / (4 FN)) (counting half 0's
+  // MFMAs first when early); part_lo(t) is the first part at or after gap t
+  static constexpr int part_lo(int t) {
+    const int d = t - kT0;
+    return d <= 0 ? 0 : (d * 4 * FN + kGaps - 1) / kGaps;
+  }
+  static_assert(kGaps > 0 && (4 * FN + kGaps - 1) / kGaps <= 3, "at most three parts a gap");
+
+  // the expansion parts after MFMA g (0 .. 2 HM FN - 1 across the two halves)
+  __device__ __forceinline__ void expand_parts(int g, i32x4 (&raw)[FN], i32x6 (&bn)[FN], uint32_t z0,
+                                               uint32_t z1) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int k = part_lo(g) + j;
+      if (g >= kT0 && k < part_lo(g + 1) && k < 4 * FN) {
+        if (k % 4 == 0) expand_part<0>(raw[k / 4], bn[k / 4], z0, z1);
+        if (k % 4 == 1) expand_part<1>(raw[k / 4], bn[k / 4], z0, z1);
+        if (k % 4 == 2) expand_part<2>(raw[k / 4], bn[k / 4], z0, z1);
+        if (k % 4 == 3) expand_part<3>(raw[k / 4], bn[k / 4], z0, z1);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void block_c2(int st, int nst, int dma_kb, const i32x6 (&b)[FN], i32x6 (&bn)[FN],
+                                           i32x4 (&raw)[FN], i32x6 (&a)[FM], f32x4 (&acc)[FN][FM], int scale,
+                                           uint32_t z0, uint32_t z1) {
+    constexpr int NS = HM * FN;
+    if constexpr (kEarly) {
+      wait_vmcnt<(STAGES - 2) * LPW>();  // block i+1 landed (later blocks' DMAs may be in flight)
+      __builtin_amdgcn_s_barrier();
+    }
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      const int fm = t / FN, fn = t % FN;
+      mfma_fp6(acc[fn][fm], b[fn], a[fm], scale);
+      if (t % 2 == 1 && t / 2 < HM) a[HM + t / 2] = read_a(st, HM + t / 2);
+      if constexpr (kEarly) {
+        if (t < FN) raw[t] = read_b_raw(nst, t);
+        expand_parts(t, raw, bn, z0, z1);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < HM; ++i) asm volatile("" ::"v"(a[i]));
+    wait_vmcnt<(STAGES - 2) * LPW>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      const int fm = HM + t / FN, fn = t % FN;
+      mfma_fp6(acc[fn][fm], b[fn], a[fm], scale);
+      if (!kEarly && t < FN) raw[t] = read_b_raw(nst, t);
+      if (t >= FN && t < FN + HM) a[t - FN] = read_a(nst, t - FN);
+#pragma unroll
+      for (int p = 0; p < LPW; ++p)
+        if (t == (p * NS) / LPW) issue_piece(dma_kb, st, p);
+      expand_parts(kEarly ? NS + t : t, raw, bn, z0, z1);
+    }
+    // The MFMA reads its operand registers over its passes: the half's
+    // fragments (b included) stay live to its end, so no temporary of the
+    // expansions lands in the registers of an MFMA issued just before it.
+#pragma unroll
+    for (int i = HM; i < FM; ++i) asm volatile("" ::"v"(a[i]));
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) asm volatile("" ::"v"(b[fn]));
+  }
 
   // k-block i (ring stage st) with weight fragments b; bn receives block i+1's.
   __device__ __forceinline__ void block(int st, int nst, int dma_kb, const i32x6 (&b)[FN], i32x6 (&bn)[FN],
@@ -1538,7 +1684,7 @@ struct Fp6Engine {
     // in the registers of an MFMA issued just before it
 #pragma unroll
     for (int i = 0; i < HM; ++i) asm volatile("" ::"v"(a[i]));
-    wait_vmcnt<LPW>();
+    wait_vmcnt<(STAGES - 2) * LPW>();
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
 #pragma unroll
@@ -1558,8 +1704,39 @@ struct Fp6Engine {
   __device__ __forceinline__ void run(int n, f32x4 (&acc)[FN][FM]) {
     static_assert(LPW <= 2 * FN * HM, "DMA pieces fit the half");
     const int scale = (int)0x82828282u;  // E8M0 scales of 2^3 (one byte per 32-feature group)
+    if constexpr (CW) {
+      const uint32_t z0 = __builtin_amdgcn_readfirstlane(kFp6cZ0), z1 = __builtin_amdgcn_readfirstlane(kFp6cZ1);
+      i32x6 a[FM], b[FN];
+      i32x4 raw[FN];
+      wait_vmcnt<(STAGES - 1) * LPW>();  // block 0 (and the epilogue operands) landed
+      __builtin_amdgcn_s_barrier();
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) raw[fn] = read_b_raw(0, fn);
+#pragma unroll
+      for (int fm = 0; fm < HM; ++fm) a[fm] = read_a(0, fm);
+      const int last = n - 1;
+      int st = 0;
+      auto nxt = [](int s) { return s + 1 == STAGES ? 0 : s + 1; };
+      {
+        i32x6 b1[FN];
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) b[fn] = fp6c_expand(raw[fn], z0, z1);
+        asm volatile("s_nop 4" ::: "memory");
+        int i = 0;
+        for (; i + 1 < n; i += 2) {
+          block_c2(st, nxt(st), min(i + STAGES, last), b, b1, raw, a, acc, scale, z0, z1);
+          st = nxt(st);
+          block_c2(st, nxt(st), min(i + 1 + STAGES, last), b1, b, raw, a, acc, scale, z0, z1);
+          st = nxt(st);
+        }
+        if (i < n) block_c2(st, nxt(st), min(i + STAGES, last), b, b1, raw, a, acc, scale, z0, z1);
+      }
+      mfma_drain_f(acc);
+      wait_vmcnt<0>();
+      return;
+    }
     i32x6 a[FM], b0[FN], b1[FN];
-    wait_vmcnt<2 * LPW>();  // block 0 (and the epilogue operands) landed
+    wait_vmcnt<(STAGES - 1) * LPW>();  // block 0 (and the epilogue operands) landed
     __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) b0[fn] = read_b(0, fn);
@@ -1582,12 +1759,12 @@ struct Fp6Engine {
 
 // The 4-wave FP6 GEMM, one BM x BN tile per workgroup, with the epilogue of
 // every W4A4 kernel (16-bit or float32 outputs, optional gated residual).
-template <int BM, int BN, int ODT>
+template <int BM, int BN, int ODT, bool CW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, BM * BN <= 128 * 128 ? 2 : 1))) void w4a4_gemm_fp6_kernel(
     const uint8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
     int K, int nblocks, int tiles_m, int tiles_n, GatedResidual gr) {
-  using E = Fp6Engine<BM, BN>;
+  using E = Fp6Engine<BM, BN, CW>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
   E e(smem);
   const int tiles = tiles_m * tiles_n;
@@ -2417,31 +2594,42 @@ Fp6Tile fp6_tile(int64_t M, int64_t N) {
   return best;
 }
 
-template <int BM, int BN, int ODT>
+template <int BM, int BN, int ODT, bool CW>
 hipError_t launch_fp6_tile(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
                            const float* bias, int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr,
                            hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16);
   const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
-  hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<BM, BN, ODT>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, act6,
+  hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<BM, BN, ODT, CW>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, act6,
                      xscales, w6, wscales, bias, out, (int)M, (int)N, (int)K, nblocks, tm, tn, gr);
   return hipGetLastError();
 }
 
-template <int ODT>
+template <int ODT, bool CW>
 hipError_t launch_fp6_t(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
                         const float* bias, int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr,
                         hipStream_t stream) {
   const Fp6Tile t = fp6_tile(M, N);
   if (t.bm == 256 && t.bn == 224)
-    return launch_fp6_tile<256, 224, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+    return launch_fp6_tile<256, 224, ODT, CW>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
   if (t.bm == 128 && t.bn == 128)
-    return launch_fp6_tile<128, 128, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+    return launch_fp6_tile<128, 128, ODT, CW>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
   if (t.bm == 128 && t.bn == 192)
-    return launch_fp6_tile<128, 192, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+    return launch_fp6_tile<128, 192, ODT, CW>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
   if (t.bm == 128)
-    return launch_fp6_tile<128, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
-  return launch_fp6_tile<256, 256, ODT>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+    return launch_fp6_tile<128, 256, ODT, CW>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+  return launch_fp6_tile<256, 256, ODT, CW>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+}
+
+template <bool CW>
+hipError_t launch_fp6_odt(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
+                          const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
+                          hipStream_t stream, const GatedResidual& gr) {
+  switch (out_dtype) {
+    case kF32: return launch_fp6_t<kF32, CW>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+    case kF16: return launch_fp6_t<kF16, CW>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+    default: return launch_fp6_t<kBF16, CW>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
+  }
 }
 
 }  // namespace
@@ -2460,13 +2648,11 @@ void fp6_plan_tile(int64_t M, int64_t N, int* bm, int* bn) {
 
 hipError_t launch_w4a4_gemm_fp6(const uint8_t* act6, const float* xscales, const uint8_t* w6, const float* wscales,
                                 const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
-                                hipStream_t stream, const GatedResidual& gr) {
+                                hipStream_t stream, const GatedResidual& gr, bool compact_weights) {
   if (M == 0 || N == 0) return hipSuccess;
-  switch (out_dtype) {
-    case kF32: return launch_fp6_t<kF32>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
-    case kF16: return launch_fp6_t<kF16>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
-    default: return launch_fp6_t<kBF16>(act6, xscales, w6, wscales, bias, M, N, K, out, gr, stream);
-  }
+  if (compact_weights)
+    return launch_fp6_odt<true>(act6, xscales, w6, wscales, bias, M, N, K, out, out_dtype, stream, gr);
+  return launch_fp6_odt<false>(act6, xscales, w6, wscales, bias, M, N, K, out, out_dtype, stream, gr);
 }
 
 }  // namespace convrot

@@ -142,6 +142,45 @@ __global__ void fp6_weight_kernel(const uint4* __restrict__ in, uint8_t* __restr
   *(uint2*)(o + 1024 + 8 * L) = make_uint2((uint32_t)s[2], (uint32_t)(s[2] >> 32));
 }
 
+// CDNA4 int4 weight -> compact FP6 blocks (the FP6 stream of each lane with the
+// two exponent bits of every field dropped: 1024 bytes a block, see
+// fp6c_expand in gemm_w4a4.hip), one thread per 16-byte lane.  A code of -8
+// (-1.0, the one field with an exponent) has no compact form: the lane stores
+// its fields regardless and raises *minus8.
+constexpr uint32_t kFp6cZ0 = 0x18618618u, kFp6cZ1 = 0x86186186u;
+
+__global__ void fp6c_weight_kernel(const uint4* __restrict__ in, uint4* __restrict__ out, int* __restrict__ minus8,
+                                   int64_t lanes) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= lanes) return;
+  const uint4 v = in[t];
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint64_t s[3] = {0, 0, 0};
+  bool bad = false;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t n = (w[c] >> (8 * j + 4 * h)) & 15u;
+        bad |= n == 8u;
+        const uint64_t code = (((n & 8u) ? kFp6Neg : kFp6Pos) >> (8 * (n & 7u))) & 0x3fu;
+        const int bit = 6 * (8 * c + 4 * h + j);
+        s[bit >> 6] |= code << (bit & 63);
+        if ((bit & 63) > 58) s[(bit >> 6) + 1] |= code >> (64 - (bit & 63));
+      }
+  const uint32_t d0 = (uint32_t)s[0], d1 = (uint32_t)(s[0] >> 32), d2 = (uint32_t)s[1];
+  const uint32_t d3 = (uint32_t)(s[1] >> 32), d4 = (uint32_t)s[2], d5 = (uint32_t)(s[2] >> 32);
+  out[t] = make_uint4((d0 & ~kFp6cZ0) | (d2 & kFp6cZ0), (d1 & ~kFp6cZ1) | (d2 & kFp6cZ1),
+                      (d3 & ~kFp6cZ0) | (d5 & kFp6cZ0), (d4 & ~kFp6cZ1) | (d5 & kFp6cZ1));
+  if (bad && minus8) *minus8 = 1;
+}
+
+__global__ void zero_int_kernel(int* __restrict__ p) {
+  if (threadIdx.x == 0) *p = 0;
+}
+
 inline unsigned grid_for(int64_t total, int block) { return (unsigned)((total + block - 1) / block); }
 
 }  // namespace
@@ -178,6 +217,19 @@ hipError_t launch_repack(const uint8_t* in, int in_layout, uint8_t* out, int out
   if (total == 0) return hipSuccess;
   hipLaunchKernelGGL(repack_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream, in, in_layout, out,
                      out_layout, N, K, total, nblocks);
+  return hipGetLastError();
+}
+
+hipError_t launch_weight_fp6c(const uint8_t* cdna4, uint8_t* fp6c, int* minus8, int64_t N, int64_t K,
+                              hipStream_t stream) {
+  const int64_t lanes = ((K + 127) / 128) * ((N + 15) / 16) * 64;
+  if (minus8) {
+    hipLaunchKernelGGL(zero_int_kernel, dim3(1), dim3(64), 0, stream, minus8);
+    if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  }
+  if (lanes == 0) return hipSuccess;
+  hipLaunchKernelGGL(fp6c_weight_kernel, dim3(grid_for(lanes, 256)), dim3(256), 0, stream, (const uint4*)cdna4,
+                     (uint4*)fp6c, minus8, lanes);
   return hipGetLastError();
 }
 

@@ -328,6 +328,38 @@ int convrot_w4a4_gemm_fp6_residual(const uint8_t* act6, const float* xscales, co
                                    const void* residual, const void* gate, int64_t gate_stride,
                                    int64_t rows_per_gate, void* out, int out_dtype, void* stream);
 
+/*
+ * Compact FP6 weights (no counterpart in the reference): a weight whose codes
+ * all lie in [-7, 7] -- every weight the reference's quantization produces
+ * (core.py:154-158 clips to +-7) -- has FP6 fields whose two exponent bits are
+ * zero.  The compact layout drops them: blocks of 16 rows x 128 features,
+ * 1024 bytes each (convrot_cdna4_bytes(N, K) in all), ordered [K/128][ceil(N/16)];
+ * lane L of a block holds at byte 16 L four dwords I0..I3 built from the
+ * lane's six FP6 stream dwords D0..D5 (the operand layout above) as
+ *   I0 = (D0 & ~Z0) | (D2 & Z0)   I1 = (D1 & ~Z1) | (D2 & Z1)
+ *   I2 = (D3 & ~Z0) | (D5 & Z0)   I3 = (D4 & ~Z1) | (D5 & Z1)
+ * with Z0 = 0x18618618 and Z1 = 0x86186186 (the exponent bits of D0 and D1).
+ *
+ * convrot_weight_fp6_compact converts a CDNA4-layout weight (K % 128 == 0).
+ * minus8 (a device int, or NULL) is zeroed, then set to 1 if a code is -8:
+ * such a weight has no compact form (use convrot_weight_fp6) and the output
+ * blocks are void.
+ */
+int convrot_weight_fp6_compact(const uint8_t* cdna4, uint8_t* fp6c, int* minus8, int64_t N, int64_t K,
+                               void* stream);
+
+/*
+ * convrot_w4a4_gemm_fp6 (residual NULL) or convrot_w4a4_gemm_fp6_residual on
+ * a compact FP6 weight w6c: the GEMM expands each weight fragment to the
+ * operand in registers (four bit operations per 16 codes), reading two thirds
+ * of the weight bytes.  Same outputs bit for bit.  Replaces the same launch
+ * site (core.py:1088-1120).
+ */
+int convrot_w4a4_gemm_fp6_compact(const uint8_t* act6, const float* xscales, const uint8_t* w6c,
+                                  const float* wscales, const float* bias, int64_t M, int64_t N, int64_t K,
+                                  const void* residual, const void* gate, int64_t gate_stride,
+                                  int64_t rows_per_gate, void* out, int out_dtype, void* stream);
+
 /* Thread-local message of the last failed call on this thread ("" if none). */
 const char* convrot_last_error(void);
 

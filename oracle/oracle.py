@@ -485,5 +485,65 @@ def fp6_to_codes(blocks: np.ndarray, rows: int, k: int) -> np.ndarray:
     return full[:rows, :k].astype(np.int8)
 
 
+# Compact FP6 weight layout (no reference counterpart).  A weight whose codes lie in [-7, 7]
+# (every weight quantize_convrot_weight produces: core.py:154-158 clips to +-7) has FP6 fields
+# whose two exponent bits are zero, so each field carries 4 bits of information.  The compact
+# layout keeps the FP6 operand layout's blocks of 16 rows x 128 features and lane order, at
+# 1024 bytes a block ([K/128][R_pad/16][1024]): lane L's four dwords I0..I3 at byte 16*L
+# hold the FP6 stream dwords D0..D5 of that lane (feature i at stream bits 6i..6i+5) as
+#     I0 = (D0 & ~Z0) | (D2 & Z0)    I1 = (D1 & ~Z1) | (D2 & Z1)
+#     I2 = (D3 & ~Z0) | (D5 & Z0)    I3 = (D4 & ~Z1) | (D5 & Z1)
+# where Z0 / Z1 are the exponent-bit positions of D0 / D1 (D3 / D4): the exponent bits of
+# D0 and D1 hold D2's information bits, and D2's own exponent bits are exactly the positions
+# in neither mask.  Expansion back to the operand: D0 = I0 & ~Z0, D1 = I1 & ~Z1,
+# D2 = (I0 & Z0) | (I1 & Z1), four bit operations per 16 fields.
+FP6C_Z0 = 0x18618618
+FP6C_Z1 = 0x86186186
+FP6C_BLOCK_BYTES = 1024
+
+
+def _fp6_lane_dwords(blocks: np.ndarray) -> np.ndarray:
+    """FP6 blocks [kb, rb, 1536] -> the stream dwords D0..D5 of each lane, [kb, rb, 64, 6] uint32."""
+    kb, rb, _ = blocks.shape
+    head = np.ascontiguousarray(blocks[..., :1024]).view("<u4").reshape(kb, rb, 64, 4)
+    tail = np.ascontiguousarray(blocks[..., 1024:]).view("<u4").reshape(kb, rb, 64, 2)
+    return np.concatenate([head, tail], axis=-1)
+
+
+def codes_to_fp6c(codes: np.ndarray) -> np.ndarray:
+    """Row-major int8 codes [R, K] in [-7, 7] (K % 128 == 0) -> compact FP6 blocks
+    [K/128, R_pad/16, 1024]."""
+    codes = np.asarray(codes)
+    if codes.size and (codes.min() < -7 or codes.max() > 7):
+        raise ValueError("the compact FP6 layout holds the codes -7 .. 7 only")
+    d = _fp6_lane_dwords(codes_to_fp6(codes))
+    z0, z1 = np.uint32(FP6C_Z0), np.uint32(FP6C_Z1)
+    i0 = (d[..., 0] & ~z0) | (d[..., 2] & z0)
+    i1 = (d[..., 1] & ~z1) | (d[..., 2] & z1)
+    i2 = (d[..., 3] & ~z0) | (d[..., 5] & z0)
+    i3 = (d[..., 4] & ~z1) | (d[..., 5] & z1)
+    lanes = np.stack([i0, i1, i2, i3], axis=-1).astype("<u4")
+    kb, rb = lanes.shape[:2]
+    return np.ascontiguousarray(lanes.view(np.uint8).reshape(kb, rb, 1024))
+
+
+def fp6c_expand(blocks: np.ndarray) -> np.ndarray:
+    """Compact FP6 blocks [kb, rb, 1024] -> the FP6 operand blocks [kb, rb, 1536] the GEMM's
+    matrix instruction reads (the kernel's in-register expansion)."""
+    kb, rb, _ = blocks.shape
+    i = np.ascontiguousarray(blocks).view("<u4").reshape(kb, rb, 64, 4)
+    z0, z1 = np.uint32(FP6C_Z0), np.uint32(FP6C_Z1)
+    d = np.stack([i[..., 0] & ~z0, i[..., 1] & ~z1, (i[..., 0] & z0) | (i[..., 1] & z1),
+                  i[..., 2] & ~z0, i[..., 3] & ~z1, (i[..., 2] & z0) | (i[..., 3] & z1)], axis=-1).astype("<u4")
+    head = d[..., :4].view(np.uint8).reshape(kb, rb, 1024)
+    tail = np.ascontiguousarray(d[..., 4:]).view(np.uint8).reshape(kb, rb, 512)
+    return np.ascontiguousarray(np.concatenate([head, tail], axis=-1))
+
+
+def fp6c_to_codes(blocks: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """Exact inverse of codes_to_fp6c, dropping the padding."""
+    return fp6_to_codes(fp6c_expand(blocks), rows, k)
+
+
 def cpu_threads() -> int:
     return len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)

@@ -53,3 +53,13 @@ def tuning():
     yield _Tuning()
     for name in used:
         _native.set_tuning(name, None)
+
+
+@pytest.fixture
+def fp6_form():
+    """set(form) picks the FP6 weight form ConvRotLinear caches for one test
+    (set_fp6_weight_form); "auto" is restored at teardown."""
+    from convrot_mlx_amd import core
+
+    yield core.set_fp6_weight_form
+    core.set_fp6_weight_form("auto")

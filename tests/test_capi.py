@@ -247,6 +247,18 @@ def test_fp6_validation(lib):
     assert core.fp6_bytes(4608, 3072) == lib.convrot_fp6_bytes(4608, 3072) == 24 * 288 * 1536
     bm, bn = ctypes.c_int(0), ctypes.c_int(0)
     assert lib.convrot_w4a4_fp6_tile(0, 64, ctypes.byref(bm), ctypes.byref(bn)) == 1
+    # compact weights: the same shape rules, and a gate needs a residual
+    assert lib.convrot_weight_fp6_compact(None, None, None, 64, 192, None) == 2
+    assert _err(lib) == "FP6 operands require in_features divisible by 128, got 192"
+    assert lib.convrot_weight_fp6_compact(p, p, p + 2, 64, 256, None) == 1
+    assert "4-byte aligned" in _err(lib)
+    c = lib.convrot_w4a4_gemm_fp6_compact
+    assert c(p, p, p, p, None, big_m, 3072, 15360, None, None, 0, 1, p, BF16, None) == 2
+    assert c(p, p, p, p, None, 64, 64, 256, None, p, 64, 1, p, BF16, None) == 1
+    assert _err(lib) == "a gate needs a residual"
+    assert c(p, p, p, p, None, 64, 64, 256, p, p, 64, 0, p, BF16, None) == 1
+    assert _err(lib) == "rows_per_gate must be positive, got 0"
+    assert c(p, p, p, p, None, 0, 64, 256, None, None, 0, 1, p, BF16, None) == 0
 
 
 @pytest.mark.parametrize("name,value", [("fp6_tile", "64x64"), ("fp6_tile", "256x256x"), ("fp6_tile", "256x192"),

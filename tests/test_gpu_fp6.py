@@ -357,3 +357,160 @@ def test_video_transfer_shape_bit_exact(orc, dev):
     a_codes, xs = orc.prepare_codes(x16, "bfloat16", G)
     _assert_exact(from_dev(got), orc.w4a4_matmul_codes_large(a_codes, w_codes, xs, wscales, bias, "bfloat16"),
                   "7800x5120->5120")
+
+
+# ---- compact FP6 weights (the FP6 fields without their exponent bits, 0.5 byte a weight)
+
+
+def _weight_fp6c(nat, wq_dev, N, K, dev):
+    out = torch.zeros(int(nat.load().convrot_cdna4_bytes(N, K)), dtype=torch.uint8, device=dev)
+    flag = torch.full((1,), 7, dtype=torch.int32, device=dev)
+    nat.check(nat.load().convrot_weight_fp6_compact(nat.ptr(wq_dev), nat.ptr(out), nat.ptr(flag), N, K,
+                                                    nat.stream_of(dev)))
+    torch.cuda.synchronize()
+    return out, int(flag.item())
+
+
+def _gemm_fp6c(nat, a6, xs, w6c, ws, b, M, N, K, dtype, dev, residual=None, gate=None, gate_stride=0, rpg=1):
+    out = torch.empty((M, N), dtype=dtype, device=dev)
+    nat.check(nat.load().convrot_w4a4_gemm_fp6_compact(
+        nat.ptr(a6), nat.ptr(xs), nat.ptr(w6c), nat.ptr(ws), nat.ptr(b), M, N, K, nat.ptr(residual), nat.ptr(gate),
+        gate_stride, rpg, nat.ptr(out), nat.dtype_code(dtype), nat.stream_of(dev)))
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("N,K", [(46, 128), (264, 384), (3072, 3072), (1000, 15360)])
+def test_weight_fp6_compact_matches_oracle(orc, dev, N, K):
+    """CDNA4 weight -> compact FP6 blocks: every byte as oracle.codes_to_fp6c of the same
+    codes (padding included), the -8 flag cleared; a -8 code anywhere raises the flag."""
+    nat = _nat()
+    rng = np.random.default_rng(N + K + 6)
+    w = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
+    got, flag = _weight_fp6c(nat, _u8(orc.codes_to_cdna4(w), dev), N, K, dev)
+    assert flag == 0
+    _assert_exact(from_dev(got), orc.codes_to_fp6c(w).reshape(-1), f"compact weight {N}x{K}")
+    assert np.array_equal(orc.fp6c_to_codes(from_dev(got).reshape(K // 128, -1, 1024), N, K), w)
+    w[N // 2, K - 1] = -8
+    _, flag = _weight_fp6c(nat, _u8(orc.codes_to_cdna4(w), dev), N, K, dev)
+    assert flag == 1
+
+
+@pytest.mark.parametrize("tile", ["256x256", "256x224", "128x256", "128x128", "128x192"])
+@pytest.mark.parametrize("M,K,N", [(300, 384, 1000), (37, 128, 48), (520, 1536, 264), (1000, 640, 232)])
+def test_fp6_compact_gemm_every_tile(orc, dev, tuning, tile, M, K, N):
+    """The FP6 GEMM on compact weights (each fragment expanded in registers), every tile forced,
+    ragged M / N: bit-exact against the oracle in bf16, f16 and f32, and a gated residual in
+    bf16 against oracle.gated_residual."""
+    nat = _nat()
+    tuning.set("fp6_tile", tile)
+    rng = np.random.default_rng(M * 5 + K + N)
+    a = rng.integers(-7, 8, size=(M, K), dtype=np.int8)
+    w = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
+    a[1] = 0
+    w[2] = 7
+    w[3] = -7
+    xs = rng.uniform(0.01, 0.2, size=(M,)).astype(np.float32)
+    ws = rng.uniform(0.01, 0.2, size=(N,)).astype(np.float32)
+    b = rng.normal(size=(N,)).astype(np.float32)
+    args = (_u8(orc.codes_to_fp6(a), dev), _u8(xs, dev), _u8(orc.codes_to_fp6c(w), dev), _u8(ws, dev), _u8(b, dev))
+    for out_dtype, dt in (("bfloat16", torch.bfloat16), ("float16", torch.float16), ("float32", torch.float32)):
+        out = _gemm_fp6c(nat, *args, M, N, K, dt, dev)
+        _assert_exact(from_dev(out), orc.w4a4_matmul_codes_large(a, w, xs, ws, b, out_dtype),
+                      f"compact tile {tile} {M}x{K}x{N} {out_dtype}")
+    res16 = orc.from_f32((rng.normal(size=(M, N)) * 4).astype(np.float32), "bfloat16")
+    gate16 = orc.from_f32(rng.normal(size=(2, N)).astype(np.float32), "bfloat16")
+    rpg = (M + 1) // 2
+    out = _gemm_fp6c(nat, *args, M, N, K, torch.bfloat16, dev, residual=to_dev(res16, "bfloat16", dev),
+                     gate=to_dev(gate16, "bfloat16", dev), gate_stride=N, rpg=rpg)
+    lin = orc.w4a4_matmul_codes_large(a, w, xs, ws, b, "bfloat16")
+    _assert_exact(from_dev(out), orc.gated_residual(lin, res16, gate16, rpg, "bfloat16"), f"compact residual {tile}")
+
+
+def test_layer_caches_compact_weights_except_minus8(orc, dev, fp6_form):
+    """ConvRotLinear caches the compact form for a quantized weight (0.5 byte a weight) and
+    the 1536-byte FP6 blocks for a weight holding a -8 code (assigned as raw CDNA4 bytes);
+    both layers reproduce the oracle bit for bit."""
+    from convrot_mlx_amd import ConvRotLinear, core
+
+    fp6_form("compact")
+    M, K, N = 300, 384, 200
+    rng = np.random.default_rng(300)
+    x16 = orc.from_f32(rng.normal(size=(M, K)).astype(np.float32), "bfloat16")
+    a_codes, xs = orc.prepare_codes(x16, "bfloat16", 64)
+    for minus8 in (False, True):
+        w = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
+        if minus8:
+            w[7, 100] = -8
+        ws = rng.uniform(0.001, 0.01, size=N).astype(np.float32)
+        b = rng.normal(size=N).astype(np.float32)
+        layer = ConvRotLinear(K, N, group_size=64, device=dev)
+        layer.qweight = _u8(orc.codes_to_cdna4(w), dev)
+        layer.scales = _u8(ws, dev)
+        layer.bias = _u8(b, dev)
+        got = layer(to_dev(x16, "bfloat16", dev))
+        torch.cuda.synchronize()
+        w6 = layer._fp6_cache[1]
+        assert w6.shape[-1] == (1536 if minus8 else 1024)
+        assert w6.numel() == (core.fp6_bytes(N, K) if minus8 else int(np.prod(core.cdna4_shape(N, K))))
+        _assert_exact(from_dev(got), orc.w4a4_matmul_codes_large(a_codes, w, xs, ws, b, "bfloat16"),
+                      f"layer, -8 in weight: {minus8}")
+
+
+def test_fp6_weight_form_policy(orc, dev, fp6_form):
+    """The automatic FP6 weight form: compact where the GEMM's tile has 256 rows (config 3's
+    4608-row products), the 1536-byte operand blocks where it has 128 (512 rows); a forced
+    form applies everywhere, a bad name raises, and a layer rebuilds its cache when the
+    setting changes -- every form giving the same output bits."""
+    from convrot_mlx_amd import ConvRotLinear, core, quantize_convrot_weight
+
+    assert core.fp6_weight_form(4608, 3072) == "compact" and core.fp6_weight_form(4608, 21504) == "compact"
+    assert core.fp6_weight_form(512, 3072) == "full"
+    with pytest.raises(ValueError, match="weight form"):
+        core.set_fp6_weight_form("tiny")
+    M, K, N, G = 512, 1024, 768, 64
+    gen = torch.Generator(device=dev).manual_seed(6)
+    qw, ws = quantize_convrot_weight((torch.randn((N, K), generator=gen, device=dev) * 0.02).to(torch.bfloat16), G)
+    layer = ConvRotLinear(K, N, group_size=G, device=dev).load_nk_weight(qw, ws)
+    x = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+    outs = {}
+    for form, block in (("auto", 1536), ("compact", 1024), ("full", 1536)):
+        fp6_form(form)
+        outs[form] = layer(x)
+        torch.cuda.synchronize()
+        assert layer._fp6_cache[1].shape[-1] == block, form
+    assert torch.equal(outs["compact"], outs["full"]) and torch.equal(outs["auto"], outs["full"])
+
+
+def test_layer_under_graph_capture_without_fp6_cache(orc, dev, fp6_form):
+    """A layer whose FP6 weight form is not cached yet, first called under HIP-graph capture,
+    runs on INT8 operands (the compact conversion reads a flag back and cannot run there);
+    every replay equals the eager FP6 result bit for bit, and the cache appears on the next
+    eager call."""
+    from convrot_mlx_amd import ConvRotLinear, core, quantize_convrot_weight
+
+    fp6_form("compact")
+    M, K, N, G = 512, 1024, 768, 64
+    gen = torch.Generator(device=dev).manual_seed(5)
+    w = (torch.randn((N, K), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    qw, ws = quantize_convrot_weight(w, G)
+    layer = ConvRotLinear(K, N, group_size=G, device=dev).load_nk_weight(qw, ws)
+    x = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        layer(x[:16])  # the few-row path: workspace-free, no FP6 form
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            static = layer(x)
+        assert layer._fp6_cache is None
+        eager = layer(x)
+        torch.cuda.synchronize()
+        assert layer._fp6_cache is not None and layer._fp6_cache[1].shape[-1] == 1024
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static, eager)
+            layer(x[:300])
+    torch.cuda.current_stream().wait_stream(stream)

@@ -358,6 +358,42 @@ def test_fp6_layout_brute_force(orc):
     assert np.array_equal(cd, v)  # same (row, feature) -> lane assignment: lane 16*(k%128//32) + r%16
 
 
+def test_fp6c_masks_are_the_exponent_bits(orc):
+    """The compact layout's masks, derived from the e2m3 field layout: field i of a lane's
+    16-field run sits at stream bits 6i .. 6i+5 with its exponent at 6i+3, 6i+4; Z0 / Z1 are
+    those positions inside dwords D0 / D1, and D2's exponent positions are exactly the bits in
+    neither mask (so D2's information bits fill D0's and D1's exponent bits)."""
+    exp_bits = [6 * i + b for i in range(16) for b in (3, 4)]
+    masks = [sum(1 << (p - 32 * d) for p in exp_bits if 32 * d <= p < 32 * d + 32) for d in range(3)]
+    assert masks[0] == orc.FP6C_Z0 and masks[1] == orc.FP6C_Z1
+    assert orc.FP6C_Z0 & orc.FP6C_Z1 == 0
+    assert orc.FP6C_Z0 | orc.FP6C_Z1 == ~masks[2] & 0xFFFFFFFF
+    assert bin(orc.FP6C_Z0).count("1") + bin(orc.FP6C_Z1).count("1") + bin(masks[2]).count("1") == 32
+
+
+def test_fp6c_layout_round_trips_every_code_at_every_position(orc):
+    """Every code -7 .. 7 at every one of a lane's 32 positions (the rest random), in a ragged
+    37 x 256 operand: expanding the compact blocks gives the FP6 operand blocks bit for bit,
+    and the codes come back.  Swapping the masks (a plausible slip) does not round-trip."""
+    rng = np.random.default_rng(66)
+    R, K = 37, 256
+    for v in range(-7, 8):
+        c = rng.integers(-7, 8, size=(R, K), dtype=np.int8)
+        c[:, (np.arange(K) + v) % 32 == 0] = v
+        c[np.arange(R) % 5 == 0] = v
+        blocks = orc.codes_to_fp6c(c)
+        assert blocks.shape == (2, 3, 1024)
+        assert np.array_equal(orc.fp6c_expand(blocks), orc.codes_to_fp6(c))
+        assert np.array_equal(orc.fp6c_to_codes(blocks, R, K), c)
+    i = np.ascontiguousarray(blocks).view("<u4").reshape(2, 3, 64, 4)
+    z0, z1 = np.uint32(orc.FP6C_Z1), np.uint32(orc.FP6C_Z0)  # swapped
+    d2 = (i[..., 0] & z0) | (i[..., 1] & z1)
+    want = orc.codes_to_fp6(c)[..., :1024].view("<u4").reshape(2, 3, 64, 4)[..., 2]
+    assert not np.array_equal(d2, want)
+    with pytest.raises(ValueError, match="-7 .. 7"):
+        orc.codes_to_fp6c(np.full((16, 128), -8, np.int8))
+
+
 # ------------------------------------------------------------------ matmuls
 
 
