@@ -128,7 +128,7 @@ int convrot_set_tuning(const char* name, const char* value) {
         v = value[0];
         break;
       case kTuneW4a16Cfg:
-        good = strchr("ABCDEFGHIJKT", value[0]) != nullptr && value[1] == '\0';
+        good = strchr("ABCDEFT", value[0]) != nullptr && value[1] == '\0';
         v = value[0];
         break;
       default: {

@@ -533,6 +533,9 @@ hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const f
 //                4.3 us vs 4.9, 12288->3072 8.7 vs 12.3; while 3072->6144
 //                takes 5.8 us in A against 8.1 in B, whose 16 waves per tile
 //                outnumber K = 3072's 24 k-blocks)
+//   D (1,3,8,3)  M <= 16 where the weight tiles split into whole rounds of three
+//                per workgroup (N = 12288 on 256 CUs)
+//   E (2,3,8,2)  17 <= M <= 32 there: both 16-token halves in one workgroup
 //   C (2,2,8,2)  sweeps and tests only (one 32-token tile: slower than two of A)
 //   F (4,2,4,2)  sweeps and tests only (slower than A at every M measured)
 //   T            the tiled kernel (256 / 128 edges), M >= kTiledMinM
@@ -564,16 +567,21 @@ hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, con
   // tiles of long K and stays in A up to M = 256, 78 us against 99 us).
   const double m16 = (double)((M + 15) / 16 * 16);
   if (M >= kTiledMinM && tiled_plan(M, N, K).us < 2.0 * m16 * (double)N * (double)K / 246e6 + 5.0) cfg = 'T';
-  if (const int v = tuning(kTuneW4a16Cfg); v >= 'A' && v <= 'Z') cfg = (char)v;
+  // Three weight tiles a workgroup where that makes whole rounds of 256
+  // workgroups (N = 12288: 768 tiles), one token tile at up to 16 rows and
+  // both 16-row halves of 17 .. 32 rows in one workgroup (every weight byte read
+  // once).  Config 4, 3072 -> 12288 (HIP-graph replays, one box): M = 1 7.65
+  // against 8.1 us in A, M = 8 8.05 against 8.6, M = 32 10.5 against 12.6.
+  if (nblocks % 3 == 0 && (nblocks / 3) % device_cus() == 0 && M <= 32) cfg = M <= 16 ? 'D' : 'E';
+  if (const int v = tuning(kTuneW4a16Cfg); v == 'A' || v == 'B' || v == 'C' || v == 'D' || v == 'E' || v == 'F' ||
+                                           v == 'T')
+    cfg = (char)v;
   switch (cfg) {
     case 'T': return launch_tiled<ADT, ODT>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    case 'D': return launch_t<ADT, ODT, 2, 3, 12, 2, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    case 'E': return launch_t<ADT, ODT, 2, 1, 16, 3, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    case 'G': return launch_t<ADT, ODT, 2, 2, 12, 2, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    case 'H': return launch_t<ADT, ODT, 2, 1, 12, 4, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    case 'I': return launch_t<ADT, ODT, 2, 1, 16, 2, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    case 'J': return launch_t<ADT, ODT, 1, 3, 8, 3, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    case 'K': return launch_t<ADT, ODT, 2, 3, 8, 3, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'D':
+      return M >= kQuadMinM ? launch_t<ADT, ODT, 1, 3, 8, 3, true>(act, wq, ws, bias, M, N, K, out, gr, stream)
+                            : launch_t<ADT, ODT, 1, 3, 8, 3, false>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case 'E': return launch_t<ADT, ODT, 2, 3, 8, 2, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
     case 'C': return launch_t<ADT, ODT, 2, 2, 8, 2, true>(act, wq, ws, bias, M, N, K, out, gr, stream);
     case 'A':
       return M >= kQuadMinM ? launch_t<ADT, ODT, 1, 2, 8, 3, true>(act, wq, ws, bias, M, N, K, out, gr, stream)

@@ -375,7 +375,7 @@ const char* convrot_last_error(void);
  *   gemm_no_dma      "1"                  register-staged int8 W4A4 kernel
  *   gemm_smallm_max  rows                 largest M of the few-row W4A4 kernel (0: never)
  *   w4a4_smallm_cfg  "A" | "B" | "C" | "F"  few-row W4A4 work split
- *   w4a16_cfg        "A" | "B" | "C" | "F" | "T"  W4A16 split or tiled kernel
+ *   w4a16_cfg        "A" .. "F" | "T"     W4A16 split (A, B, C, D, E or F) or tiled kernel
  *   w4a16_tile       "BMxBN"              W4A16 tiled-kernel tile
  *   prep_ni          "1" | "3" | "4"      prep kernel 1024-feature blocks per wave
  *   sk_spin_limit    polls                stream-K bounded wait before giving up

@@ -244,9 +244,10 @@ def test_layer_forwards(orc, dev, backend):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
 @pytest.mark.parametrize("cfg,B,L,K,N", [("A", 1, 5, 256, 200), ("A", 2, 12, 384, 200), ("B", 2, 4, 384, 70),
-                                         ("C", 2, 20, 256, 136), ("F", 1, 40, 512, 96), ("T", 2, 100, 384, 260)])
+                                         ("C", 2, 20, 256, 136), ("D", 2, 7, 384, 200), ("E", 2, 13, 256, 330),
+                                         ("F", 1, 40, 512, 96), ("T", 2, 100, 384, 260)])
 def test_w4a16_kernels(orc, dev, tuning, cfg, B, L, K, N, dtype):
-    """The W4A16 GEMM's gated-residual epilogue on each of its kernels (splits A, B, C, F and
+    """The W4A16 GEMM's gated-residual epilogue on each of its kernels (splits A to F and
     the tiled kernel, forced; split A below and from 8 rows, i.e. both activation load orders),
     per-image gates, ragged N: residual + gate * linear equals
     torch's composition on the same kernel's plain output, bit for bit, out of place and in

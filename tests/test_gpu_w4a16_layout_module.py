@@ -95,8 +95,8 @@ def test_w4a16_config4_complete_path(orc, dev, M, K, N):
     assert (err <= tol).all(), f"max excess {np.max(err - tol)} (max err {err.max()})"
 
 
-@pytest.mark.parametrize("cfg", ["A", "B", "C", "F", "T"])
-@pytest.mark.parametrize("M,K,N", [(17, 96, 46), (37, 2688, 530), (1, 4000, 33), (5, 12288, 3072)])
+@pytest.mark.parametrize("cfg", ["A", "B", "C", "D", "E", "F", "T"])
+@pytest.mark.parametrize("M,K,N", [(17, 96, 46), (37, 2688, 530), (1, 4000, 33), (5, 12288, 3072), (32, 3072, 1000)])
 def test_w4a16_every_split(orc, dev, tuning, cfg, M, K, N):
     """Each W4A16 work split (forced through the w4a16_cfg tuning override) on ragged M/N and on K that is
     not a multiple of the 128-feature block (the tail features must read as zero)."""
@@ -109,7 +109,7 @@ def test_w4a16_every_split(orc, dev, tuning, cfg, M, K, N):
     _w4a16_check(orc, dev, act, "bfloat16", w, ws, b, "bfloat16")
 
 
-@pytest.mark.parametrize("cfg", ["A", "B"])
+@pytest.mark.parametrize("cfg", ["A", "B", "D"])
 @pytest.mark.parametrize("act_dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("K,N", [(3072, 12288), (2720, 530), (12288, 3072)])
 def test_w4a16_load_orders_agree(orc, dev, tuning, cfg, act_dtype, K, N):
