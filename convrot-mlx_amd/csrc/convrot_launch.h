@@ -21,7 +21,7 @@ enum TuneKey : int {
   kTuneGemmNoDma,        // 1: the register-staged W4A4 kernel instead of the DMA kernels
   kTuneGemmSmallmMax,    // largest M the few-row W4A4 kernel takes (0: never)
   kTuneW4a4SmallmCfg,    // few-row W4A4 split, as a character code ('A', 'B', 'C', 'F')
-  kTuneW4a16Cfg,         // W4A16 kernel, as a character code ('A', 'B', 'C', 'F', 'T')
+  kTuneW4a16Cfg,         // W4A16 kernel, as a character code ('A' .. 'F', 'T')
   kTuneW4a16Tile,        // W4A16 tiled kernel tile: bm | bn << 10
   kTunePrepNi,           // prep kernel 1024-feature iterations per wave (1, 3 or 4)
   kTuneSkSpinLimit,      // stream-K bounded wait: polls before an owner gives up

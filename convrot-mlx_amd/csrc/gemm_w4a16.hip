@@ -542,7 +542,7 @@ hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const f
 // At M = 1 both stream the 18.9 MB weight matrix in ~8 us (~2.3 TB/s), where
 // a plain 19 MB device copy takes ~10 us; the rest is weight expansion
 // (~2 VALU ops per code) and the launch/tail.  The w4a16_cfg tuning override
-// (A|B|C|F|T) forces the kernel (sweeps and tests).
+// (A .. F, T) forces the kernel (sweeps and tests).
 constexpr int64_t kTiledMinM = 64;
 // From kQuadMinM rows on, splits A and B load activations in the quad-coalesced
 // order and transpose them through LDS (transpose_quads4): at M = 16 on the
