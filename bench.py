@@ -458,10 +458,13 @@ def w4a16_figure(torch, core, nat, dev):
     bf16, M in {1, 8, 32}.  A ~10 us launch is shorter than the host's launch interval, so the
     launches are captured in a HIP graph and replayed; every replay's output is checked against
     the eager one.  Weights cycle through > 512 MB so each launch streams its int4 weights from
-    HBM.  Headline bytes per GEMM launch: N*K/2 (int4 weights)."""
+    HBM.  The GEMM is convrot_w4a16_gemm_ws with a stream-K workspace, as ConvRotLinear calls it
+    (12288->3072 at M=32 splits K over workgroups).  Headline bytes per GEMM launch: N*K/2 (int4
+    weights)."""
     lib, stream_fn = nat.load(), nat.stream_of
     gen = torch.Generator(device=dev)
     gen.manual_seed(4)
+    work = torch.zeros(int(lib.convrot_w4a4_workspace_bytes()), dtype=torch.uint8, device=dev)
     G = CONFIG4["G"]
     figures = []
     for K, N in CONFIG4["shapes"]:
@@ -481,8 +484,9 @@ def w4a16_figure(torch, core, nat, dev):
                                               None, stream_fn(dev)))
 
             def gemm(i):
-                nat.check(lib.convrot_w4a16_gemm(nat.ptr(rot), nat.DTYPE_BF16, nat.ptr(weights[i]), nat.ptr(ws),
-                                                 nat.ptr(bias), M, N, K, nat.ptr(y), nat.DTYPE_BF16, stream_fn(dev)))
+                nat.check(lib.convrot_w4a16_gemm_ws(nat.ptr(rot), nat.DTYPE_BF16, nat.ptr(weights[i]), nat.ptr(ws),
+                                                    nat.ptr(bias), M, N, K, None, None, 0, 1, nat.ptr(work),
+                                                    work.numel(), nat.ptr(y), nat.DTYPE_BF16, stream_fn(dev)))
 
             timings = {}
             for name, with_prep in (("gemm", False), ("path", True)):
@@ -515,8 +519,9 @@ def w4a16_figure(torch, core, nat, dev):
                             "path_us": round(timings["path"], 2), "int4_weight_GBps": round(gbps, 1),
                             "pct_hbm": round(100 * gbps / HBM_PEAK_GBPS, 1)})
         del weights
-    return {"what": "W4A16 GEMM (int4 weights N*K/2 bytes per launch) and complete path, G=256, bf16; "
-                    "HIP-graph replays, weights cycled through > 512 MB",
+    return {"what": "W4A16 GEMM (int4 weights N*K/2 bytes per launch; convrot_w4a16_gemm_ws with a stream-K "
+                    "workspace, as ConvRotLinear runs it) and complete path, G=256, bf16; HIP-graph replays, "
+                    "weights cycled through > 512 MB",
             "shapes": figures}
 
 

@@ -41,6 +41,8 @@ SIGNATURES = {
     "convrot_w4a16_gemm": (_i32, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "convrot_w4a16_gemm_residual": (_i32, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp,
                                            _i32, _vp]),
+    "convrot_w4a16_gemm_ws": (_i32, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64,
+                                     _vp, _i32, _vp]),
     "convrot_pack_int4": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "convrot_unpack_int4": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "convrot_repack_weight": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _vp]),

@@ -544,15 +544,17 @@ def _gated_residual(residual: torch.Tensor, gate: torch.Tensor | None, out_shape
     return GatedResidual(res, g, stride, rpg, inplace)
 
 
-# Stream-K workspaces of the W4A4 GEMM, one per (device index, stream handle):
-# allocated by torch (zero-filled, stream-ordered) on the stream's first eager
-# W4A4 launch and kept, so the library itself allocates nothing on this path.
+# Stream-K workspaces, one per (device index, stream handle), shared by the
+# W4A4 GEMM (stream-K plans) and the W4A16 GEMM (split-K plans): allocated by
+# torch (zero-filled, stream-ordered) on the stream's first eager launch and
+# kept, so the library itself allocates nothing on these paths.
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def _workspace(device: torch.device) -> torch.Tensor | None:
     """The stream-K workspace of `device`'s current stream, or None under graph capture
-    before one exists (the GEMM then runs a data-parallel plan, same results bit for bit)."""
+    before one exists (the W4A4 GEMM then runs a data-parallel plan, same results bit for
+    bit; the W4A16 GEMM its unsplit plan)."""
     stream = torch.cuda.current_stream(device)
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
     ws = _WORKSPACES.get(key)
@@ -835,20 +837,20 @@ def hip_w4a16_matmul(activations, qweight, wscales, bias, *, output_dtype, out_f
     act = activations.contiguous()
     w = _as_cdna4(qweight, n, k)
     ws, b = _f32(wscales), _f32(bias)
-    if gr is None:
+    if gr is not None and gr.inplace:
+        out = gr.residual.view(m, n)
+    else:
         out = torch.empty((m, n), dtype=output_dtype, device=act.device)
-        nat.check(
-            nat.load().convrot_w4a16_gemm(
-                nat.ptr(act), nat.dtype_code(act.dtype), nat.ptr(w), nat.ptr(ws), nat.ptr(b), m, n, k,
-                nat.ptr(out), nat.dtype_code(output_dtype), nat.stream_of(act.device),
-            )
-        )
-        return out
-    out = gr.residual.view(m, n) if gr.inplace else torch.empty((m, n), dtype=output_dtype, device=act.device)
+    # the stream's W4A4 workspace lets the weight-streaming kernel split K over
+    # workgroups (few output tiles, long K, M <= 32); none under graph capture
+    # before it exists (the unsplit plan)
+    work = _workspace(act.device)
     nat.check(
-        nat.load().convrot_w4a16_gemm_residual(
+        nat.load().convrot_w4a16_gemm_ws(
             nat.ptr(act), nat.dtype_code(act.dtype), nat.ptr(w), nat.ptr(ws), nat.ptr(b), m, n, k,
-            nat.ptr(gr.residual), nat.ptr(gr.gate), gr.stride, gr.rows_per_gate,
+            nat.ptr(gr.residual if gr is not None else None), nat.ptr(gr.gate if gr is not None else None),
+            gr.stride if gr is not None else 0, gr.rows_per_gate if gr is not None else 1,
+            nat.ptr(work), work.numel() if work is not None else 0,
             nat.ptr(out), nat.dtype_code(output_dtype), nat.stream_of(act.device),
         )
     )

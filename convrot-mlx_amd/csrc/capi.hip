@@ -128,7 +128,7 @@ int convrot_set_tuning(const char* name, const char* value) {
         v = value[0];
         break;
       case kTuneW4a16Cfg:
-        good = strchr("ABCDEFT", value[0]) != nullptr && value[1] == '\0';
+        good = strchr("ABCDEFST", value[0]) != nullptr && value[1] == '\0';
         v = value[0];
         break;
       default: {
@@ -535,6 +535,27 @@ int convrot_w4a16_gemm_residual(const void* act, int act_dtype, const uint8_t* q
   return launch_status(convrot::launch_w4a16_gemm(act, act_dtype, qweight, wscales, bias, M, N, K, out, out_dtype,
                                                   (hipStream_t)stream, gr),
                        "convrot_w4a16_gemm_residual");
+}
+
+int convrot_w4a16_gemm_ws(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales,
+                          const float* bias, int64_t M, int64_t N, int64_t K, const void* residual, const void* gate,
+                          int64_t gate_stride, int64_t rows_per_gate, void* workspace, int64_t workspace_bytes,
+                          void* out, int out_dtype, void* stream) {
+  if (int rc = check_w4a16(act, act_dtype, qweight, wscales, M, N, K, out, out_dtype)) return rc;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+    return fail(CONVROT_ERR_INVALID, "invalid workspace (%lld bytes)", (long long)workspace_bytes);
+  if (workspace && !aligned(workspace, 256)) return fail(CONVROT_ERR_INVALID, "workspace must be 256-byte aligned");
+  if (gate && !residual) return fail(CONVROT_ERR_INVALID, "a gate needs a residual");
+  if (gate && rows_per_gate <= 0)
+    return fail(CONVROT_ERR_INVALID, "rows_per_gate must be positive, got %lld", (long long)rows_per_gate);
+  if (M == 0 || N == 0) return ok();
+  convrot::GatedResidual gr{};
+  if (residual)
+    if (int rc = check_residual(residual, gate, gate_stride, rows_per_gate, M, N, &gr)) return rc;
+  const convrot::Workspace work{(uint8_t*)workspace, workspace ? (size_t)workspace_bytes : 0};
+  return launch_status(convrot::launch_w4a16_gemm(act, act_dtype, qweight, wscales, bias, M, N, K, out, out_dtype,
+                                                  (hipStream_t)stream, gr, work),
+                       "convrot_w4a16_gemm_ws");
 }
 
 int convrot_pack_int4(const int8_t* values, int64_t rows, int64_t packed_cols, uint8_t* out, void* stream) {

@@ -276,6 +276,17 @@ __device__ __forceinline__ void dma4(i32x4_sgpr rsrc, uint32_t voffset, uint32_t
   asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc), "{m0}"(lds_addr) : "memory");
 }
 
+// 16 bytes per lane at p + OFF through a device-scope (sc1) load, coherent
+// across CUs and XCDs with the sc1 stores that wrote it.  Issued through asm,
+// so the compiler neither tracks nor waits for it: the caller waits with
+// wait_vmcnt and keeps the uses behind that wait.
+template <int OFF>
+__device__ __forceinline__ i32x4 load_dev16(const void* p) {
+  i32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off offset:%2 sc1" : "=v"(v) : "v"(p), "i"(OFF) : "memory");
+  return v;
+}
+
 // s_waitcnt on vmcnt only (expcnt and lgkmcnt left at "no wait").
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

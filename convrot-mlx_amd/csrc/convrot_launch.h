@@ -21,7 +21,7 @@ enum TuneKey : int {
   kTuneGemmNoDma,        // 1: the register-staged W4A4 kernel instead of the DMA kernels
   kTuneGemmSmallmMax,    // largest M the few-row W4A4 kernel takes (0: never)
   kTuneW4a4SmallmCfg,    // few-row W4A4 split, as a character code ('A', 'B', 'C', 'F')
-  kTuneW4a16Cfg,         // W4A16 kernel, as a character code ('A' .. 'F', 'T')
+  kTuneW4a16Cfg,         // W4A16 kernel, as a character code ('A' .. 'F', 'S', 'T')
   kTuneW4a16Tile,        // W4A16 tiled kernel tile: bm | bn << 10
   kTunePrepNi,           // prep kernel 1024-feature iterations per wave (1, 3 or 4)
   kTuneSkSpinLimit,      // stream-K bounded wait: polls before an owner gives up
@@ -116,9 +116,25 @@ hipError_t launch_w4a4_smallm(const int8_t* act, const float* xscales, const uin
 // Compute units of the current device (cached per device).
 int device_cus();
 
+// The W4A16 weight-streaming kernel can split K over workgroups when the
+// caller gives a stream-K workspace (few weight tiles, long K, M <= 32): each
+// workgroup stores its float32 partial, and the last of a tile group to
+// arrive adds the group's partials in split order (deterministic) and runs
+// the epilogue.  In the workspace: one arrival counter per (weight-tile group,
+// token tile) on its own 128-byte line in the control block's last 12 KiB
+// (after the stream-K words and flags, which this split never touches; each
+// counter is back at zero when its launch ends), and the partials from
+// kW4a16PartialOffset on (the stream-K partial area: W4A4 and W4A16 launches
+// on one stream never overlap in time).
+constexpr size_t kW4a16CounterOffset = 20480;
+constexpr int kW4a16MaxGroups = 96;
+constexpr size_t kW4a16PartialOffset = 32768;
+static_assert(kW4a16CounterOffset + (size_t)kW4a16MaxGroups * 128 <= kW4a16PartialOffset, "counters");
+
 hipError_t launch_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales,
                              const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
-                             hipStream_t stream, const GatedResidual& gr = GatedResidual{});
+                             hipStream_t stream, const GatedResidual& gr = GatedResidual{},
+                             const Workspace& work = Workspace{});
 
 hipError_t launch_pack_int4(const int8_t* values, int64_t rows, int64_t packed_cols, uint8_t* out,
                             hipStream_t stream);

@@ -85,16 +85,28 @@ __device__ __forceinline__ f32x4 mfma16(i32x4 a, i32x4 b, f32x4 c) {
                                                   0, 0);
 }
 
+// Split of K over workgroups (grid.z): workgroup z takes the k-blocks
+// [z * kspan, (z + 1) * kspan).  part: float32 partial fragments, NB * FM of
+// 1 KB (16 bytes a lane) per (group, split), group = blockIdx.y * gridDim.x +
+// blockIdx.x; ctr: the group's arrival counter at ctr[32 * group] (zero
+// before the launch, zero again after it).  gridDim.x is a multiple of the 8
+// XCDs, so the splits of a group (linear workgroup ids x + gridDim.x * z,
+// dispatched round-robin to the XCDs) all run on one XCD and share its L2;
+// the groups past the weight tiles exit at once.
+struct SplitK {
+  uint8_t* part = nullptr;
+  int* ctr = nullptr;
+  int splits = 1;
+  int kspan = 0;
+};
+
 // Single token tile: four waves per SIMD (at most 128 VGPRs), so that the
 // whole grid's weight loads can be in flight at once.
-template <int ADT, int ODT, int FM, int NB, int SPLIT, int KPW, bool QL>
+template <int ADT, int ODT, int FM, int NB, int SPLIT, int KPW, bool QL, bool SK = false>
 __global__ __launch_bounds__(SPLIT * 64) __attribute__((amdgpu_waves_per_eu(FM == 1 ? 4 : 1)))
-void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
-                                                                const uint8_t* __restrict__ wq,
-                                                                const float* __restrict__ wscales,
-                                                                const float* __restrict__ bias,
-                                                                void* __restrict__ out, int M, int N, int K,
-                                                                int nblocks, int kblocks, GatedResidual gr) {
+void w4a16_gemm_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ wq,
+                       const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out,
+                       int M, int N, int K, int nblocks, int kblocks, GatedResidual gr, SplitK sk) {
   __shared__ __attribute__((aligned(16))) f32x4 red[SPLIT > 1 ? SPLIT : 1][NB * FM][64];
   __shared__ __attribute__((aligned(16))) uint8_t xpose[QL ? SPLIT * kXposeBytes : 16];  // per-wave buffers
   __shared__ float epi[2][NB * 16];  // the epilogue's weight scales and bias
@@ -102,6 +114,7 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
   const int nb0 = blockIdx.x * NB;
   const int m0 = blockIdx.y * 16 * FM;
   const int q = lane >> 4, r = lane & 15;
+  if (SK && nb0 >= nblocks) return;  // XCD padding (whole workgroup)
 
   // Wave 0, which alone runs the epilogue, loads the tile's weight scales and
   // bias before the weights, so that their round trip does not follow the
@@ -131,16 +144,21 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
       (void*)(act + (int64_t)m0 * K), (short)0, rows_valid * K * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(wq + (int64_t)nb0 * 1024), (short)0, (int)(((int64_t)kblocks * nblocks - nb0) * 1024), 0x00020000);
-  for (int kb0 = wave * KPW; kb0 < kblocks; kb0 += SPLIT * KPW) {
+  const int kb_lo = SK ? (int)blockIdx.z * sk.kspan : 0;
+  const int kb_hi = SK ? min(kb_lo + sk.kspan, kblocks) : kblocks;
+  for (int kb0 = kb_lo + wave * KPW; kb0 < kb_hi; kb0 += SPLIT * KPW) {
     uint4 w[KPW][NB];
     i32x4 aop[KPW][FM][4];  // lane (q, r) -> 8 values at features kb*128 + 32q + 8c of row r (after QL's transpose)
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
-      const int kb = kb0 + i;  // blocks at or past kblocks read zeros
+      // blocks at or past kblocks read zeros; with SK so do the blocks at or
+      // past kb_hi, which belong to the next split (offset past the range)
+      const int kb = kb0 + i;
+      const bool kin = !SK || kb < kb_hi;
 #pragma unroll
       for (int t = 0; t < NB; ++t) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-            rw, (int)(((uint32_t)kb * (uint32_t)nblocks + (uint32_t)t) * 1024u + (uint32_t)lane * 16u), 0, 0);
+        const uint32_t off = ((uint32_t)kb * (uint32_t)nblocks + (uint32_t)t) * 1024u + (uint32_t)lane * 16u;
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(kin ? off : 0x80000000u), 0, 0);
         w[i][t] = make_uint4(v.x, v.y, v.z, v.w);
       }
 #pragma unroll
@@ -155,7 +173,7 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
           const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
               ra, (int)((uint32_t)row * (uint32_t)K * 2u + (uint32_t)k * 2u), 0, 0);
           // a ragged K end would read the next row: zero it (K is a multiple of 8)
-          aop[i][fm][c] = k < K ? (i32x4){(int)v.x, (int)v.y, (int)v.z, (int)v.w} : (i32x4){0, 0, 0, 0};
+          aop[i][fm][c] = k < K && kin ? (i32x4){(int)v.x, (int)v.y, (int)v.z, (int)v.w} : (i32x4){0, 0, 0, 0};
         }
     }
 #pragma unroll
@@ -191,6 +209,45 @@ void w4a16_gemm_kernel(const uint16_t* __restrict__ act,
         for (int w2 = 1; w2 < SPLIT; ++w2) s += red[w2][t * FM + fm][lane];
         acc[t][fm] = s;
       }
+  }
+
+  if constexpr (SK) {
+    // Store this split's partial (device-scope stores), then count the
+    // arrival once they are complete; the group's last arrival adds all its
+    // partials in split order (the same sum whichever split arrives last),
+    // rearms the counter and runs the epilogue.  No workgroup waits for another.
+    const int grp = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    constexpr int NF = NB * FM;
+    uint8_t* const gbase = sk.part + (size_t)grp * sk.splits * (NF * 1024) + lane * 16;
+    uint64_t* const mine = (uint64_t*)(gbase + (size_t)blockIdx.z * (NF * 1024));
+#pragma unroll
+    for (int t = 0; t < NB; ++t)
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const f32x4 a = acc[t][fm];
+        uint64_t* const p = mine + (t * FM + fm) * 128;
+        __hip_atomic_store(p, (uint64_t)__float_as_uint(a[0]) | ((uint64_t)__float_as_uint(a[1]) << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p + 1, (uint64_t)__float_as_uint(a[2]) | ((uint64_t)__float_as_uint(a[3]) << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    wait_vmcnt<0>();
+    int arrived = 0;
+    if (lane == 0) arrived = atomicAdd(&sk.ctr[32 * grp], 1);
+    if (__builtin_amdgcn_readlane(arrived, 0) != sk.splits - 1) return;
+    if (lane == 0) __hip_atomic_store(&sk.ctr[32 * grp], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int z = 0; z < sk.splits; ++z) {
+      i32x4 v[NF];
+#pragma unroll
+      for (int f = 0; f < NF; ++f) v[f] = load_dev16<0>(gbase + ((size_t)z * NF + f) * 1024);
+      wait_vmcnt<0>();
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        asm volatile("" : "+v"(v[f]));  // the adds stay behind the wait
+        const f32x4 p = __builtin_bit_cast(f32x4, v[f]);
+        acc[f / FM][f % FM] = z == 0 ? p : acc[f / FM][f % FM] + p;
+      }
+    }
   }
 
   // ---- epilogue (core.py:1151-1152): (dots * ws) + bias, rounded once
@@ -536,8 +593,51 @@ hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const f
   const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
   dim3 grid((unsigned)((nblocks + NB - 1) / NB), (unsigned)((M + 16 * FM - 1) / (16 * FM)));
   hipLaunchKernelGGL((w4a16_gemm_kernel<ADT, ODT, FM, NB, SPLIT, KPW, QL>), grid, dim3(64 * SPLIT), 0, stream,
-                     (const uint16_t*)act, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, gr);
+                     (const uint16_t*)act, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, gr, SplitK{});
   return hipGetLastError();
+}
+
+template <int ADT, int ODT, int FM, int NB, int SPLIT, int KPW, bool QL>
+hipError_t launch_sk_t(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M, int64_t N,
+                       int64_t K, void* out, const GatedResidual& gr, const SplitK& sk, hipStream_t stream) {
+  const int nblocks = (int)((N + 15) / 16), kblocks = (int)((K + 127) / 128);
+  const int groups8 = ((nblocks + NB - 1) / NB + 7) / 8 * 8;
+  dim3 grid((unsigned)groups8, (unsigned)((M + 16 * FM - 1) / (16 * FM)), (unsigned)sk.splits);
+  hipLaunchKernelGGL((w4a16_gemm_kernel<ADT, ODT, FM, NB, SPLIT, KPW, QL, true>), grid, dim3(64 * SPLIT), 0, stream,
+                     (const uint16_t*)act, wq, ws, bias, out, (int)M, (int)N, (int)K, nblocks, kblocks, gr, sk);
+  return hipGetLastError();
+}
+
+// Split-K plan for the weight-streaming kernel: three weight tiles and up to
+// 32 token rows (one token tile) per workgroup, eight waves of three k-blocks,
+// the k-blocks cut into `splits` ranges so that groups x splits fills the CUs
+// once.  Possible at M <= 32 with a workspace, at most kW4a16MaxGroups groups
+// of three weight tiles (N <= 4608), at least two splits' worth of groups per
+// CU count and K of at least 48 k-blocks: 12288 -> 3072 runs as 64 groups x 4
+// splits of 24 k-blocks.  Taken automatically from 9 rows on: the split's
+// tail (partial stores acknowledged, the arrival atomic, the partial loads:
+// three device-scope round trips) costs more than it saves below that.
+// HIP-graph replays, unsplit -> split, 12288 -> 3072: M = 1 8.66 -> 9.82 us,
+// M = 8 9.64 -> 10.29, M = 16 11.18 -> 10.62, M = 32 14.25 -> 13.39;
+// 15360 -> 3072: M = 8 11.86 -> 11.33, M = 16 13.66 -> 11.84, M = 32
+// 16.79 -> 15.01.  `forced` (w4a16_cfg "S") drops the row minimum.
+bool w4a16_split_plan(int64_t M, int64_t N, int64_t K, const Workspace& work, bool forced, SplitK* sk) {
+  constexpr int kNB = 3, kKS = 8 * 3;
+  const int64_t nblocks = (N + 15) / 16, kblocks = (K + 127) / 128;
+  const int64_t groups = (nblocks + kNB - 1) / kNB, groups8 = (groups + 7) / 8 * 8;
+  if (!work.ptr || M > 32 || (M < 9 && !forced) || kblocks < 2 * kKS || groups8 > kW4a16MaxGroups) return false;
+  const int64_t splits_fit = device_cus() / groups;
+  if (splits_fit < 2) return false;
+  const int64_t kspan = (kblocks + splits_fit - 1) / splits_fit;
+  const int64_t splits = (kblocks + kspan - 1) / kspan;
+  const int64_t fm = M > 16 ? 2 : 1;
+  const size_t part_bytes = (size_t)(groups8 * splits * kNB * fm) * 1024;
+  if (kW4a16PartialOffset + part_bytes > work.bytes) return false;
+  sk->part = work.ptr + kW4a16PartialOffset;
+  sk->ctr = (int*)(work.ptr + kW4a16CounterOffset);
+  sk->splits = (int)splits;
+  sk->kspan = (int)kspan;
+  return true;
 }
 
 // Configurations (FM token tiles, NB weight tiles, SPLIT waves, KPW blocks
@@ -555,10 +655,12 @@ hipError_t launch_t(const void* act, const uint8_t* wq, const float* ws, const f
 //   C (2,2,8,2)  sweeps and tests only (one 32-token tile: slower than two of A)
 //   F (4,2,4,2)  sweeps and tests only (slower than A at every M measured)
 //   T            the tiled kernel (256 / 128 edges), M >= kTiledMinM
+//   S            split K over workgroups (1,3,8,3) / (2,3,8,3) where A or B
+//                would run and a workspace is given (w4a16_split_plan)
 // At M = 1 both stream the 18.9 MB weight matrix in ~8 us (~2.3 TB/s), where
 // a plain 19 MB device copy takes ~10 us; the rest is weight expansion
 // (~2 VALU ops per code) and the launch/tail.  The w4a16_cfg tuning override
-// (A .. F, T) forces the kernel (sweeps and tests).
+// (A .. F, S, T) forces the kernel (sweeps and tests; S needs a workspace).
 constexpr int64_t kTiledMinM = 64;
 // From kQuadMinM rows on, splits A and B load activations in the quad-coalesced
 // order and transpose them through LDS (transpose_quads4): at M = 16 on the
@@ -573,7 +675,8 @@ constexpr int64_t kTiledMinM = 64;
 constexpr int64_t kQuadMinM = 6;
 template <int ADT, int ODT>
 hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
-                        int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
+                        int64_t N, int64_t K, void* out, const GatedResidual& gr, const Workspace& work,
+                        hipStream_t stream) {
   const int64_t nblocks = (N + 15) / 16;
   char cfg = (M <= 16 && nblocks <= 256) ? 'B' : 'A';
   // From kTiledMinM rows on, the tiled kernel takes over where its modelled
@@ -589,9 +692,19 @@ hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, con
   // once).  Config 4, 3072 -> 12288 (HIP-graph replays, one box): M = 1 7.65
   // against 8.1 us in A, M = 8 8.05 against 8.6, M = 32 10.5 against 12.6.
   if (nblocks % 3 == 0 && (nblocks / 3) % device_cus() == 0 && M <= 32) cfg = M <= 16 ? 'D' : 'E';
-  if (const int v = tuning(kTuneW4a16Cfg); v == 'A' || v == 'B' || v == 'C' || v == 'D' || v == 'E' || v == 'F' ||
-                                           v == 'T')
-    cfg = (char)v;
+  // With a workspace, split K where A or B would leave CUs idle or walk K
+  // twice (12288 -> 3072: 192 weight tiles; see w4a16_split_plan).
+  const int forced = tuning(kTuneW4a16Cfg);
+  SplitK sk;
+  if ((forced == 'S' || (forced < 0 && (cfg == 'A' || cfg == 'B'))) &&
+      w4a16_split_plan(M, N, K, work, forced == 'S', &sk)) {
+    if (M > 16) return launch_sk_t<ADT, ODT, 2, 3, 8, 3, true>(act, wq, ws, bias, M, N, K, out, gr, sk, stream);
+    return M >= kQuadMinM ? launch_sk_t<ADT, ODT, 1, 3, 8, 3, true>(act, wq, ws, bias, M, N, K, out, gr, sk, stream)
+                          : launch_sk_t<ADT, ODT, 1, 3, 8, 3, false>(act, wq, ws, bias, M, N, K, out, gr, sk, stream);
+  }
+  if (forced == 'A' || forced == 'B' || forced == 'C' || forced == 'D' || forced == 'E' || forced == 'F' ||
+      forced == 'T')
+    cfg = (char)forced;
   switch (cfg) {
     case 'T': return launch_tiled<ADT, ODT>(act, wq, ws, bias, M, N, K, out, gr, stream);
     case 'D':
@@ -611,11 +724,12 @@ hipError_t launch_shape(const void* act, const uint8_t* wq, const float* ws, con
 
 template <int ADT>
 hipError_t launch_odt(int odt, const void* act, const uint8_t* wq, const float* ws, const float* bias, int64_t M,
-                      int64_t N, int64_t K, void* out, const GatedResidual& gr, hipStream_t stream) {
+                      int64_t N, int64_t K, void* out, const GatedResidual& gr, const Workspace& work,
+                      hipStream_t stream) {
   switch (odt) {
-    case kF32: return launch_shape<ADT, kF32>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    case kF16: return launch_shape<ADT, kF16>(act, wq, ws, bias, M, N, K, out, gr, stream);
-    default: return launch_shape<ADT, kBF16>(act, wq, ws, bias, M, N, K, out, gr, stream);
+    case kF32: return launch_shape<ADT, kF32>(act, wq, ws, bias, M, N, K, out, gr, work, stream);
+    case kF16: return launch_shape<ADT, kF16>(act, wq, ws, bias, M, N, K, out, gr, work, stream);
+    default: return launch_shape<ADT, kBF16>(act, wq, ws, bias, M, N, K, out, gr, work, stream);
   }
 }
 
@@ -623,10 +737,11 @@ hipError_t launch_odt(int odt, const void* act, const uint8_t* wq, const float* 
 
 hipError_t launch_w4a16_gemm(const void* act, int act_dtype, const uint8_t* qweight, const float* wscales,
                              const float* bias, int64_t M, int64_t N, int64_t K, void* out, int out_dtype,
-                             hipStream_t stream, const GatedResidual& gr) {
+                             hipStream_t stream, const GatedResidual& gr, const Workspace& work) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (act_dtype == kF16) return launch_odt<kF16>(out_dtype, act, qweight, wscales, bias, M, N, K, out, gr, stream);
-  return launch_odt<kBF16>(out_dtype, act, qweight, wscales, bias, M, N, K, out, gr, stream);
+  if (act_dtype == kF16)
+    return launch_odt<kF16>(out_dtype, act, qweight, wscales, bias, M, N, K, out, gr, work, stream);
+  return launch_odt<kBF16>(out_dtype, act, qweight, wscales, bias, M, N, K, out, gr, work, stream);
 }
 
 bool w4a16_tile_known(int bm, int bn) {

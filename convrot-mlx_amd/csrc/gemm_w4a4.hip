@@ -1829,12 +1829,9 @@ constexpr int kSkSpinLimit = 1 << 22;  // ~1 s of s_sleep 4 polls: a lost flag e
 // Its stores stay C++ atomics (64-bit): the compiler must see every store to
 // keep the wait state a VMEM store of more than 64 bits needs before its data
 // registers are rewritten, which it cannot do for a store inside asm.
-template <int OFF>
-__device__ __forceinline__ i32x4 load_dev16(const void* p) {
-  i32x4 v;
-  asm volatile("global_load_dwordx4 %0, %1, off offset:%2 sc1" : "=v"(v) : "v"(p), "i"(OFF) : "memory");
-  return v;
-}
+// (load_dev16 is in convrot_device.h.)
+static_assert(kSkCtlWords + kSkMaxGrid * kSkMaxWaves <= (int)(kW4a16CounterOffset / 4),
+              "the W4A16 split-K counters follow the stream-K flags in the control block");
 
 // One wave's partial tile: fragment f = fn * FM + fm at byte 1024 f + 16 lane.
 template <int FN, int FM>

@@ -249,6 +249,26 @@ int convrot_w4a16_gemm_residual(const void* act, int act_dtype, const uint8_t* q
                                 int64_t gate_stride, int64_t rows_per_gate, void* out,
                                 int out_dtype, void* stream);
 
+/*
+ * convrot_w4a16_gemm / _residual (residual and gate may be NULL) with a
+ * caller-provided workspace: the same zero-filled stream-K workspace that
+ * convrot_w4a4_gemm_ws takes (convrot_w4a4_workspace_bytes() bytes, 256-byte
+ * aligned; both GEMMs may share one per stream, launches on it must not
+ * overlap in time).  With it the weight-streaming kernel may split K over
+ * workgroups (9 <= M <= 32, N <= 4608, K >= 6144: 12288 -> 3072 runs on every
+ * CU and reads each weight byte once); the last workgroup of each tile group adds
+ * the float32 partials in a fixed order, so results are deterministic, and
+ * leaves the workspace ready for the next launch.  workspace = NULL (0 bytes)
+ * gives convrot_w4a16_gemm's plan.  The summation order differs from the
+ * unsplit kernel's, within the float32 accumulation bound.
+ * Replaces mpp_w4a16_matmul (core.py:1123-1152), as convrot_w4a16_gemm.
+ */
+int convrot_w4a16_gemm_ws(const void* act, int act_dtype, const uint8_t* qweight,
+                          const float* wscales, const float* bias, int64_t M, int64_t N,
+                          int64_t K, const void* residual, const void* gate,
+                          int64_t gate_stride, int64_t rows_per_gate, void* workspace,
+                          int64_t workspace_bytes, void* out, int out_dtype, void* stream);
+
 /* pack_signed_int4 (core.py:97-105): int8 [rows, 2*packed_cols] -> uint8 [rows, packed_cols]. */
 int convrot_pack_int4(const int8_t* values, int64_t rows, int64_t packed_cols, uint8_t* out,
                       void* stream);
@@ -375,7 +395,8 @@ const char* convrot_last_error(void);
  *   gemm_no_dma      "1"                  register-staged int8 W4A4 kernel
  *   gemm_smallm_max  rows                 largest M of the few-row W4A4 kernel (0: never)
  *   w4a4_smallm_cfg  "A" | "B" | "C" | "F"  few-row W4A4 work split
- *   w4a16_cfg        "A" .. "F" | "T"     W4A16 split (A, B, C, D, E or F) or tiled kernel
+ *   w4a16_cfg        "A" .. "F" | "S" | "T"  W4A16 split (A .. F), split K over workgroups
+ *                                        (S, with a workspace) or tiled kernel
  *   w4a16_tile       "BMxBN"              W4A16 tiled-kernel tile
  *   prep_ni          "1" | "3" | "4"      prep kernel 1024-feature blocks per wave
  *   sk_spin_limit    polls                stream-K bounded wait before giving up
