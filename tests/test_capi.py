@@ -176,6 +176,26 @@ def test_gemm_residual_validation(lib):
     assert _err(lib) == "gate rows 16 elements apart overlap (N=32)"
 
 
+def test_w4a16_gemm_ws_validation(lib):
+    """convrot_w4a16_gemm_ws runs convrot_w4a16_gemm's checks, then the workspace and residual
+    checks of convrot_w4a4_gemm_ws, before anything is launched."""
+    g = lib.convrot_w4a16_gemm_ws
+    p = 0x10000
+    assert g(p, 0, p, p, None, 4, 32, 64, None, None, 0, 1, None, 0, p, BF16, None) == 1
+    assert _err(lib) == "MPP W4A16 requires float16 or bfloat16 activation, got float32"
+    assert g(p, BF16, p, p, None, 4, 32, 48, None, None, 0, 1, None, 0, p, BF16, None) == 1
+    assert _err(lib) == "W4A16 GEMM requires K divisible by 32, got 48"
+    assert g(p, BF16, p, p, None, 4, 32, 64, None, None, 0, 1, None, 4096, p, BF16, None) == 1
+    assert _err(lib) == "invalid workspace (4096 bytes)"
+    assert g(p, BF16, p, p, None, 4, 32, 64, None, None, 0, 1, p + 16, 4096, p, BF16, None) == 1
+    assert _err(lib) == "workspace must be 256-byte aligned"
+    assert g(p, BF16, p, p, None, 4, 32, 64, None, p, 32, 1, None, 0, p, BF16, None) == 1
+    assert _err(lib) == "a gate needs a residual"
+    assert g(p, BF16, p, p, None, 4, 32, 64, p, p, 32, 0, None, 0, p, BF16, None) == 1
+    assert _err(lib) == "rows_per_gate must be positive, got 0"
+    assert g(p, BF16, p, p, None, 0, 32, 64, None, None, 0, 1, None, 0, p, BF16, None) == 0  # M = 0: nothing to do
+
+
 def test_gemm_noalloc_validation(lib):
     """convrot_w4a4_gemm_noalloc (arguments of convrot_w4a4_gemm_residual; residual NULL: the
     plain GEMM) rejects bad arguments before it touches its scratch or launches anything."""
