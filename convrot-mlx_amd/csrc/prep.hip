@@ -572,10 +572,17 @@ __global__ __launch_bounds__(1024) void prep_kernel(const void* __restrict__ x, 
       const int64_t mblocks = ((int64_t)gridDim.x + 15) >> 4;
       uint8_t* blk = (uint8_t*)out + ((int64_t)(fh >> 7) * mblocks + (row >> 4)) * 1536;
       const int L = ((fh >> 5) & 3) * 16 + (int)(row & 15);
+      // The two halves of a 32-feature group share slot L: 12 bytes of the
+      // first, then the second's first dword (its other 8 bytes go to the
+      // block's tail).  They sit in lanes kPair apart (bit 4 of fh is lane bit
+      // 2 for groups of 256 and 1024, lane bit 0 otherwise), so the first lane
+      // writes the whole 16-byte slot: two stores a pair instead of three.
+      // Both lanes of a pair are past the row end or neither (K % 128 == 0).
+      constexpr int kPair = (S == 4 || S == 5) ? 4 : 1;
+      const uint32_t d0_second = (uint32_t)__shfl_down((int)d0, kPair);
       if ((fh & 16) == 0) {
-        *(uint3*)(blk + 16 * L) = make_uint3(d0, d1, d2);
+        *(uint4*)(blk + 16 * L) = make_uint4(d0, d1, d2, d0_second);
       } else {
-        *(uint32_t*)(blk + 16 * L + 12) = d0;
         *(uint2*)(blk + 1024 + 8 * L) = make_uint2(d1, d2);
       }
       continue;
