@@ -886,7 +886,9 @@ class ConvRotLinear(nn.Module):
     Backends: "hip-w4a4" (default) / "hip-w4a16" hold qweight in the CDNA4
     tile layout; "mpp-w4a4" / "mpp-w4a16" keep the reference's K x packed-N
     contract for qweight (so reference checkpoints and repacks load
-    unchanged) and run the same kernels on a cached CDNA4 repack.
+    unchanged) and run the same kernels on a cached CDNA4 repack.  A hip-*
+    layer given a K x packed-N qweight by assignment, as reference code does,
+    runs it the same way (a CDNA4 repack cached per tensor version).
     The default comes from $CONVROT_BACKEND, then $CONVROT_MLX_BACKEND.
     """
 
@@ -961,8 +963,11 @@ class ConvRotLinear(nn.Module):
         return self
 
     def _device_weight(self) -> torch.Tensor:
+        """The CDNA4 weight the kernels read.  A hip-* layer holds it as `qweight`; an mpp-*
+        layer, and a hip-* layer given a reference-style K x packed-N `qweight` (the
+        reference's assignment, core.py:1244-1250), repack theirs once per tensor version."""
         q = self.qweight
-        if self.weight_layout == WEIGHT_LAYOUT_CDNA4:
+        if self.weight_layout == WEIGHT_LAYOUT_CDNA4 and q.ndim != 2:
             _check_cdna4(q, self.out_features, self.in_features)
             return q
         key = (q.data_ptr(), q._version, tuple(q.shape), q.device)

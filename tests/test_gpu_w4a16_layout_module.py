@@ -238,6 +238,30 @@ def _layer_reference(orc, x, dense_w, dense_b, G, dtype="bfloat16"):
     return orc.w4a4_matmul_codes(a_codes, w_codes, xscales, wscales, dense_b, dtype)
 
 
+@pytest.mark.parametrize("backend", ["hip-w4a4", "hip-w4a16"])
+def test_default_backend_takes_reference_assignment(orc, dev, backend):
+    """Reference code assigns a K x packed-N qweight (test_core.py:375-402's layer set-up); on the
+    hip-* backends that runs on a cached CDNA4 repack, with the same output bits as load_nk_weight."""
+    api = _api()
+    rng = np.random.default_rng(31)
+    n = 34
+    dense_w = orc.from_f32(rng.normal(size=(n, 256)).astype(np.float32), "bfloat16")
+    dense_b = torch.from_numpy(rng.normal(size=(n,)).astype(np.float32)).to(dev)
+    values = to_dev(orc.from_f32(rng.normal(size=(2, 7, 256)).astype(np.float32), "bfloat16"), "bfloat16", dev)
+    qweight, wscales = api.quantize_convrot_weight(to_dev(dense_w, "bfloat16", dev))
+    ref_layer = api.ConvRotLinear(256, n, backend=backend, device=dev)
+    ref_layer.load_nk_weight(qweight, wscales, dense_b)
+    layer = api.ConvRotLinear(256, n, backend=backend, device=dev)
+    layer.qweight = api.repack_nk_weight_for_mpp(qweight)
+    layer.scales = wscales
+    layer.bias = dense_b
+    assert layer.qweight.ndim == 2 and layer.backend == backend
+    assert torch.equal(layer(values), ref_layer(values))
+    layer.qweight = api.repack_nk_weight_for_mpp(torch.zeros_like(qweight))  # a new tensor: the repack follows
+    out = layer(values)
+    assert torch.equal(out, dense_b.to(torch.bfloat16).expand_as(out))  # zero codes: bias alone
+
+
 @pytest.mark.parametrize("backend", ["hip-w4a4", "mpp-w4a4"])
 def test_layer_matches_contract_bf16(orc, dev, backend):
     """test_core.py:375-402: (2,7,256) -> 33 (34 for the even-N mpp layout), seed 29, bit-exact."""
