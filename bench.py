@@ -132,8 +132,11 @@ class PathRunner:
     full_weights the operand blocks everywhere."""
 
     def __init__(self, nat, dev, M, G, fp6=True, full_weights=False):
+        import torch
+
         self.nat, self.lib, self.stream, self.M, self.G = nat, nat.load(), nat.stream_of(dev), M, G
         self.fp6, self.full = fp6, full_weights
+        self.work = torch.zeros(int(self.lib.convrot_w4a4_workspace_bytes()), dtype=torch.uint8, device=dev)
 
     def prep(self, L):
         nat = self.nat
@@ -151,10 +154,12 @@ class PathRunner:
             nat.check(self.lib.convrot_w4a4_gemm_fp6(nat.ptr(L["a6"]), nat.ptr(L["xs"]), nat.ptr(L["w6"]),
                                                      nat.ptr(L["ws"]), nat.ptr(L["bias"]), self.M, L["N"], L["K"],
                                                      nat.ptr(L["out"]), nat.DTYPE_BF16, self.stream))
-        else:
-            nat.check(self.lib.convrot_w4a4_gemm(nat.ptr(L["qact"]), nat.ACT_INT8, nat.ptr(L["xs"]),
-                                                 nat.ptr(L["wq"]), nat.ptr(L["ws"]), nat.ptr(L["bias"]), self.M,
-                                                 L["N"], L["K"], nat.ptr(L["out"]), nat.DTYPE_BF16, self.stream))
+        else:  # with the stream-K workspace, as ConvRotLinear calls it
+            nat.check(self.lib.convrot_w4a4_gemm_ws(nat.ptr(L["qact"]), nat.ACT_INT8, nat.ptr(L["xs"]),
+                                                    nat.ptr(L["wq"]), nat.ptr(L["ws"]), nat.ptr(L["bias"]), self.M,
+                                                    L["N"], L["K"], None, None, 0, 1, nat.ptr(self.work),
+                                                    self.work.numel(), nat.ptr(L["out"]), nat.DTYPE_BF16,
+                                                    self.stream))
 
     def step(self, layers, events=None):
         for j, L in enumerate(layers):

@@ -461,7 +461,7 @@ int convrot_w4a4_gemm_noalloc(const void* act, int act_format, const float* xsca
   convrot::GatedResidual gr{};
   if (residual)
     if (int rc = check_residual(residual, gate, gate_stride, rows_per_gate, M, N, &gr)) return rc;
-  // The same plan as convrot_w4a4_gemm; its workspace must fit the static scratch.
+  // The plan of convrot_w4a4_gemm_ws with a full workspace; its workspace must fit the static scratch.
   const size_t need = convrot::w4a4_plan_workspace_bytes(act_format, M, N, K);
   if (need > convrot::kNoAllocScratchBytes)
     return fail(CONVROT_ERR_INVALID,

@@ -70,11 +70,10 @@ struct Workspace {
 };
 constexpr size_t kSkWorkspaceBytes = 32768 + (size_t)256 * 256 * 256 * 4;
 
-// Where a W4A4 launch takes its stream-K workspace from: the library's own
-// buffer of the launch stream (made on first need), or a given one (nullptr:
-// data-parallel plans only).
+// The stream-K workspace of a W4A4 launch: none (data-parallel plans only; the
+// library never allocates one), or a given one (its null pointer: the same).
 struct WorkspaceSource {
-  enum Kind { kLibrary, kGiven } kind = kLibrary;
+  enum Kind { kNone, kGiven } kind = kNone;
   Workspace given{};
 };
 
@@ -84,7 +83,7 @@ hipError_t launch_w4a4_gemm(const void* act, int act_format, const float* xscale
                             const GatedResidual& gr = GatedResidual{}, WorkspaceSource src = WorkspaceSource{});
 
 // Synchronizes `stream`, then reads and clears the error word of `workspace`
-// (nullptr: the library's own workspace of the stream, if any).  Returns 0
+// (nullptr: the no-alloc entry point's static scratch on this device, if set up).  Returns 0
 // (no error), 1 (a bounded stream-K wait gave up since the last check; *what
 // describes it) or -1 (a HIP call failed).
 int w4a4_workspace_status(const void* workspace, hipStream_t stream, const char** what);

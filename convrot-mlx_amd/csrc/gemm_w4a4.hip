@@ -2249,43 +2249,6 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool allow_dma, size_t ws_byte
   return best;
 }
 
-// Stream-K workspace held by the library for the entry points without a
-// workspace argument: one per (device, stream), of kSkWorkspaceBytes (enough
-// for every plan), allocated and zero-filled (stream-ordered, no host
-// synchronization) by the first launch on that stream outside graph capture,
-// and kept until the process ends.  A launch under capture on a stream that
-// has none runs a data-parallel plan (same results bit for bit).
-struct SkBuffer {
-  int dev;
-  hipStream_t stream;
-  uint8_t* ptr;
-};
-std::mutex g_sk_mu;
-std::vector<SkBuffer> g_sk_buffers;
-
-Workspace library_workspace(hipStream_t stream, bool create) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return {};
-  std::lock_guard<std::mutex> lock(g_sk_mu);
-  for (const SkBuffer& b : g_sk_buffers)
-    if (b.dev == dev && b.stream == stream) return {b.ptr, kSkWorkspaceBytes};
-  if (!create) return {};
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return {};
-  void* p = nullptr;
-  if (hipMalloc(&p, kSkWorkspaceBytes) != hipSuccess) {
-    (void)hipGetLastError();
-    return {};
-  }
-  if (hipMemsetAsync(p, 0, (size_t)kSkPartialOffset, stream) != hipSuccess) {
-    (void)hipGetLastError();
-    (void)hipFree(p);  // never used by a launch
-    return {};
-  }
-  g_sk_buffers.push_back({dev, stream, (uint8_t*)p});
-  return {(uint8_t*)p, kSkWorkspaceBytes};
-}
-
 // Scratch of convrot_w4a4_gemm_noalloc: a stream-K workspace that is a
 // file-scope device array, so that entry point allocates nothing.  Every GPU
 // the library runs on holds its own copy (at its own device address) until
@@ -2402,12 +2365,11 @@ hipError_t launch_t(const void* act, const float* xs, const uint8_t* wq, const f
                     int64_t M, int64_t N, int64_t K, void* out, const GatedResidual& gr, WorkspaceSource src,
                     hipStream_t stream) {
   const bool dma = !APACK && tuning(kTuneGemmNoDma) != 1;
-  // The plan with the workspace this call can have; the library's own buffer
-  // is made only when the chosen plan needs it.
-  Workspace wsp = src.kind == WorkspaceSource::kLibrary ? library_workspace(stream, false) : src.given;
-  const size_t avail = src.kind == WorkspaceSource::kLibrary && !wsp.ptr ? kSkWorkspaceBytes : wsp.bytes;
-  const Plan plan = choose_plan(M, N, K, dma, dma ? avail : 0);
-  if (plan.sk && !wsp.ptr && src.kind == WorkspaceSource::kLibrary) wsp = library_workspace(stream, true);
+  // The plan with the workspace this call has: none (the entry points without a
+  // workspace argument, which allocate nothing) leaves the data-parallel plans,
+  // whose outputs are the stream-K plans' bit for bit.
+  const Workspace wsp = src.kind == WorkspaceSource::kGiven ? src.given : Workspace{};
+  const Plan plan = choose_plan(M, N, K, dma, dma && wsp.ptr ? wsp.bytes : 0);
   const Tile t = plan.t;
   if (dma) {
 #define CONVROT_DMA(BM_, BN_, WM_, WN_, S_)                                       \
@@ -2531,7 +2493,6 @@ int w4a4_workspace_status(const void* workspace, hipStream_t stream, const char*
   if (hipStreamSynchronize(stream) != hipSuccess) return -1;
   const uint8_t* bufs[2] = {(const uint8_t*)workspace, nullptr};
   if (!workspace) {
-    bufs[0] = library_workspace(stream, false).ptr;
     const int dev = current_device();
     if (dev >= 0) {
       std::lock_guard<std::mutex> lock(g_noalloc_mu);

@@ -16,21 +16,18 @@
  *  - Return value: CONVROT_OK or a nonzero status.  convrot_last_error()
  *    returns a thread-local message for the last failure on the calling
  *    thread (the same text the Python layer raises as ValueError).
- *  - Scratch memory.  The W4A4 GEMM's stream-K plans need a workspace of
- *    convrot_w4a4_workspace_bytes() (a control block plus int32 partial
- *    tiles).  convrot_w4a4_gemm_ws takes it from the caller.  convrot_w4a4_gemm
- *    and convrot_w4a4_gemm_residual use the library's own workspace of the
- *    (device, stream): the first launch on that stream outside graph capture
- *    that needs it allocates it (hipMalloc + a stream-ordered zero fill, no
- *    host synchronization) and it is kept until the process ends; a launch
- *    under capture on a stream without one runs a data-parallel plan (same
- *    results bit for bit).  This is the library's only allocation.
- *    convrot_w4a4_gemm_noalloc instead uses a static device array (one per
- *    GPU, shared by all its calls) and allocates nothing.  Besides these
- *    workspaces and convrot_set_tuning's overrides the library keeps no global
- *    state.  Launches that use one workspace must not overlap in time: keep
- *    them on one stream, and do not replay a captured graph concurrently with
- *    other launches on its capture stream.
+ *  - Scratch memory.  The library never allocates device memory.  The W4A4
+ *    GEMM's stream-K plans (and the W4A16 GEMM's split of K) need a workspace
+ *    of convrot_w4a4_workspace_bytes() (a control block plus partial tiles):
+ *    convrot_w4a4_gemm_ws and convrot_w4a16_gemm_ws take it from the caller;
+ *    convrot_w4a4_gemm and convrot_w4a4_gemm_residual, which have no
+ *    workspace, run the data-parallel plans (the same results bit for bit);
+ *    convrot_w4a4_gemm_noalloc uses a static device array (one per GPU,
+ *    shared by all its calls).  Besides these workspaces and
+ *    convrot_set_tuning's overrides the library keeps no global state.
+ *    Launches that use one workspace must not overlap in time: keep them on
+ *    one stream, and do not replay a captured graph concurrently with other
+ *    launches on its capture stream.
  *  - Otherwise calls are reentrant; concurrent calls on different streams are
  *    safe.
  */
@@ -138,7 +135,9 @@ int convrot_prepare_gelu(const void* head, int64_t head_features, int64_t head_s
  * with the numerics of reference_w4a4_matmul (core.py:1155-1171).
  * qweight: CONVROT_LAYOUT_CDNA4 bytes for an (N, K) weight.  bias may be NULL
  * (treated as zeros, like the reference's zero bias vector, core.py:1258).
- * K % 32 == 0, K <= 65536.
+ * K % 32 == 0, K <= 65536.  Without a workspace argument it runs the
+ * data-parallel plans only; convrot_w4a4_gemm_ws adds the stream-K plans
+ * (few tiles, long K) with the same outputs.
  */
 int convrot_w4a4_gemm(const void* act, int act_format, const float* xscales,
                       const uint8_t* qweight, const float* wscales, const float* bias,
@@ -197,9 +196,9 @@ int convrot_w4a4_gemm_ws(const void* act, int act_format, const float* xscales,
  * Reports whether a stream-K owner's bounded wait gave up (a partial tile
  * that never arrived; that owner wrote NaN over its output tile instead of a
  * silently wrong value) since the last call: synchronizes `stream`, reads and
- * clears the error word of `workspace` (NULL: the library's own workspace of
- * `stream` and the static scratch of convrot_w4a4_gemm_noalloc on the current
- * GPU).  Returns CONVROT_ERR_LAUNCH with a message if so, else CONVROT_OK.
+ * clears the error word of `workspace` (NULL: the static scratch of
+ * convrot_w4a4_gemm_noalloc on the current GPU, if a call set it up).
+ * Returns CONVROT_ERR_LAUNCH with a message if so, else CONVROT_OK.
  * Not callable under graph capture.  No counterpart in the reference (its
  * kernels have no error path, core.py:1106-1120).
  */
@@ -210,8 +209,9 @@ int convrot_w4a4_status(const void* workspace, void* stream);
  * allocation: for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
  * counterpart in the reference (MLX allocates every kernel output itself,
- * core.py:1106-1113).  It runs the same plan as convrot_w4a4_gemm, bit for bit,
- * taking the stream-K workspace from a static device array of
+ * core.py:1106-1113).  It runs the plan convrot_w4a4_gemm_ws runs with a full
+ * workspace (stream-K where that is faster; outputs the same bits as
+ * convrot_w4a4_gemm), taking the stream-K workspace from a static device array of
  * 64 MiB + 32 KiB per GPU (kept until the process ends), which covers every
  * plan on up to 256 CUs; a plan that would need more is rejected with
  * CONVROT_ERR_INVALID.  The first call on a GPU looks up that array's address

@@ -1,5 +1,6 @@
 """GPU: convrot_w4a4_gemm_noalloc (the W4A4 GEMM with its stream-K workspace in a static
-device array, no allocation) against convrot_w4a4_gemm through the C ABI, bit for bit.
+device array, no allocation) against convrot_w4a4_gemm (no workspace: the data-parallel
+plans) through the C ABI, bit for bit.
 
 Two calls in a row on each plan, the second with a smaller input (the array keeps the
 first call's contents; the stream-K control block must be left ready by every launch):
