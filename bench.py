@@ -128,7 +128,7 @@ class PathRunner:
     """Launches of the complete path (prep -> GEMM) of one set of linears on one stream,
     on FP6 or INT8 operands, with optional HIP events around every launch.  FP6 weights are
     the form ConvRotLinear caches for the shape (core.fp6_weight_form: the compact 0.5-byte
-    form where the GEMM runs a 256-row tile, else the 0.75-byte operand blocks), or with
+    form unless a setting asks for the 0.75-byte operand blocks), or with
     full_weights the operand blocks everywhere."""
 
     def __init__(self, nat, dev, M, G, fp6=True, full_weights=False):
@@ -382,9 +382,9 @@ def main() -> int:
             f_ms, f_prep, f_gemm, _, _ = measure_path(torch, np, full, sets, shapes, M, args.steps, 3)
             result["fp6_full_weights"] = {
                 "what": "the same step on the 1536-byte FP6 weight blocks (0.75 byte a weight) for every shape, "
-                        "instead of the compact ones (0.5 byte a weight, expanded in registers) that "
-                        "ConvRotLinear caches where the GEMM runs a 256-row tile (forms used: "
-                        + ", ".join(L["form"] for L in sets[0]) + ")",
+                        "instead of the forms ConvRotLinear caches (forms used: "
+                        + ", ".join(L["form"] for L in sets[0]) + "; compact: 0.5 byte a weight, expanded "
+                        "in registers)",
                 "ms_per_step": round(f_ms, 4), "tops": round(float(ops.sum() / (f_ms * 1e-3) / 1e12), 1),
                 "gemm_per_shape_us": [round(t * 1e3, 2) for t in f_gemm]}
     if not args.no_extras:

@@ -677,9 +677,7 @@ FP6_MAX_OPERAND_BYTES = (1 << 32) - (1 << 20)
 _fp6_operands = os.getenv("CONVROT_FP6_OPERANDS", "1") != "0"
 # Which FP6 weight form ConvRotLinear caches: "compact" (0.5 byte per weight, each
 # fragment expanded in registers inside the GEMM), "full" (the 0.75-byte operand
-# blocks), or "auto": compact where the GEMM's tile for the layer's first FP6
-# product has 256 rows (the expansions hide between its MFMAs: as fast or faster
-# than full), full where it has 128 (compact measured ~10 % slower there).
+# blocks), or "auto" (the library's choice: compact, see fp6_weight_form).
 FP6_WEIGHT_FORMS = ("auto", "compact", "full")
 _fp6_weight_form = os.getenv("CONVROT_FP6_WEIGHTS", "auto")
 
@@ -708,10 +706,14 @@ def set_fp6_weight_form(form: str) -> None:
 
 def fp6_weight_form(rows: int, out_features: int) -> str:
     """The FP6 weight form ("compact" or "full") ConvRotLinear caches for a layer whose first
-    FP6 product has `rows` rows and `out_features` output features, under the current setting."""
-    if _fp6_weight_form != "auto":
-        return _fp6_weight_form
-    return "compact" if nat.fp6_tile(rows, out_features)[0] == 256 else "full"
+    FP6 product has `rows` rows and `out_features` output features, under the current setting.
+
+    "auto" is the compact form on every tile.  Timed with the weights streamed from HBM, as a
+    model's step reads them, it wins on the 128-row tiles too (config 2: 1818 -> 1927 TOPS;
+    the FLUX.1-dev DiT step: 32.25 -> 31.64 ms, bit-identical), although an isolated GEMM
+    with its weights warm in the Infinity Cache runs the 128-row compact tiles ~10 % slower."""
+    del rows, out_features  # one form for every shape (the arguments keep the per-layer query)
+    return "compact" if _fp6_weight_form == "auto" else _fp6_weight_form
 
 
 def fp6_bytes(rows: int, features: int) -> int:

@@ -440,6 +440,29 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
     allf = allf.float()
     convrot_weights = linear_weight_bytes(model)
     convrot_memory = step_peak_memory(model, inputs)
+    # The same fused model with the compact FP6 weight form on every FP6 layer (the automatic
+    # form keeps the 0.75-byte operand blocks where the GEMM runs 128-row tiles), then on INT8
+    # operands only (no FP6 weight form cached): the same output bits, less weight memory.
+    from convrot_mlx_amd import ConvRotLinear, set_fp6_operands, set_fp6_weight_form
+
+    set_fp6_weight_form("compact")
+    try:
+        compact, compact_ms, compact_graph_ms = time_step(model, inputs, steps)
+        compact_weights = linear_weight_bytes(model)
+        compact_memory = step_peak_memory(model, inputs)
+    finally:
+        set_fp6_weight_form("auto")
+    set_fp6_operands(False)
+    try:
+        for m in model.modules():
+            if isinstance(m, ConvRotLinear):
+                m._fp6_cache = None
+        torch.cuda.empty_cache()
+        int8, int8_ms, int8_graph_ms = time_step(model, inputs, steps)
+        int8_weights = linear_weight_bytes(model)
+        int8_memory = step_peak_memory(model, inputs)
+    finally:
+        set_fp6_operands(True)
 
     def dev_stats(out):
         diff = out - dense
@@ -494,6 +517,20 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
                                                       dense_memory["step_peak_GiB"]), 1),
             "reference": "M4 Pro, MLX allocator peak over a whole 20-step generation: 24.603 GiB dense vs "
                          "9.296 GiB ConvRot, 62.2 % less (docs/benchmarks/m4-pro.md:23-31)",
+            "compact_fp6_everywhere": {
+                "what": "the fused model with set_fp6_weight_form('compact'): every FP6 layer caches the "
+                        "0.5-byte compact form",
+                "linears": compact_weights, "step": compact_memory, "graph_ms": round(compact_graph_ms, 2),
+                "graph_speedup_vs_dense": round(dense_graph_ms / compact_graph_ms, 3),
+                "identical_output": bool(torch.equal(compact.float(), allf)),
+            },
+            "int8_operands_only": {
+                "what": "the fused model with set_fp6_operands(False): every product on the INT8 kernels, "
+                        "no FP6 weight form cached (int4 qweight only)",
+                "linears": int8_weights, "step": int8_memory, "graph_ms": round(int8_graph_ms, 2),
+                "graph_speedup_vs_dense": round(dense_graph_ms / int8_graph_ms, 3),
+                "identical_output": bool(torch.equal(int8.float(), allf)),
+            },
         },
     }
 

@@ -458,14 +458,14 @@ def test_layer_caches_compact_weights_except_minus8(orc, dev, fp6_form):
 
 
 def test_fp6_weight_form_policy(orc, dev, fp6_form):
-    """The automatic FP6 weight form: compact where the GEMM's tile has 256 rows (config 3's
-    4608-row products), the 1536-byte operand blocks where it has 128 (512 rows); a forced
-    form applies everywhere, a bad name raises, and a layer rebuilds its cache when the
-    setting changes -- every form giving the same output bits."""
+    """The automatic FP6 weight form is the compact one on every tile (256-row tiles at config 3's
+    4608 rows, 128-row tiles at 512 rows); a forced form applies everywhere, a bad name raises,
+    and a layer rebuilds its cache when the setting changes -- every form giving the same
+    output bits."""
     from convrot_mlx_amd import ConvRotLinear, core, quantize_convrot_weight
 
     assert core.fp6_weight_form(4608, 3072) == "compact" and core.fp6_weight_form(4608, 21504) == "compact"
-    assert core.fp6_weight_form(512, 3072) == "full"
+    assert core.fp6_weight_form(512, 3072) == "compact"
     with pytest.raises(ValueError, match="weight form"):
         core.set_fp6_weight_form("tiny")
     M, K, N, G = 512, 1024, 768, 64
@@ -474,7 +474,7 @@ def test_fp6_weight_form_policy(orc, dev, fp6_form):
     layer = ConvRotLinear(K, N, group_size=G, device=dev).load_nk_weight(qw, ws)
     x = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
     outs = {}
-    for form, block in (("auto", 1536), ("compact", 1024), ("full", 1536)):
+    for form, block in (("auto", 1024), ("compact", 1024), ("full", 1536)):
         fp6_form(form)
         outs[form] = layer(x)
         torch.cuda.synchronize()
