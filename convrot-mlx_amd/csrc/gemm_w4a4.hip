@@ -1454,8 +1454,8 @@ __device__ __forceinline__ i32x6 fp6c_expand(const i32x4& i, uint32_t z0, uint32
   return d;
 }
 
-// The 4-wave FP6 tile: BM x BN, waves 2 x 2, FN x FM 16 x 16 accumulator
-// blocks per wave in the AGPRs; a 3-stage LDS ring of k-blocks (the tile's
+// The FP6 tile: BM x BN, waves 2 x WN, FN x FM 16 x 16 accumulator blocks per
+// wave in the AGPRs; a 3-stage LDS ring of k-blocks (the tile's
 // activation blocks, then its weight blocks).  Per k-block, one k-step of FN x
 // FM MFMAs in two halves: half 0 (fragment rows 0 .. FM/2-1) reads the
 // block's other activation fragments; a barrier publishes block i+1 and frees
@@ -1468,12 +1468,18 @@ __device__ __forceinline__ i32x6 fp6c_expand(const i32x4& i, uint32_t z0, uint32
 // fragment fn >= 1 during half 0 of block i+1, which runs its MFMAs fragment
 // by fragment (fn-major), so each expansion overlaps the MFMAs of fragment
 // fn - 1.
-template <int BM, int BN, bool CW = false>
+//
+// WN = 2: four waves, one a SIMD (up to 128 x 112 wave tiles).  WN = 4 (the
+// 256 x 256 tile): eight waves, two a SIMD, each with a 128 x 64 wave tile in
+// 128 AGPRs and at most 128 VGPRs; while one wave of a SIMD waits at the
+// block barrier or on its fragment reads, the other's MFMAs run, and the
+// activation blocks in LDS serve four wave columns instead of two.
+template <int BM, int BN, bool CW = false, int WN = 2>
 struct Fp6Engine {
   // A fourth ring stage on the 128-row compact tiles that run one workgroup per
   // CU: their block i+1 is published at block i's start, half a block earlier.
-  static constexpr int NW = 4, STAGES = (CW && BM == 128 && BN > 128) ? 4 : 3;
-  static constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 16, FN = TN / 16, HM = FM / 2;
+  static constexpr int NW = 2 * WN, STAGES = (CW && BM == 128 && BN > 128) ? 4 : 3;
+  static constexpr int TM = BM / 2, TN = BN / WN, FM = TM / 16, FN = TN / 16, HM = FM / 2;
   static constexpr int WBLK = CW ? 1024 : 1536;  // bytes of one 16 x 128 weight block
   static constexpr int A_BYTES = (BM / 16) * 1536, B_BYTES = (BN / 16) * WBLK, STAGE_BYTES = A_BYTES + B_BYTES;
   // 1 KB DMA pieces per k-block; a wave issues APW + BPW of them (a count that
@@ -1503,8 +1509,8 @@ struct Fp6Engine {
     smem_addr = (uint32_t)(uintptr_t)s;
     lane = threadIdx.x & 63;
     wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    wm = wave / 2;
-    wn = wave % 2;
+    wm = wave / WN;
+    wn = wave % WN;
   }
 
   __device__ __forceinline__ void issue_epi(const float* xscales, const float* wscales, const float* bias, int M,
@@ -1757,14 +1763,16 @@ struct Fp6Engine {
   }
 };
 
-// The 4-wave FP6 GEMM, one BM x BN tile per workgroup, with the epilogue of
-// every W4A4 kernel (16-bit or float32 outputs, optional gated residual).
-template <int BM, int BN, int ODT, bool CW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, BM * BN <= 128 * 128 ? 2 : 1))) void w4a4_gemm_fp6_kernel(
+// The FP6 GEMM, one BM x BN tile per workgroup of 2 WN waves, with the
+// epilogue of every W4A4 kernel (16-bit or float32 outputs, optional gated
+// residual).  Two waves a SIMD for the 128 x 128 tile (two workgroups a CU)
+// and the 8-wave 256 x 256 tile.
+template <int BM, int BN, int ODT, bool CW, int WN>
+__global__ __launch_bounds__(WN * 128) __attribute__((amdgpu_waves_per_eu(WN == 4 ? 2 : 1, BM * BN <= 128 * 128 || WN == 4 ? 2 : 1))) void w4a4_gemm_fp6_kernel(
     const uint8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
     const float* __restrict__ wscales, const float* __restrict__ bias, void* __restrict__ out, int M, int N,
     int K, int nblocks, int tiles_m, int tiles_n, GatedResidual gr) {
-  using E = Fp6Engine<BM, BN, CW>;
+  using E = Fp6Engine<BM, BN, CW, WN>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[E::SMEM_BYTES];
   E e(smem);
   const int tiles = tiles_m * tiles_n;
@@ -2517,11 +2525,12 @@ int w4a4_workspace_status(const void* workspace, hipStream_t stream, const char*
 // with the same epilogues as the INT8 kernels.
 namespace {
 
-// FP6 tiles and the time per tile each takes relative to 256 x 256 (per tile,
-// at the same K).  The plan takes the tile with the least modelled time,
-// rounds of whole tiles over the CUs times the tile's relative time: at 4608
-// tokens, 256 x 224 turns 216 tiles (N = 3072) into 252 and 864 (N = 12288)
-// into 990, both a near-whole number of rounds; 128 x 256 fills the CUs at
+// FP6 tiles and the time per tile each takes relative to a 4-wave 256 x 256
+// tile (per tile, at the same K).  The plan takes the tile with the least
+// modelled time, rounds of whole tiles over the CUs times the tile's relative
+// time.  The 8-wave 256 x 256 tile runs 0.83-0.90 of that time (0.86 in the
+// plan), which puts it before 256 x 224 (0.9) wherever both need the same
+// rounds: every config-3 shape at 4608 tokens; 128 x 256 fills the CUs at
 // a few thousand tokens; 128 x 128 (two workgroups per CU) at 256-1024 tokens
 // with N = 3072: 12288 -> 3072 at 512 tokens takes 28.5 us against 42.0 on
 // 128 x 256 (its relative time 0.43 measured at 256-1024 tokens); 128 x 192
@@ -2531,7 +2540,7 @@ struct Fp6Tile {
   int bm, bn;
   double rel;
 };
-constexpr Fp6Tile kFp6Tiles[5] = {{256, 256, 1.0}, {256, 224, 0.9}, {128, 256, 0.62}, {128, 128, 0.43}, {128, 192, 0.56}};
+constexpr Fp6Tile kFp6Tiles[5] = {{256, 256, 0.86}, {256, 224, 0.9}, {128, 256, 0.62}, {128, 128, 0.43}, {128, 192, 0.56}};
 
 Fp6Tile fp6_tile(int64_t M, int64_t N) {
   const int forced = tuning(kTuneFp6Tile);
@@ -2558,7 +2567,8 @@ hipError_t launch_fp6_tile(const uint8_t* act6, const float* xscales, const uint
                            hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16);
   const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
-  hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<BM, BN, ODT, CW>), dim3((unsigned)(tm * tn)), dim3(256), 0, stream, act6,
+  constexpr int WN = (BM == 256 && BN == 256) ? 4 : 2;  // 8 waves on the 256 x 256 tile
+  hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<BM, BN, ODT, CW, WN>), dim3((unsigned)(tm * tn)), dim3(WN * 128), 0, stream, act6,
                      xscales, w6, wscales, bias, out, (int)M, (int)N, (int)K, nblocks, tm, tn, gr);
   return hipGetLastError();
 }
