@@ -393,9 +393,16 @@ def linear_weight_bytes(model: nn.Module) -> dict:
             "bytes_per_weight": round((stored + derived) / max(1, weights), 4)}
 
 
-def step_peak_memory(model: nn.Module, inputs: dict) -> dict:
+def allocated_baseline() -> int:
+    """Bytes torch's allocator holds on the device now (what the process held before a model)."""
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return torch.cuda.memory_allocated()
+
+
+def step_peak_memory(model: nn.Module, inputs: dict, base: int = 0) -> dict:
     """Device memory around one eager step (torch's allocator): resident before it and the peak
-    during it, in GiB."""
+    during it, in GiB, net of `base` bytes held by the process before the model was built."""
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     torch.cuda.reset_peak_memory_stats()
@@ -404,7 +411,8 @@ def step_peak_memory(model: nn.Module, inputs: dict) -> dict:
         model(**inputs)
     torch.cuda.synchronize()
     gib = float(1 << 30)
-    return {"resident_GiB": round(resident / gib, 3), "step_peak_GiB": round(torch.cuda.max_memory_allocated() / gib, 3)}
+    return {"resident_GiB": round((resident - base) / gib, 3),
+            "step_peak_GiB": round((torch.cuda.max_memory_allocated() - base) / gib, 3)}
 
 
 def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_tokens: int = 512,
@@ -414,10 +422,11 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
 
     p = p or FluxParams()
     dev = torch.device("cuda:0")
+    base = allocated_baseline()
     model = build(p, dev)
     inputs = make_inputs(p, img_tokens, txt_tokens, dev)
     dense_weights = linear_weight_bytes(model)
-    dense_memory = step_peak_memory(model, inputs)
+    dense_memory = step_peak_memory(model, inputs, base)
     dense, dense_ms, dense_graph_ms = time_step(model, inputs, steps)
     dense = dense.float()
     linears = sum(1 for m in model.modules() if isinstance(m, nn.Linear))
@@ -439,17 +448,17 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
     allf, all_ms, all_graph_ms = time_step(model, inputs, steps)
     allf = allf.float()
     convrot_weights = linear_weight_bytes(model)
-    convrot_memory = step_peak_memory(model, inputs)
-    # The same fused model with the compact FP6 weight form on every FP6 layer (the automatic
-    # form keeps the 0.75-byte operand blocks where the GEMM runs 128-row tiles), then on INT8
-    # operands only (no FP6 weight form cached): the same output bits, less weight memory.
+    convrot_memory = step_peak_memory(model, inputs, base)
+    # The same fused model with the 0.75-byte FP6 operand blocks cached instead of the compact
+    # 0.5-byte form (the automatic choice), then on INT8 operands only (no FP6 weight form
+    # cached): the same output bits, other weight memory.
     from convrot_mlx_amd import ConvRotLinear, set_fp6_operands, set_fp6_weight_form
 
-    set_fp6_weight_form("compact")
+    set_fp6_weight_form("full")
     try:
-        compact, compact_ms, compact_graph_ms = time_step(model, inputs, steps)
-        compact_weights = linear_weight_bytes(model)
-        compact_memory = step_peak_memory(model, inputs)
+        full, full_ms, full_graph_ms = time_step(model, inputs, steps)
+        full_weights = linear_weight_bytes(model)
+        full_memory = step_peak_memory(model, inputs, base)
     finally:
         set_fp6_weight_form("auto")
     set_fp6_operands(False)
@@ -460,7 +469,7 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
         torch.cuda.empty_cache()
         int8, int8_ms, int8_graph_ms = time_step(model, inputs, steps)
         int8_weights = linear_weight_bytes(model)
-        int8_memory = step_peak_memory(model, inputs)
+        int8_memory = step_peak_memory(model, inputs, base)
     finally:
         set_fp6_operands(True)
 
@@ -510,19 +519,20 @@ def config5_figure(p: FluxParams | None = None, img_tokens: int = 1024, txt_toke
             "what": "torch allocator bytes on the device: the Linears' weights (dense bf16 weight + bias, or "
                     "ConvRotLinear qweight + scales + bias as stored, plus the derived FP6 operand weights "
                     "cached for products of 256+ rows), and the resident / peak bytes of one eager step of "
-                    "the whole model (dense, and W4A4 with every fusion on)",
+                    "the whole model (dense, and W4A4 with every fusion on), net of what the process held "
+                    "before the model was built",
             "dense_linears": dense_weights, "w4a4_linears": convrot_weights,
             "dense_step": dense_memory, "w4a4_step": convrot_memory,
             "step_peak_reduction_pct": round(100.0 * (1.0 - convrot_memory["step_peak_GiB"] /
                                                       dense_memory["step_peak_GiB"]), 1),
             "reference": "M4 Pro, MLX allocator peak over a whole 20-step generation: 24.603 GiB dense vs "
                          "9.296 GiB ConvRot, 62.2 % less (docs/benchmarks/m4-pro.md:23-31)",
-            "compact_fp6_everywhere": {
-                "what": "the fused model with set_fp6_weight_form('compact'): every FP6 layer caches the "
-                        "0.5-byte compact form",
-                "linears": compact_weights, "step": compact_memory, "graph_ms": round(compact_graph_ms, 2),
-                "graph_speedup_vs_dense": round(dense_graph_ms / compact_graph_ms, 3),
-                "identical_output": bool(torch.equal(compact.float(), allf)),
+            "full_fp6_weights": {
+                "what": "the fused model with set_fp6_weight_form('full'): every FP6 layer caches the "
+                        "0.75-byte FP6 operand blocks instead of the 0.5-byte compact form",
+                "linears": full_weights, "step": full_memory, "graph_ms": round(full_graph_ms, 2),
+                "graph_speedup_vs_dense": round(dense_graph_ms / full_graph_ms, 3),
+                "identical_output": bool(torch.equal(full.float(), allf)),
             },
             "int8_operands_only": {
                 "what": "the fused model with set_fp6_operands(False): every product on the INT8 kernels, "
