@@ -1470,10 +1470,11 @@ __device__ __forceinline__ i32x6 fp6c_expand(const i32x4& i, uint32_t z0, uint32
 // fn - 1.
 //
 // WN = 2: four waves, one a SIMD (up to 128 x 112 wave tiles).  WN = 4 (the
-// 256 x 256 tile): eight waves, two a SIMD, each with a 128 x 64 wave tile in
-// 128 AGPRs and at most 128 VGPRs; while one wave of a SIMD waits at the
-// block barrier or on its fragment reads, the other's MFMAs run, and the
-// activation blocks in LDS serve four wave columns instead of two.
+// 256 x 256, 128 x 256 and 128 x 192 tiles): eight waves, two a SIMD, with
+// 128 x 64, 64 x 64 and 64 x 48 wave tiles (at most 128 AGPRs and 128 VGPRs);
+// while one wave of a SIMD waits at the block barrier or on its fragment
+// reads, the other's MFMAs run, and the activation blocks in LDS serve four
+// wave columns instead of two.
 template <int BM, int BN, bool CW = false, int WN = 2>
 struct Fp6Engine {
   // A fourth ring stage on the 128-row compact tiles that run one workgroup per
@@ -1766,7 +1767,7 @@ struct Fp6Engine {
 // The FP6 GEMM, one BM x BN tile per workgroup of 2 WN waves, with the
 // epilogue of every W4A4 kernel (16-bit or float32 outputs, optional gated
 // residual).  Two waves a SIMD for the 128 x 128 tile (two workgroups a CU)
-// and the 8-wave 256 x 256 tile.
+// and the 8-wave tiles.
 template <int BM, int BN, int ODT, bool CW, int WN>
 __global__ __launch_bounds__(WN * 128) __attribute__((amdgpu_waves_per_eu(WN == 4 ? 2 : 1, BM * BN <= 128 * 128 || WN == 4 ? 2 : 1))) void w4a4_gemm_fp6_kernel(
     const uint8_t* __restrict__ act, const float* __restrict__ xscales, const uint8_t* __restrict__ wq,
@@ -2535,12 +2536,13 @@ namespace {
 // with N = 3072: 12288 -> 3072 at 512 tokens takes 28.5 us against 42.0 on
 // 128 x 256 (its relative time 0.43 measured at 256-1024 tokens); 128 x 192
 // (192 tiles: one round) at 1536 tokens, 12288 -> 3072 in 37.0 us against 45.1
-// (relative time 0.56 at 1536-2048 tokens).
+// (relative time 0.56 at 1536-2048 tokens).  With eight waves 128 x 256 and
+// 128 x 192 run 5-10 % and 2-4 % faster than with four (0.58 and 0.54).
 struct Fp6Tile {
   int bm, bn;
   double rel;
 };
-constexpr Fp6Tile kFp6Tiles[5] = {{256, 256, 0.86}, {256, 224, 0.9}, {128, 256, 0.62}, {128, 128, 0.43}, {128, 192, 0.56}};
+constexpr Fp6Tile kFp6Tiles[5] = {{256, 256, 0.86}, {256, 224, 0.9}, {128, 256, 0.58}, {128, 128, 0.43}, {128, 192, 0.54}};
 
 Fp6Tile fp6_tile(int64_t M, int64_t N) {
   const int forced = tuning(kTuneFp6Tile);
@@ -2567,7 +2569,8 @@ hipError_t launch_fp6_tile(const uint8_t* act6, const float* xscales, const uint
                            hipStream_t stream) {
   const int nblocks = (int)((N + 15) / 16);
   const int tm = (int)((M + BM - 1) / BM), tn = (int)((N + BN - 1) / BN);
-  constexpr int WN = (BM == 256 && BN == 256) ? 4 : 2;  // 8 waves on the 256 x 256 tile
+  // 8 waves on 256 x 256, 128 x 256 and 128 x 192; 4 on 256 x 224 and 128 x 128
+  constexpr int WN = ((BM == 256 && BN == 256) || (BM == 128 && BN >= 192)) ? 4 : 2;
   hipLaunchKernelGGL((w4a4_gemm_fp6_kernel<BM, BN, ODT, CW, WN>), dim3((unsigned)(tm * tn)), dim3(WN * 128), 0, stream, act6,
                      xscales, w6, wscales, bias, out, (int)M, (int)N, (int)K, nblocks, tm, tn, gr);
   return hipGetLastError();
