@@ -140,7 +140,7 @@ def set_tuning(name: str, value: str | None) -> None:
     """Force one of the library's kernel / plan choices (tuning sweeps and tests); None or ""
     restores the automatic choice.  Names: gemm_tile ("BMxBN[wWMxWN[sS]]"), gemm_sk (0/1),
     gemm_sk_min, gemm_no_dma, gemm_smallm_max, w4a4_smallm_cfg (A/B/C/F), w4a16_cfg
-    (A/B/C/D/E/F/T), w4a16_tile ("BMxBN"), prep_ni (1/3/4), sk_spin_limit, gemm_persist (0: never;
+    (A/B/C/D/E/F, S: split K, T), w4a16_tile ("BMxBN"), prep_ni (1/3/4), sk_spin_limit, gemm_persist (0: never;
     G: always, on G workgroups), gemm_mfma32 (0/1), fp6_tile ("BMxBN": 256x256, 256x224, 128x256, 128x192, 128x128)."""
     check(load().convrot_set_tuning(name.encode(), None if value is None else str(value).encode()))
 
