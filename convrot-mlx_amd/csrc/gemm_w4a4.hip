@@ -2554,7 +2554,13 @@ Fp6Tile fp6_tile(int64_t M, int64_t N) {
   double best_cost = -1.0;
   for (const Fp6Tile& t : kFp6Tiles) {
     const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
-    const double cost = (double)((tiles + cus - 1) / cus) * t.rel;
+    double cost = (double)((tiles + cus - 1) / cus) * t.rel;
+    // Two 128 x 128 workgroups share a CU and the dispatcher refills CUs as
+    // workgroups finish, so a grid of many such tiles runs in time nearly
+    // linear in the tile count (0.33 per CU-load of tiles from two full
+    // rounds of two a CU on: 1536 x 3072 -> 12288, 1152 tiles, 40.8 us
+    // against 44.5 on 128 x 192); fewer tiles keep the rounded model.
+    if (t.bm == 128 && t.bn == 128 && tiles >= 4 * cus) cost = (double)tiles / (double)cus * 0.33;
     if (best_cost < 0 || cost < best_cost - 1e-9) {
       best = t;
       best_cost = cost;
