@@ -307,3 +307,18 @@ def test_tuning_accepts_built_tiles(lib, name, value):
             assert f"{bm.value}x{bn.value}" == value
     finally:
         assert lib.convrot_set_tuning(name.encode(), None) == 0
+
+
+# The automatic FP6 tile on a 256-CU device (the query falls back to 256 CUs without a GPU):
+# the 8-wave 256x256 tile at every config-3 shape, 128x192 at config 2's N = 3072 and
+# 3072 -> 12288 taken by 128x128 once four or more of its tiles fall to each CU.
+@pytest.mark.parametrize("M,N,tile", [(4608, 9216, "256x256"), (4608, 3072, "256x256"), (4608, 12288, "256x256"),
+                                      (4608, 21504, "256x256"), (1536, 3072, "128x192"), (1536, 9216, "256x256"),
+                                      (1536, 12288, "128x128"), (512, 3072, "128x128"), (512, 9216, "128x192"),
+                                      (1024, 12288, "256x256")])
+def test_fp6_plan(lib, M, N, tile):
+    import ctypes
+
+    bm, bn = ctypes.c_int(0), ctypes.c_int(0)
+    assert lib.convrot_w4a4_fp6_tile(M, N, ctypes.byref(bm), ctypes.byref(bn)) == 0
+    assert f"{bm.value}x{bn.value}" == tile
